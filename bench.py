@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Headline benchmark: BCSR SpMM on one MI355X.
+
+Workload (default `templates`, BASELINE configs[2], the configuration the
+north-star target is quoted on): A = 16384 x 16384 fp16, 0.5 % dense, rows
+from 1024 column-pattern templates, shuffled; B = 16384 x 128 fp16; C fp32.
+The Tier-2 preparation runs once, untimed by the step loop and reported
+separately: host Jaccard clustering (threshold 0.5, width 16) -> GPU row
+permutation -> GPU CSR->BCSR.  A step is one Tier-1 SpMM call
+C = A_bcsr * B on device-resident inputs (the B-panel repack and the MFMA
+tile kernel).  `value` is the effective throughput 2*nnz*N / t.
+
+The JSON line also carries:
+  roofline      algorithmic HBM bytes per call / measured call time vs 8 TB/s;
+                `traffic` is the measured HBM bytes per call from rocprofv3
+                FETCH_SIZE + WRITE_SIZE (profiles/spmm_traffic.json) when
+                that profile exists, else null;
+  cpu_baseline  the same BCSR SpMM on the host cores (C oracle, fp32
+                accumulation), repeated over the full matrix for ~10 s.
+Usage: python bench.py [--steps K] [--warmup W] [--config NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "effective TFLOPS (2·nnz·N/t) + % HBM roofline, BCSR SpMM on 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+WORKLOADS = {
+    "templates": "configs[2]: 16384^2 fp16, 0.5%, 1024 templates x 82 cols, shuffled, "
+                 "clustering on, N=128",
+    "blocks": "configs[1]: 8192^2 fp16, 5% dense 16x16 blocks, N=256, Tier-1",
+    "cpu_ref": "configs[0]: 1024^2 fp32, 1% uniform, N=64",
+    "pruned": "configs[4]: 14336x4096 fp16, 90% pruned, N=2048, clustering off",
+    "gnn": "configs[3]: 131072^2 power-law adjacency fp16, N=64, clustering on",
+}
+
+
+def host_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_baseline(p, N, nnz, seconds):
+    """C oracle BCSR SpMM (fp32 accumulation) on all host threads, repeated
+    over the whole matrix until `seconds` have elapsed; median per call."""
+    import oracle
+
+    brp, bci, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    threads = host_threads()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        oracle.bcsr_spmm_f32(p.M, p.K, N, brp, bci, bv, p.B, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    t = statistics.median(times)
+    return {
+        "value": 2.0 * nnz * N / t / 1e12,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"whole matrix ({len(bci)} blocks), {len(times)} runs, median "
+                  f"{t * 1e3:.1f} ms/call; BCSR tile product with fp32 accumulation "
+                  f"(oracle/oracle.c xo_bcsr_spmm_f32)",
+    }
+
+
+def load_traffic(config):
+    path = os.path.join(ROOT, "profiles", "spmm_traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return d.get(config)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="templates", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-pipeline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import xspmm_amd as X
+    from xspmm_amd import synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    X.load()
+
+    print(f"[bench] generating {args.config}", file=sys.stderr, flush=True)
+    p = synth.CONFIGS[args.config]()
+    M, K, N, nnz = p.M, p.K, p.N, p.nnz
+    A = X.CSRMatrix.from_host(M, K, p.rp, p.ci, p.vals)
+    B = torch.as_tensor(p.B).cuda()
+
+    # --- Tier-2 preparation (once) -----------------------------------------
+    prep = {}
+    t0 = time.perf_counter()
+    if p.cluster:
+        perm = X.compute_1d_jaccard_clustering(M, K, p.rp, p.ci, 0.5, 16)
+    else:
+        perm = np.arange(M, dtype=p.rp.dtype)
+    prep["clustering_host_ms"] = (time.perf_counter() - t0) * 1e3
+    perm_d = torch.as_tensor(perm).cuda()
+    torch.cuda.synchronize()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record()
+    Ap = X.apply_permutation(A, perm_d) if p.cluster else A
+    e1.record()
+    Bm = X.csr_to_bcsr(Ap)
+    e2.record()
+    torch.cuda.synchronize()
+    prep["permutation_ms"] = e0.elapsed_time(e1)
+    prep["conversion_ms"] = e1.elapsed_time(e2)
+    nnzb, Mb = Bm.num_blocks, Bm.num_block_rows
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+
+    # --- timed Tier-1 steps ------------------------------------------------
+    print(f"[bench] nnz={nnz} nnzb={nnzb}; warmup {args.warmup}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        X.spmm(Bm, B, C, N)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        X.spmm(Bm, B, C, N)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = start.elapsed_time(stop) / args.steps
+    t = ms * 1e-3
+    print(f"[bench] {args.steps} steps, {ms:.4f} ms/step", file=sys.stderr, flush=True)
+
+    # spot check of C on sampled rows against an fp64 numpy product
+    rows = np.random.default_rng(0).choice(M, size=min(256, M), replace=False)
+    Ch = C.cpu().numpy()[rows].astype(np.float64)
+    Bf = p.B.astype(np.float64)
+    vf = p.vals.astype(np.float64)
+    ref = np.stack([vf[p.rp[r]:p.rp[r + 1]] @ Bf[p.ci[p.rp[r]:p.rp[r + 1]]] for r in rows])
+    spot = float(np.linalg.norm(Ch - ref) / max(np.linalg.norm(ref), 1e-300))
+
+    sT = p.vals.dtype.itemsize
+    sI = p.rp.dtype.itemsize
+    alg_bytes = nnzb * 256 * sT + nnzb * sI + (Mb + 1) * sI + K * N * sT + M * N * 4
+    achieved = alg_bytes / t / 1e9
+    eff = 2.0 * nnz * N / t / 1e12
+    padded = 2.0 * nnzb * 256 * N / t / 1e12
+    mfma_peak = FP16_PEAK_TFLOPS if sT == 2 else FP32_MFMA_PEAK_TFLOPS
+
+    stages = None
+    if not args.no_pipeline:
+        _, stages = X.spmm_pipeline(A, B, optimize_pattern=p.cluster)
+        torch.cuda.synchronize()
+
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(p, N, nnz, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": eff,
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if sT == 2 else "f32",
+        "data": "synthetic (seeded generator xspmm_amd/synth.py)",
+        "config": {
+            "workload": f"{args.config} ({WORKLOADS[args.config]})",
+            "M": M, "K": K, "N": N, "nnz": nnz, "nnzb": nnzb,
+            "index": "int32", "accumulate": "fp32",
+            "clustering": bool(p.cluster),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": load_traffic(args.config),
+            "kernel": "Tier-1 call: pack_b_panels + spmm_f16_kernel",
+            "alg_bytes_per_call": alg_bytes,
+        },
+        "padded_tflops": padded,
+        "mfma_frac": padded / mfma_peak,
+        "wall_s_timed_region": wall,
+        "spot_check_rel_frob": spot,
+        "prep": prep,
+        "pipeline_stages_ms": stages,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

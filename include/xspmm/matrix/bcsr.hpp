@@ -1,0 +1,149 @@
+#pragma once
+// Device-resident BCSR matrix: bcsr_row_ptr[Mb+1], bcsr_col_ind[nnzb] (block
+// columns, ascending within a block-row) and bcsr_values[nnzb*r*c] (each block
+// row-major).  Interface as in the reference (include/xspmm/matrix/bcsr.hpp:12-116).
+//
+// Added to the reference interface: the element shape (get_num_rows /
+// get_num_cols).  csr_to_bcsr records the CSR's M and K, so SpMM masks the
+// rows and columns of ragged edge blocks instead of touching memory outside
+// B and C.  A matrix built directly from the constructor reports the padded
+// shape Mb*r x Kb*c, which is what the reference's kernel assumes.
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <utility>
+
+#include "xspmm/core/executor.hpp"
+
+namespace xspmm {
+
+template <typename ValueType, typename IndexType = int64_t>
+class BCSRMatrix {
+public:
+    BCSRMatrix(std::shared_ptr<const Executor> exec, IndexType num_block_rows,
+               IndexType num_block_cols, IndexType num_blocks, IndexType r_block, IndexType c_block)
+        : exec_(std::move(exec)),
+          num_block_rows_(num_block_rows), num_block_cols_(num_block_cols), num_blocks_(num_blocks),
+          r_block_(r_block), c_block_(c_block),
+          num_rows_(num_block_rows * r_block), num_cols_(num_block_cols * c_block)
+    {
+        if (num_block_rows < 0 || num_block_cols < 0 || num_blocks < 0) {
+            throw std::invalid_argument("BCSR dimensions must be non-negative.");
+        }
+        exec_->allocate(reinterpret_cast<void**>(&bcsr_row_ptr_),
+                        (static_cast<size_t>(num_block_rows) + 1) * sizeof(IndexType));
+        if (num_blocks > 0) {
+            exec_->allocate(reinterpret_cast<void**>(&bcsr_col_ind_),
+                            static_cast<size_t>(num_blocks) * sizeof(IndexType));
+            exec_->allocate(reinterpret_cast<void**>(&bcsr_values_), value_bytes());
+        }
+    }
+
+    ~BCSRMatrix() { release(); }
+
+    BCSRMatrix(const BCSRMatrix&) = delete;
+    BCSRMatrix& operator=(const BCSRMatrix&) = delete;
+
+    BCSRMatrix(BCSRMatrix&& o) noexcept
+        : exec_(std::move(o.exec_)),
+          num_block_rows_(o.num_block_rows_), num_block_cols_(o.num_block_cols_), num_blocks_(o.num_blocks_),
+          r_block_(o.r_block_), c_block_(o.c_block_), num_rows_(o.num_rows_), num_cols_(o.num_cols_),
+          bcsr_row_ptr_(o.bcsr_row_ptr_), bcsr_col_ind_(o.bcsr_col_ind_), bcsr_values_(o.bcsr_values_)
+    {
+        o.bcsr_row_ptr_ = nullptr;
+        o.bcsr_col_ind_ = nullptr;
+        o.bcsr_values_ = nullptr;
+    }
+
+    BCSRMatrix& operator=(BCSRMatrix&& o) noexcept {
+        if (this != &o) {
+            release();
+            exec_ = std::move(o.exec_);
+            num_block_rows_ = o.num_block_rows_;
+            num_block_cols_ = o.num_block_cols_;
+            num_blocks_ = o.num_blocks_;
+            r_block_ = o.r_block_;
+            c_block_ = o.c_block_;
+            num_rows_ = o.num_rows_;
+            num_cols_ = o.num_cols_;
+            bcsr_row_ptr_ = o.bcsr_row_ptr_;
+            bcsr_col_ind_ = o.bcsr_col_ind_;
+            bcsr_values_ = o.bcsr_values_;
+            o.bcsr_row_ptr_ = nullptr;
+            o.bcsr_col_ind_ = nullptr;
+            o.bcsr_values_ = nullptr;
+        }
+        return *this;
+    }
+
+    IndexType get_num_block_rows() const { return num_block_rows_; }
+    IndexType get_num_block_cols() const { return num_block_cols_; }
+    IndexType get_num_blocks() const { return num_blocks_; }
+    IndexType get_r_block() const { return r_block_; }
+    IndexType get_c_block() const { return c_block_; }
+
+    // Element shape (see the header comment).
+    IndexType get_num_rows() const { return num_rows_; }
+    IndexType get_num_cols() const { return num_cols_; }
+    void set_shape(IndexType num_rows, IndexType num_cols) {
+        if (num_rows < 0 || num_cols < 0 || num_rows > num_block_rows_ * r_block_ ||
+            num_cols > num_block_cols_ * c_block_) {
+            throw std::invalid_argument("BCSR element shape exceeds its block grid.");
+        }
+        num_rows_ = num_rows;
+        num_cols_ = num_cols;
+    }
+
+    IndexType* get_bcsr_row_ptr() const { return bcsr_row_ptr_; }
+    IndexType* get_bcsr_col_ind() const { return bcsr_col_ind_; }
+    ValueType* get_bcsr_values() const { return bcsr_values_; }
+
+    std::shared_ptr<const Executor> get_executor() const { return exec_; }
+
+    void copy_from_host(const IndexType* host_row_ptr, const IndexType* host_col_ind,
+                        const ValueType* host_values)
+    {
+        exec_->copy_from_host(bcsr_row_ptr_, host_row_ptr,
+                              (static_cast<size_t>(num_block_rows_) + 1) * sizeof(IndexType));
+        if (num_blocks_ > 0) {
+            exec_->copy_from_host(bcsr_col_ind_, host_col_ind,
+                                  static_cast<size_t>(num_blocks_) * sizeof(IndexType));
+            exec_->copy_from_host(bcsr_values_, host_values, value_bytes());
+        }
+    }
+
+private:
+    size_t value_bytes() const {
+        return static_cast<size_t>(num_blocks_) * static_cast<size_t>(r_block_) *
+               static_cast<size_t>(c_block_) * sizeof(ValueType);
+    }
+
+    void release() noexcept {
+        if (!exec_) return;
+        try {
+            if (bcsr_row_ptr_) exec_->free(bcsr_row_ptr_);
+            if (bcsr_col_ind_) exec_->free(bcsr_col_ind_);
+            if (bcsr_values_) exec_->free(bcsr_values_);
+        } catch (...) {
+        }
+        bcsr_row_ptr_ = nullptr;
+        bcsr_col_ind_ = nullptr;
+        bcsr_values_ = nullptr;
+    }
+
+    std::shared_ptr<const Executor> exec_;
+    IndexType num_block_rows_;
+    IndexType num_block_cols_;
+    IndexType num_blocks_;
+    IndexType r_block_;
+    IndexType c_block_;
+    IndexType num_rows_;
+    IndexType num_cols_;
+
+    IndexType* bcsr_row_ptr_ = nullptr;
+    IndexType* bcsr_col_ind_ = nullptr;
+    ValueType* bcsr_values_ = nullptr;
+};
+
+}  // namespace xspmm

@@ -1,0 +1,127 @@
+/*
+ * xspmm_capi.h -- flat C ABI of libxspmm.so (MI355X / gfx950).
+ *
+ * The C++ template API under include/xspmm/ is the drop-in for C++ callers.
+ * These entry points expose the same operations to FFI callers (ctypes, cgo,
+ * JNI, ...): plain pointers, sizes and type codes, no C++ or torch types.
+ * Each one cites the reference interface it replaces.
+ *
+ * Conventions
+ *   - vtype: XSPMM_F32 or XSPMM_F16 (value type of A and B; C is always fp32).
+ *   - itype: XSPMM_I32 or XSPMM_I64 (index type of every index array).
+ *   - Unless stated otherwise pointers are device pointers on the current HIP
+ *     device, and `stream` is a hipStream_t (NULL = the null stream).  Work is
+ *     enqueued on `stream`; functions that must read a size back (the
+ *     conversion count, the pipeline) synchronize that stream.
+ *   - Return value: XSPMM_OK, or an error code with a message available from
+ *     xspmm_last_error() (thread-local).  Nothing throws across this ABI.
+ *   - Every function rejects negative sizes and unknown type codes with
+ *     XSPMM_ERR_INVALID and leaves its outputs untouched.
+ */
+#ifndef XSPMM_CAPI_H
+#define XSPMM_CAPI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XSPMM_F32 0
+#define XSPMM_F16 1
+#define XSPMM_I32 0
+#define XSPMM_I64 1
+
+#define XSPMM_OK 0
+#define XSPMM_ERR_INVALID 1     /* bad argument (std::invalid_argument in C++) */
+#define XSPMM_ERR_HIP 2         /* HIP runtime error (std::runtime_error "HIP Error: ...") */
+#define XSPMM_ERR_UNSUPPORTED 3 /* valid request this build does not support */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* xspmm_last_error(void);
+
+/* ABI version (bumped on any signature change). */
+int xspmm_abi_version(void);
+
+/*
+ * Tier-1 BCSR SpMM: C[M x N] = A_bcsr * B[K x N], row-major, ld = N.
+ * A has 16x16 blocks: brp[Mb+1], bci[nnzb], bvals[nnzb*256] (row-major
+ * blocks).  M <= 16*Mb and K <= 16*Kb are the element shape; rows of C
+ * beyond M are not written and B rows beyond K are not read.  C is
+ * overwritten.  Asynchronous on `stream`.
+ * Replaces xspmm::spmm(const BCSRMatrix<In, Idx>&, const In* B, Out* C, Idx N)
+ * (reference include/xspmm/xspmm.hpp:14-18, src/hip/unstructured_mtx_mul.hip:108-146).
+ */
+int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                    int64_t nnzb, const void* brp, const void* bci, const void* bvals,
+                    const void* B, float* C, int64_t N, void* stream);
+
+/*
+ * CSR -> BCSR, phase 1: writes bcsr_row_ptr[Mb+1] (device) for r x c blocks,
+ * Mb = ceil(M/r), and stores nnzb in *nnzb_out (host).  Synchronizes `stream`.
+ * Fails with XSPMM_ERR_INVALID if a column index lies outside [0, K).
+ * Phase 2 fills bcsr_col_ind[nnzb] and bcsr_vals[nnzb*r*c] (device).
+ * Replaces xspmm::csr_to_bcsr (reference include/xspmm/matrix/conversion.hpp:19-22,
+ * src/core/conversion.cpp:8-100).
+ */
+int xspmm_csr_to_bcsr_count(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
+                            const void* ci, int64_t r_block, int64_t c_block,
+                            void* bcsr_row_ptr, int64_t* nnzb_out, void* stream);
+int xspmm_csr_to_bcsr_fill(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
+                           const void* rp, const void* ci, const void* vals,
+                           int64_t r_block, int64_t c_block, const void* bcsr_row_ptr,
+                           void* bcsr_col_ind, void* bcsr_vals, void* stream);
+
+/*
+ * Row permutation of a CSR matrix: new row i = old row perm[i].
+ * new_rp[M+1], new_ci[nnz], new_vals[nnz] are caller-allocated (device).
+ * perm must be a permutation of [0, M).  Asynchronous on `stream`.
+ * Replaces xspmm::apply_permutation (reference include/xspmm/clustering.hpp:34-38,
+ * src/hip/mtx_permutation.hip:12-67).
+ */
+int xspmm_apply_permutation(int vtype, int itype, int64_t M, int64_t nnz, const void* rp,
+                            const void* ci, const void* vals, const void* perm,
+                            void* new_rp, void* new_ci, void* new_vals, void* stream);
+
+/*
+ * Dense row scatter out[perm[r], :] = in[r, :] of an M x N fp32 matrix.
+ * Asynchronous on `stream`.
+ * Replaces xspmm::unpermute_dense_matrix (reference include/xspmm/xspmm.hpp:35-40,
+ * src/hip/mtx_permutation.hip:73-95).
+ */
+int xspmm_unpermute_dense(int itype, const float* in, float* out, const void* perm,
+                          int64_t M, int64_t N, void* stream);
+
+/*
+ * Host Jaccard row clustering on HOST arrays rp[M+1], ci[nnz]; writes
+ * perm_out[M] (host).  Identical result to the reference's
+ * src/cpu/clustering_sylos_labini.cpp:51-120.  nthreads <= 0 picks the
+ * number of online CPUs.
+ * Replaces xspmm::compute_1d_jaccard_clustering (reference include/xspmm/clustering.hpp:19-25).
+ */
+int xspmm_jaccard_clustering_host(int itype, int64_t M, int64_t K, const void* rp,
+                                  const void* ci, float dist_thresh, int64_t block_width,
+                                  void* perm_out, int nthreads);
+
+/*
+ * Tier-2 pipeline on device CSR arrays rp/ci/vals, device B and C.
+ * hw_block_size must be 16.  With optimize_pattern != 0: cluster (host) ->
+ * permute -> convert -> SpMM -> unpermute; else convert -> SpMM.  timings
+ * (nullable, host) receives the six SpMMTimings fields in declaration order:
+ * clustering, permutation, conversion, spmm, unpermutation, total (ms);
+ * fields of stages that do not run are left unchanged.  Returns after C is
+ * complete.
+ * Replaces xspmm::spmm(exec, const CSRMatrix&, B, C, N, hw_block_size,
+ * optimize_pattern, SpMMTimings*) (reference include/xspmm/xspmm.hpp:24-32,
+ * src/hip/unstructured_mtx_mul.hip:31-100).
+ */
+int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
+                        const void* rp, const void* ci, const void* vals, const void* B,
+                        float* C, int64_t N, int64_t hw_block_size, int optimize_pattern,
+                        double* timings, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XSPMM_CAPI_H */

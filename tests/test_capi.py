@@ -1,0 +1,118 @@
+"""CPU: the C-ABI library loads, exports what include/xspmm_capi.h declares,
+rejects bad arguments before touching the GPU, and its host clustering (the
+product's, not the oracle's) reproduces the reference's permutations."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+import xspmm_amd as X
+from tests.helpers import golden_cases, widen
+from xspmm_amd import synth
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "xspmm_capi.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(xspmm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = X.load()
+    syms = declared_symbols()
+    assert len(syms) >= 9
+    for s in syms:
+        assert hasattr(L, s), s
+    assert L.xspmm_abi_version() == 1
+    assert L.xspmm_last_error() == b""
+
+
+def test_bad_type_codes_are_rejected_without_gpu():
+    L = X.load()
+    rc = L.xspmm_bcsr_spmm(7, X.I32, 16, 16, 1, 1, 0, None, None, None, None, None, 16, None)
+    assert rc == X.ERR_INVALID and b"value type" in L.xspmm_last_error()
+    rc = L.xspmm_bcsr_spmm(X.F16, 9, 16, 16, 1, 1, 0, None, None, None, None, None, 16, None)
+    assert rc == X.ERR_INVALID and b"index type" in L.xspmm_last_error()
+    rc = L.xspmm_unpermute_dense(5, None, None, None, 4, 4, None)
+    assert rc == X.ERR_INVALID
+
+
+def test_negative_and_inconsistent_sizes_are_rejected_without_gpu():
+    L = X.load()
+    assert L.xspmm_bcsr_spmm(X.F16, X.I32, -1, 16, 1, 1, 0, None, None, None, None, None, 16,
+                             None) == X.ERR_INVALID
+    # element shape larger than the block grid
+    assert L.xspmm_bcsr_spmm(X.F16, X.I32, 33, 16, 2, 1, 0, None, None, None, None, None, 16,
+                             None) == X.ERR_INVALID
+    n = C.c_int64(0)
+    assert L.xspmm_csr_to_bcsr_count(X.I32, 4, 4, 0, None, None, 0, 16, None, C.byref(n),
+                                     None) == X.ERR_INVALID
+    assert L.xspmm_csr_to_bcsr_count(X.I32, 4, 4, 0, None, None, 2000, 16, None, C.byref(n),
+                                     None) == X.ERR_INVALID
+    assert L.xspmm_csr_to_bcsr_count(X.I32, 4, 4, 0, None, None, 16, 16, None, None,
+                                     None) == X.ERR_INVALID
+    assert L.xspmm_spmm_pipeline(X.F16, X.I32, 4, 4, 0, None, None, None, None, None, 4, 8, 1,
+                                 None, None) == X.ERR_INVALID
+    assert b"hw_block_size" in L.xspmm_last_error()
+
+
+def test_host_clustering_error_paths():
+    with pytest.raises(X.XspmmInvalidArgument):
+        X.compute_1d_jaccard_clustering(2, 16, np.array([0, 1, 2], np.int32),
+                                        np.array([0, 99], np.int32))
+    with pytest.raises(X.XspmmInvalidArgument):
+        X.compute_1d_jaccard_clustering(1, 16, np.array([0, 1], np.int32),
+                                        np.array([0], np.int32), block_width=0)
+    assert len(X.compute_1d_jaccard_clustering(0, 16, np.array([0], np.int32),
+                                               np.zeros(0, np.int32))) == 0
+
+
+JAC = golden_cases("jaccard")
+
+
+@pytest.mark.parametrize("engine", ["scan", "index", "auto"])
+@pytest.mark.parametrize("case", JAC, ids=[c["name"] for c in JAC])
+def test_product_clustering_matches_reference_golden(case, engine, monkeypatch):
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    for nthreads in (1, 4):
+        perm = X.compute_1d_jaccard_clustering(int(case["M"]), int(case["K"]), case["rp"],
+                                               case["ci"], float(case["thresh"]),
+                                               int(case["bw"]), nthreads=nthreads)
+        assert perm.dtype == case["rp"].dtype
+        np.testing.assert_array_equal(widen(perm), widen(case["perm"]))
+
+
+@pytest.mark.parametrize("engine", ["scan", "index"])
+@pytest.mark.parametrize("seed", range(8))
+def test_product_clustering_matches_oracle_random(seed, engine, monkeypatch):
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    rng = np.random.default_rng(300 + seed)
+    M, K = int(rng.integers(1, 2500)), int(rng.integers(16, 3000))
+    thr = float([0.5, 0.5, 0.4, 0.5, 0.25, 0.7, 0.5, 0.5][seed])
+    bw = [16, 16, 8, 4, 16, 16, 2, 16][seed]
+    p = synth.random_csr(M, K, 4, float(rng.uniform(0.001, 0.03)), seed=seed,
+                         dtype=np.float32, unsorted=bool(seed % 2))
+    want = oracle.jaccard(M, K, p.rp, p.ci, thr, bw)
+    got = X.compute_1d_jaccard_clustering(M, K, p.rp, p.ci, thr, bw, nthreads=1 + seed % 4)
+    np.testing.assert_array_equal(widen(got), want)
+
+
+def test_product_clustering_templates_like_input():
+    # a scaled-down version of the headline configuration (same generator)
+    p = synth.templates(M=2048, n_templates=128, seed=5)
+    want = oracle.jaccard(p.M, p.K, p.rp, p.ci)
+    for engine in ("scan", "index"):
+        os.environ["XSPMM_CLUSTER_ENGINE"] = engine
+        try:
+            got = X.compute_1d_jaccard_clustering(p.M, p.K, p.rp, p.ci, nthreads=4)
+        finally:
+            del os.environ["XSPMM_CLUSTER_ENGINE"]
+        np.testing.assert_array_equal(widen(got), want)

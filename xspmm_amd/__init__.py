@@ -1,0 +1,287 @@
+"""xspmm_amd -- MI355X-native xSpMM SpMM hot path.
+
+The product is ``libxspmm.so`` (built from ``xspmm_amd/csrc`` with hipcc for
+gfx950): hand-written HIP kernels behind the reference's C++ API
+(``include/xspmm/*.hpp``) and a flat C ABI (``include/xspmm_capi.h``).
+
+This module is the Python view of that C ABI.  It mirrors the reference's
+operator interface -- ``CSRMatrix``, ``BCSRMatrix``, ``csr_to_bcsr``,
+``compute_1d_jaccard_clustering``, ``apply_permutation``, Tier-1 ``spmm``,
+the Tier-2 pipeline ``spmm_pipeline`` and ``unpermute_dense_matrix`` -- with
+torch tensors as device buffers.  Every call goes to the HIP library; there
+is no CPU fallback, and importing the library fails loudly when it has not
+been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libxspmm.so")
+
+F32, F16 = 0, 1
+I32, I64 = 0, 1
+OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3
+
+TIMING_FIELDS = ("clustering_ms", "permutation_ms", "conversion_ms", "spmm_ms",
+                 "unpermutation_ms", "total_pipeline_ms")
+
+_lib = None
+
+
+class XspmmError(RuntimeError):
+    """A HIP or unsupported-operation failure reported by libxspmm."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+class XspmmInvalidArgument(XspmmError, ValueError):
+    """std::invalid_argument in the C++ API."""
+
+
+def load():
+    """Load libxspmm.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                           "(make -C xspmm_amd/csrc)")
+    L = C.CDLL(LIB_PATH)
+    p, i64, i32 = C.c_void_p, C.c_int64, C.c_int
+    L.xspmm_last_error.restype = C.c_char_p
+    L.xspmm_last_error.argtypes = []
+    L.xspmm_abi_version.restype = i32
+    L.xspmm_abi_version.argtypes = []
+    L.xspmm_bcsr_spmm.restype = i32
+    L.xspmm_bcsr_spmm.argtypes = [i32, i32, i64, i64, i64, i64, i64, p, p, p, p, p, i64, p]
+    L.xspmm_csr_to_bcsr_count.restype = i32
+    L.xspmm_csr_to_bcsr_count.argtypes = [i32, i64, i64, i64, p, p, i64, i64, p,
+                                          C.POINTER(C.c_int64), p]
+    L.xspmm_csr_to_bcsr_fill.restype = i32
+    L.xspmm_csr_to_bcsr_fill.argtypes = [i32, i32, i64, i64, i64, p, p, p, i64, i64, p, p, p, p]
+    L.xspmm_apply_permutation.restype = i32
+    L.xspmm_apply_permutation.argtypes = [i32, i32, i64, i64, p, p, p, p, p, p, p, p]
+    L.xspmm_unpermute_dense.restype = i32
+    L.xspmm_unpermute_dense.argtypes = [i32, p, p, p, i64, i64, p]
+    L.xspmm_jaccard_clustering_host.restype = i32
+    L.xspmm_jaccard_clustering_host.argtypes = [i32, i64, i64, p, p, C.c_float, i64, p, i32]
+    L.xspmm_spmm_pipeline.restype = i32
+    L.xspmm_spmm_pipeline.argtypes = [i32, i32, i64, i64, i64, p, p, p, p, p, i64, i64, i32,
+                                      C.POINTER(C.c_double), p]
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc == OK:
+        return
+    msg = load().xspmm_last_error().decode(errors="replace")
+    if rc == ERR_INVALID:
+        raise XspmmInvalidArgument(rc, msg)
+    raise XspmmError(rc, msg)
+
+
+# ---------------------------------------------------------------------------
+# type codes / pointers
+# ---------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def vcode(dtype) -> int:
+    torch = _torch()
+    if dtype in (torch.float16, np.float16):
+        return F16
+    if dtype in (torch.float32, np.float32):
+        return F32
+    raise TypeError(f"unsupported value dtype {dtype}")
+
+
+def icode(dtype) -> int:
+    torch = _torch()
+    if dtype in (torch.int32, np.int32):
+        return I32
+    if dtype in (torch.int64, np.int64):
+        return I64
+    raise TypeError(f"unsupported index dtype {dtype}")
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None and t.numel() > 0 else C.c_void_p(0)
+
+
+def _stream():
+    torch = _torch()
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _device(dev=None):
+    torch = _torch()
+    if dev is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return torch.device(dev)
+
+
+# ---------------------------------------------------------------------------
+# matrices
+# ---------------------------------------------------------------------------
+
+@dataclass
+class CSRMatrix:
+    """Device CSR matrix (reference include/xspmm/matrix/csr.hpp:12-71)."""
+    num_rows: int
+    num_cols: int
+    row_ptr: object   # torch int32/int64 [M+1]
+    col_ind: object   # [nnz]
+    values: object    # torch float16/float32 [nnz]
+
+    @property
+    def nnz(self) -> int:
+        return int(self.col_ind.numel())
+
+    @classmethod
+    def from_host(cls, M, K, rp, ci, vals, device=None, index_dtype=None):
+        torch = _torch()
+        dev = _device(device)
+        rp = np.asarray(rp)
+        idt = index_dtype or rp.dtype
+        it = torch.int32 if np.dtype(idt) == np.int32 else torch.int64
+        return cls(int(M), int(K),
+                   torch.as_tensor(np.ascontiguousarray(rp)).to(dev, it),
+                   torch.as_tensor(np.ascontiguousarray(ci)).to(dev, it),
+                   torch.as_tensor(np.ascontiguousarray(vals)).to(dev))
+
+
+@dataclass
+class BCSRMatrix:
+    """Device BCSR matrix (reference include/xspmm/matrix/bcsr.hpp:12-116),
+    plus the element shape num_rows x num_cols."""
+    num_block_rows: int
+    num_block_cols: int
+    r_block: int
+    c_block: int
+    num_rows: int
+    num_cols: int
+    row_ptr: object   # [Mb+1]
+    col_ind: object   # [nnzb]
+    values: object    # [nnzb * r * c]
+
+    @property
+    def num_blocks(self) -> int:
+        return int(self.col_ind.numel())
+
+
+# ---------------------------------------------------------------------------
+# operations
+# ---------------------------------------------------------------------------
+
+def csr_to_bcsr(A: CSRMatrix, r_block: int = 16, c_block: int = 16) -> BCSRMatrix:
+    """GPU CSR -> BCSR (reference include/xspmm/matrix/conversion.hpp:19-22)."""
+    torch = _torch()
+    L = load()
+    dev = A.row_ptr.device
+    it = A.row_ptr.dtype
+    Mb = (A.num_rows + r_block - 1) // r_block
+    Kb = (A.num_cols + c_block - 1) // c_block
+    brp = torch.empty(Mb + 1, dtype=it, device=dev)
+    nnzb = C.c_int64(0)
+    _check(L.xspmm_csr_to_bcsr_count(icode(it), A.num_rows, A.num_cols, A.nnz, _ptr(A.row_ptr),
+                                     _ptr(A.col_ind), r_block, c_block, _ptr(brp),
+                                     C.byref(nnzb), _stream()))
+    n = nnzb.value
+    bci = torch.empty(max(n, 0), dtype=it, device=dev)
+    bv = torch.empty(max(n, 0) * r_block * c_block, dtype=A.values.dtype, device=dev)
+    _check(L.xspmm_csr_to_bcsr_fill(vcode(A.values.dtype), icode(it), A.num_rows, A.num_cols,
+                                    A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values),
+                                    r_block, c_block, _ptr(brp), _ptr(bci), _ptr(bv), _stream()))
+    return BCSRMatrix(Mb, Kb, r_block, c_block, A.num_rows, A.num_cols, brp, bci, bv)
+
+
+def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
+    """Tier-1 C = A * B (reference include/xspmm/xspmm.hpp:14-18).  B is
+    K x N row-major on the device; returns C (M x N fp32)."""
+    torch = _torch()
+    L = load()
+    if N is None:
+        N = int(B.shape[1]) if B.dim() == 2 else int(B.numel() // max(A.num_cols, 1))
+    if C_out is None:
+        C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=A.row_ptr.device)
+    if A.values.dtype != B.dtype:
+        raise TypeError("A and B must share a value dtype")
+    _check(L.xspmm_bcsr_spmm(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows, A.num_cols,
+                             A.num_block_rows, A.num_block_cols, A.num_blocks, _ptr(A.row_ptr),
+                             _ptr(A.col_ind), _ptr(A.values), _ptr(B), _ptr(C_out), N, _stream()))
+    return C_out
+
+
+def compute_1d_jaccard_clustering(M, K, rp, ci, dist_thresh=0.5, block_width=16, nthreads=0):
+    """Host Jaccard clustering on host arrays -> perm (numpy, same dtype as rp)
+    (reference include/xspmm/clustering.hpp:19-25)."""
+    L = load()
+    rp = np.ascontiguousarray(rp)
+    ci = np.ascontiguousarray(ci, dtype=rp.dtype)
+    perm = np.zeros(max(int(M), 1), dtype=rp.dtype)
+    _check(L.xspmm_jaccard_clustering_host(icode(rp.dtype), int(M), int(K),
+                                           rp.ctypes.data_as(C.c_void_p),
+                                           ci.ctypes.data_as(C.c_void_p) if ci.size else None,
+                                           C.c_float(dist_thresh), int(block_width),
+                                           perm.ctypes.data_as(C.c_void_p), int(nthreads)))
+    return perm[: int(M)]
+
+
+def apply_permutation(A: CSRMatrix, perm) -> CSRMatrix:
+    """GPU row permutation (reference include/xspmm/clustering.hpp:34-38)."""
+    torch = _torch()
+    L = load()
+    dev = A.row_ptr.device
+    it = A.row_ptr.dtype
+    perm_t = torch.as_tensor(perm).to(dev, it) if not torch.is_tensor(perm) else perm.to(dev, it)
+    nrp = torch.empty(A.num_rows + 1, dtype=it, device=dev)
+    nci = torch.empty_like(A.col_ind)
+    nv = torch.empty_like(A.values)
+    _check(L.xspmm_apply_permutation(vcode(A.values.dtype), icode(it), A.num_rows, A.nnz,
+                                     _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values),
+                                     _ptr(perm_t), _ptr(nrp), _ptr(nci), _ptr(nv), _stream()))
+    return CSRMatrix(A.num_rows, A.num_cols, nrp, nci, nv)
+
+
+def unpermute_dense_matrix(C_in, perm, out=None):
+    """out[perm[r], :] = C_in[r, :] (reference include/xspmm/xspmm.hpp:35-40)."""
+    torch = _torch()
+    L = load()
+    M, N = int(C_in.shape[0]), int(C_in.shape[1])
+    if out is None:
+        out = torch.empty_like(C_in)
+    perm_t = perm if torch.is_tensor(perm) else torch.as_tensor(np.asarray(perm)).to(C_in.device)
+    _check(L.xspmm_unpermute_dense(icode(perm_t.dtype), _ptr(C_in), _ptr(out), _ptr(perm_t), M, N,
+                                   _stream()))
+    return out
+
+
+def spmm_pipeline(A: CSRMatrix, B, C_out=None, N: int | None = None, hw_block_size: int = 16,
+                  optimize_pattern: bool = True, timings: bool = True):
+    """Tier-2 pipeline (reference include/xspmm/xspmm.hpp:24-32).
+    Returns (C, timings dict or None)."""
+    torch = _torch()
+    L = load()
+    if N is None:
+        N = int(B.shape[1])
+    if C_out is None:
+        C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=A.row_ptr.device)
+    t = (C.c_double * 6)() if timings else None
+    _check(L.xspmm_spmm_pipeline(vcode(A.values.dtype), icode(A.row_ptr.dtype), A.num_rows,
+                                 A.num_cols, A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind),
+                                 _ptr(A.values), _ptr(B), _ptr(C_out), N, hw_block_size,
+                                 1 if optimize_pattern else 0,
+                                 C.cast(t, C.POINTER(C.c_double)) if t is not None else None,
+                                 _stream()))
+    return C_out, (dict(zip(TIMING_FIELDS, list(t))) if t is not None else None)

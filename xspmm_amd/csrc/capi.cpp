@@ -1,0 +1,187 @@
+// capi.cpp -- extern "C" entry points declared in include/xspmm_capi.h.
+// Each maps type codes onto the internal launchers and turns exceptions into
+// error codes (std::invalid_argument -> XSPMM_ERR_INVALID, "HIP Error" ->
+// XSPMM_ERR_HIP, any other failure -> XSPMM_ERR_UNSUPPORTED).
+#include <cstring>
+#include <string>
+#include <utility>
+
+#include "internal.hpp"
+#include "xspmm_capi.h"
+
+using namespace xspmm::detail;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename F>
+int guarded(F&& f)
+{
+    try {
+        f();
+        g_last_error.clear();
+        return XSPMM_OK;
+    } catch (const std::invalid_argument& e) {
+        g_last_error = e.what();
+        return XSPMM_ERR_INVALID;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return std::strncmp(e.what(), "HIP Error", 9) == 0 ? XSPMM_ERR_HIP : XSPMM_ERR_UNSUPPORTED;
+    } catch (...) {
+        g_last_error = "unknown error";
+        return XSPMM_ERR_UNSUPPORTED;
+    }
+}
+
+template <typename T>
+struct Tag { using type = T; };
+
+// Calls f(Tag<value>, Tag<index>) for the requested type codes.
+template <typename F>
+void with_types(int vtype, int itype, F&& f)
+{
+    if (itype != XSPMM_I32 && itype != XSPMM_I64) throw std::invalid_argument("unknown index type code");
+    if (vtype != XSPMM_F32 && vtype != XSPMM_F16) throw std::invalid_argument("unknown value type code");
+    if (vtype == XSPMM_F16) {
+        if (itype == XSPMM_I32) f(Tag<uint16_t>{}, Tag<int32_t>{});
+        else f(Tag<uint16_t>{}, Tag<int64_t>{});
+    } else {
+        if (itype == XSPMM_I32) f(Tag<float>{}, Tag<int32_t>{});
+        else f(Tag<float>{}, Tag<int64_t>{});
+    }
+}
+
+template <typename F>
+void with_index(int itype, F&& f)
+{
+    if (itype == XSPMM_I32) f(Tag<int32_t>{});
+    else if (itype == XSPMM_I64) f(Tag<int64_t>{});
+    else throw std::invalid_argument("unknown index type code");
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+void require(bool ok, const char* what)
+{
+    if (!ok) throw std::invalid_argument(what);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* xspmm_last_error(void) { return g_last_error.c_str(); }
+
+int xspmm_abi_version(void) { return 1; }
+
+int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                    int64_t nnzb, const void* brp, const void* bci, const void* bvals,
+                    const void* B, float* C, int64_t N, void* stream)
+{
+    return guarded([&] {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            bcsr_spmm<T, I>(M, K, Mb, Kb, nnzb, static_cast<const I*>(brp), static_cast<const I*>(bci),
+                            static_cast<const T*>(bvals), static_cast<const T*>(B), C, N,
+                            as_stream(stream));
+        });
+    });
+}
+
+int xspmm_csr_to_bcsr_count(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
+                            const void* ci, int64_t r_block, int64_t c_block,
+                            void* bcsr_row_ptr, int64_t* nnzb_out, void* stream)
+{
+    return guarded([&] {
+        require(nnzb_out != nullptr, "nnzb_out is null");
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            *nnzb_out = csr_to_bcsr_count<I>(M, K, nnz, static_cast<const I*>(rp),
+                                             static_cast<const I*>(ci), r_block, c_block,
+                                             static_cast<I*>(bcsr_row_ptr), as_stream(stream));
+        });
+    });
+}
+
+int xspmm_csr_to_bcsr_fill(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
+                           const void* rp, const void* ci, const void* vals,
+                           int64_t r_block, int64_t c_block, const void* bcsr_row_ptr,
+                           void* bcsr_col_ind, void* bcsr_vals, void* stream)
+{
+    return guarded([&] {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            csr_to_bcsr_fill<T, I>(M, K, nnz, static_cast<const I*>(rp), static_cast<const I*>(ci),
+                                   static_cast<const T*>(vals), r_block, c_block,
+                                   static_cast<const I*>(bcsr_row_ptr), static_cast<I*>(bcsr_col_ind),
+                                   static_cast<T*>(bcsr_vals), as_stream(stream));
+        });
+    });
+}
+
+int xspmm_apply_permutation(int vtype, int itype, int64_t M, int64_t nnz, const void* rp,
+                            const void* ci, const void* vals, const void* perm,
+                            void* new_rp, void* new_ci, void* new_vals, void* stream)
+{
+    return guarded([&] {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            apply_permutation<T, I>(M, nnz, static_cast<const I*>(rp), static_cast<const I*>(ci),
+                                    static_cast<const T*>(vals), static_cast<const I*>(perm),
+                                    static_cast<I*>(new_rp), static_cast<I*>(new_ci),
+                                    static_cast<T*>(new_vals), as_stream(stream));
+        });
+    });
+}
+
+int xspmm_unpermute_dense(int itype, const float* in, float* out, const void* perm, int64_t M,
+                          int64_t N, void* stream)
+{
+    return guarded([&] {
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            unpermute_dense<I>(in, out, static_cast<const I*>(perm), M, N, as_stream(stream));
+        });
+    });
+}
+
+int xspmm_jaccard_clustering_host(int itype, int64_t M, int64_t K, const void* rp,
+                                  const void* ci, float dist_thresh, int64_t block_width,
+                                  void* perm_out, int nthreads)
+{
+    return guarded([&] {
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            jaccard_clustering_host<I>(M, K, static_cast<const I*>(rp), static_cast<const I*>(ci),
+                                       dist_thresh, block_width, static_cast<I*>(perm_out), nthreads);
+        });
+    });
+}
+
+int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
+                        const void* rp, const void* ci, const void* vals, const void* B,
+                        float* C, int64_t N, int64_t hw_block_size, int optimize_pattern,
+                        double* timings, void* stream)
+{
+    return guarded([&] {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            require(M >= 0 && K >= 0 && nnz >= 0 && N >= 0, "CSR dimensions must be non-negative.");
+            require(hw_block_size == 16,
+                    "xSpMM: the MFMA tile kernel requires hw_block_size == 16.");
+            int dev = 0;
+            XSPMM_HIP_CHECK(hipGetDevice(&dev));
+            init_device_pool(dev);
+            spmm_pipeline<T, I>(M, K, nnz, static_cast<const I*>(rp), static_cast<const I*>(ci),
+                                static_cast<const T*>(vals), static_cast<const T*>(B), C, N,
+                                hw_block_size, optimize_pattern != 0, timings, as_stream(stream));
+        });
+    });
+}
+
+}  // extern "C"

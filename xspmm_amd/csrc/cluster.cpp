@@ -1,0 +1,356 @@
+// cluster.cpp -- host 1-D Jaccard ("Sylos Labini") row clustering.
+//
+// Exact restatement of the reference greedy (src/cpu/clustering_sylos_labini.cpp:51-120):
+//   q_i = bitmap of the block_width-wide column blocks row i touches (:13-33);
+//   unclustered = [0..M-1]; while non-empty: seed = pop_back(); p = q_seed;
+//   for i = size-1 down to 0: cand = unclustered[i];
+//     d = |p|q| == 0 ? 0 : 1 - (float)|p&q| / (float)|p|q|          (:35-46)
+//     if d <= dist_thresh: join cand, p |= q_cand,
+//                          unclustered[i] = back(), pop_back()       (:97-104)
+//   perm = clusters in creation order, members in join order (:110-116).
+//
+// The visiting order of a seed's scan is "positions of `unclustered` as they
+// were when the seed was popped, descending": a swap-remove at position i only
+// moves an element that was already visited into slot i.  Both engines below
+// reproduce that order and the float comparison exactly, so the permutation
+// equals the reference's bit for bit.
+//
+//  * scan:  the reference loop with the candidate tests of a stretch of
+//           positions evaluated in parallel against the current pattern; the
+//           highest joining position is committed and the scan resumes below
+//           it.  A popcount bound (d >= 1 - min(|p|,|q|)/max(|p|,|q|), which is
+//           monotone under float rounding) skips most bitmap work.
+//  * index: for 0 <= dist_thresh < 1 a row can only join a cluster whose
+//           pattern shares a block with it (d = 1 otherwise), or an empty
+//           pattern if it is empty itself.  Candidates come from per-block row
+//           lists; |p&q| is counted through the lists, |p|q| = |p|+|q|-|p&q|.
+//           Work is sum over blocks of list length^2 instead of M^2 * words.
+// `auto` picks the engine with the smaller estimated cost; the environment
+// variable XSPMM_CLUSTER_ENGINE=scan|index forces one (used by the tests).
+#include <algorithm>
+#include <atomic>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <queue>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace xspmm {
+namespace detail {
+
+namespace {
+
+inline float jaccard_distance(int64_t inter, int64_t uni)
+{
+    if (uni == 0) return 0.0f;
+    return 1.0f - (static_cast<float>(inter) / static_cast<float>(uni));
+}
+
+struct Patterns {
+    int64_t M = 0, nblk = 0, words = 0;
+    std::vector<uint64_t> bits;   // M * words
+    std::vector<int32_t> count;   // popcount per row
+    const uint64_t* row(int64_t i) const { return bits.data() + i * words; }
+};
+
+template <typename I>
+Patterns build_patterns(int64_t M, int64_t K, const I* rp, const I* ci, int64_t bw)
+{
+    Patterns P;
+    P.M = M;
+    P.nblk = (K + bw - 1) / bw;
+    P.words = (P.nblk + 63) / 64;
+    if (P.words == 0) P.words = 1;
+    P.bits.assign((size_t)(M * P.words), 0ULL);
+    P.count.assign((size_t)M, 0);
+    for (int64_t i = 0; i < M; ++i) {
+        uint64_t* q = P.bits.data() + i * P.words;
+        for (int64_t j = (int64_t)rp[i]; j < (int64_t)rp[i + 1]; ++j) {
+            const int64_t c = (int64_t)ci[j];
+            if (c < 0 || c >= K) throw std::invalid_argument("clustering: column index out of range.");
+            const int64_t b = c / bw;
+            q[b >> 6] |= 1ULL << (b & 63);
+        }
+        int32_t n = 0;
+        for (int64_t w = 0; w < P.words; ++w) n += __builtin_popcountll(q[w]);
+        P.count[(size_t)i] = n;
+    }
+    return P;
+}
+
+// Minimal fork-join pool: run(f) calls f(t) for t in [0, n) on n threads
+// (t = 0 on the caller) and returns when all are done.
+class Pool {
+public:
+    explicit Pool(int n) : n_(n < 1 ? 1 : n) {
+        for (int t = 1; t < n_; ++t) th_.emplace_back([this, t] { worker(t); });
+    }
+    ~Pool() {
+        stop_.store(true, std::memory_order_release);
+        gen_.fetch_add(1, std::memory_order_acq_rel);
+        for (auto& t : th_) t.join();
+    }
+    int size() const { return n_; }
+    void run(const std::function<void(int)>& f) {
+        if (n_ == 1) {
+            f(0);
+            return;
+        }
+        task_ = &f;
+        pending_.store(n_ - 1, std::memory_order_release);
+        gen_.fetch_add(1, std::memory_order_acq_rel);
+        f(0);
+        while (pending_.load(std::memory_order_acquire) != 0) std::this_thread::yield();
+    }
+
+private:
+    void worker(int t) {
+        uint64_t seen = 0;
+        for (;;) {
+            uint64_t g;
+            int spins = 0;
+            while ((g = gen_.load(std::memory_order_acquire)) == seen) {
+                if (++spins > 64) std::this_thread::yield();
+            }
+            seen = g;
+            if (stop_.load(std::memory_order_acquire)) return;
+            (*task_)(t);
+            pending_.fetch_sub(1, std::memory_order_acq_rel);
+        }
+    }
+    int n_;
+    std::vector<std::thread> th_;
+    std::atomic<uint64_t> gen_{0};
+    std::atomic<int> pending_{0};
+    std::atomic<bool> stop_{false};
+    const std::function<void(int)>* task_ = nullptr;
+};
+
+template <typename I>
+void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
+{
+    const int64_t M = P.M, W = P.words;
+    std::vector<int64_t> un((size_t)M);
+    for (int64_t i = 0; i < M; ++i) un[(size_t)i] = i;
+    int64_t n_un = M, out = 0;
+    std::vector<uint64_t> p((size_t)W);
+    Pool pool(nthreads);
+    const int nt = pool.size();
+    std::vector<int64_t> found((size_t)nt);
+
+    while (n_un > 0) {
+        const int64_t seed = un[(size_t)--n_un];
+        perm[out++] = (I)seed;
+        std::memcpy(p.data(), P.row(seed), (size_t)W * sizeof(uint64_t));
+        int64_t pc = P.count[(size_t)seed];
+        int64_t hi = n_un - 1;  // next position to visit
+        int64_t stretch = 2048;
+        while (hi >= 0) {
+            // First joining position in [lo, hi], scanning downwards.
+            const int64_t lo = hi - stretch + 1 > 0 ? hi - stretch + 1 : 0;
+            auto test = [&](int64_t pos) {
+                const int64_t cand = un[(size_t)pos];
+                const int64_t qc = P.count[(size_t)cand];
+                const int64_t mn = qc < pc ? qc : pc, mx = qc < pc ? pc : qc;
+                if (jaccard_distance(mn, mx) > t) return false;  // cannot reach t
+                const uint64_t* q = P.row(cand);
+                int64_t inter = 0, uni = 0;
+                for (int64_t w = 0; w < W; ++w) {
+                    inter += __builtin_popcountll(p[(size_t)w] & q[w]);
+                    uni += __builtin_popcountll(p[(size_t)w] | q[w]);
+                }
+                return jaccard_distance(inter, uni) <= t;
+            };
+            int64_t hit = -1;
+            const int64_t len = hi - lo + 1;
+            if (nt == 1 || len < 4 * nt) {
+                for (int64_t pos = hi; pos >= lo; --pos)
+                    if (test(pos)) { hit = pos; break; }
+            } else {
+                pool.run([&](int tid) {
+                    const int64_t per = (len + nt - 1) / nt;
+                    const int64_t top = hi - (int64_t)tid * per;
+                    const int64_t bot = top - per + 1 > lo ? top - per + 1 : lo;
+                    int64_t f = -1;
+                    for (int64_t pos = top; pos >= bot; --pos)
+                        if (test(pos)) { f = pos; break; }
+                    found[(size_t)tid] = f;
+                });
+                for (int k = 0; k < nt; ++k)
+                    if (found[(size_t)k] > hit) hit = found[(size_t)k];
+            }
+            if (hit < 0) {
+                hi = lo - 1;
+                stretch *= 2;
+                continue;
+            }
+            const int64_t cand = un[(size_t)hit];
+            perm[out++] = (I)cand;
+            const uint64_t* q = P.row(cand);
+            pc = 0;
+            for (int64_t w = 0; w < W; ++w) {
+                p[(size_t)w] |= q[w];
+                pc += __builtin_popcountll(p[(size_t)w]);
+            }
+            un[(size_t)hit] = un[(size_t)(n_un - 1)];
+            --n_un;
+            hi = hit - 1;
+            stretch = 2048;
+        }
+    }
+}
+
+template <typename I>
+void engine_index(const Patterns& P, float t, I* perm)
+{
+    // Requires 0 <= t < 1 (checked by the caller).
+    const int64_t M = P.M, W = P.words, NB = P.nblk;
+    // Row lists per block (CSR of the transposed pattern).
+    std::vector<int64_t> start((size_t)NB + 1, 0);
+    for (int64_t i = 0; i < M; ++i) {
+        const uint64_t* q = P.row(i);
+        for (int64_t w = 0; w < W; ++w)
+            for (uint64_t b = q[w]; b; b &= b - 1) ++start[(size_t)(w * 64 + __builtin_ctzll(b)) + 1];
+    }
+    for (int64_t b = 0; b < NB; ++b) start[(size_t)b + 1] += start[(size_t)b];
+    std::vector<int64_t> rows((size_t)start[(size_t)NB]);
+    {
+        std::vector<int64_t> fill(start.begin(), start.end() - 1);
+        for (int64_t i = 0; i < M; ++i) {
+            const uint64_t* q = P.row(i);
+            for (int64_t w = 0; w < W; ++w)
+                for (uint64_t b = q[w]; b; b &= b - 1)
+                    rows[(size_t)fill[(size_t)(w * 64 + __builtin_ctzll(b))]++] = i;
+        }
+    }
+
+    std::vector<int64_t> un((size_t)M), pos((size_t)M);
+    for (int64_t i = 0; i < M; ++i) un[(size_t)i] = pos[(size_t)i] = i;
+    std::vector<uint8_t> done((size_t)M, 0);
+    std::vector<int32_t> cnt((size_t)M, 0);  // |p & q_row| for touched rows
+    std::vector<int64_t> touched;
+    std::vector<uint64_t> p((size_t)W);
+    int64_t n_un = M, out = 0;
+
+    auto remove_at = [&](int64_t at) {  // swap-remove, as the reference does
+        const int64_t moved = un[(size_t)(n_un - 1)];
+        un[(size_t)at] = moved;
+        pos[(size_t)moved] = at;
+        --n_un;
+    };
+
+    while (n_un > 0) {
+        const int64_t seed = un[(size_t)(n_un - 1)];
+        --n_un;
+        done[(size_t)seed] = 1;
+        perm[out++] = (I)seed;
+        if (P.count[(size_t)seed] == 0) {
+            // Empty pattern: exactly the remaining empty rows join, in
+            // descending position order; the pattern stays empty.
+            std::vector<std::pair<int64_t, int64_t>> empties;
+            for (int64_t k = 0; k < n_un; ++k) {
+                const int64_t r = un[(size_t)k];
+                if (P.count[(size_t)r] == 0) empties.emplace_back(k, r);
+            }
+            std::sort(empties.begin(), empties.end(),
+                      [](const auto& a, const auto& b) { return a.first > b.first; });
+            for (const auto& e : empties) {
+                perm[out++] = (I)e.second;
+                done[(size_t)e.second] = 1;
+                remove_at(pos[(size_t)e.second]);
+            }
+            continue;
+        }
+        std::memcpy(p.data(), P.row(seed), (size_t)W * sizeof(uint64_t));
+        int64_t pc = P.count[(size_t)seed];
+        std::priority_queue<std::pair<int64_t, int64_t>> heap;  // (position, row), max first
+        int64_t limit = n_un;  // only positions below `limit` are unvisited
+        auto touch_block = [&](int64_t b) {
+            for (int64_t k = start[(size_t)b]; k < start[(size_t)b + 1]; ++k) {
+                const int64_t r = rows[(size_t)k];
+                if (done[(size_t)r]) continue;
+                if (cnt[(size_t)r]++ == 0) {
+                    touched.push_back(r);
+                    if (pos[(size_t)r] < limit) heap.emplace(pos[(size_t)r], r);
+                }
+            }
+        };
+        for (int64_t w = 0; w < W; ++w)
+            for (uint64_t b = p[(size_t)w]; b; b &= b - 1) touch_block(w * 64 + __builtin_ctzll(b));
+        while (!heap.empty()) {
+            const auto top = heap.top();
+            heap.pop();
+            const int64_t at = top.first, r = top.second;
+            limit = at;
+            const int64_t inter = cnt[(size_t)r];
+            const int64_t uni = pc + P.count[(size_t)r] - inter;
+            if (jaccard_distance(inter, uni) > t) continue;
+            perm[out++] = (I)r;
+            done[(size_t)r] = 1;
+            remove_at(at);
+            const uint64_t* q = P.row(r);
+            for (int64_t w = 0; w < W; ++w) {
+                uint64_t add = q[w] & ~p[(size_t)w];
+                p[(size_t)w] |= q[w];
+                for (; add; add &= add - 1) {
+                    ++pc;
+                    touch_block(w * 64 + __builtin_ctzll(add));
+                }
+            }
+        }
+        for (int64_t r : touched) cnt[(size_t)r] = 0;
+        touched.clear();
+    }
+}
+
+}  // namespace
+
+template <typename I>
+void jaccard_clustering_host(int64_t M, int64_t K, const I* rp, const I* ci, float dist_thresh,
+                             int64_t block_width, I* perm, int nthreads)
+{
+    if (M < 0 || K < 0) throw std::invalid_argument("CSR dimensions must be non-negative.");
+    if (M == 0) return;  // reference :63
+    if (block_width <= 0) throw std::invalid_argument("clustering: block_width must be positive.");
+    if (nthreads <= 0) {
+        const unsigned hc = std::thread::hardware_concurrency();
+        nthreads = hc ? (int)(hc < 32 ? hc : 32) : 1;
+    }
+    const Patterns P = build_patterns(M, K, rp, ci, block_width);
+
+    std::string engine = "auto";
+    if (const char* e = std::getenv("XSPMM_CLUSTER_ENGINE")) engine = e;
+    const bool index_ok = dist_thresh >= 0.0f && dist_thresh < 1.0f;
+    if (engine == "auto") {
+        // Estimated work: scan ~ M^2/2 * words * 2 / threads word ops;
+        // index ~ 3 * sum over blocks of (rows touching the block)^2.
+        double scan_cost = 0.5 * (double)M * (double)M * (double)P.words * 2.0 / nthreads;
+        std::vector<int64_t> per_block((size_t)P.nblk, 0);
+        for (int64_t i = 0; i < M; ++i) {
+            const uint64_t* q = P.row(i);
+            for (int64_t w = 0; w < P.words; ++w)
+                for (uint64_t b = q[w]; b; b &= b - 1) ++per_block[(size_t)(w * 64 + __builtin_ctzll(b))];
+        }
+        double index_cost = 0;
+        for (int64_t v : per_block) index_cost += 3.0 * (double)v * (double)v;
+        engine = (index_ok && index_cost < scan_cost) ? "index" : "scan";
+    }
+    if (engine == "index" && index_ok)
+        engine_index<I>(P, dist_thresh, perm);
+    else
+        engine_scan<I>(P, dist_thresh, perm, nthreads);
+}
+
+template void jaccard_clustering_host<int32_t>(int64_t, int64_t, const int32_t*, const int32_t*,
+                                               float, int64_t, int32_t*, int);
+template void jaccard_clustering_host<int64_t>(int64_t, int64_t, const int64_t*, const int64_t*,
+                                               float, int64_t, int64_t*, int);
+
+}  // namespace detail
+}  // namespace xspmm

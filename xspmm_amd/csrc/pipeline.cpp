@@ -1,0 +1,152 @@
+// pipeline.cpp -- Tier-2 automated pipeline on raw device pointers.
+//
+// Stage order, thresholds and timing fields follow the reference
+// (src/hip/unstructured_mtx_mul.hip:31-100):
+//   clustering on : cluster (host, threshold 0.5, width hw_block_size) ->
+//                   permute rows -> CSR->BCSR -> SpMM into C_temp ->
+//                   un-permute C_temp into C;
+//   clustering off: CSR->BCSR -> SpMM into C.
+// Every stage except clustering runs on the GPU.  Each timed stage is
+// bracketed by HIP events on the pipeline stream and waited for, so host work
+// inside a bracket counts too (the reference's HipTimer does the same).
+// Differences from the reference, with identical results: C / C_temp are not
+// memset first (the SpMM overwrites every element), temporaries come from the
+// stream-ordered pool instead of hipMalloc/hipFree, and permuted row_ptr[M]
+// is the sum of the gathered lengths (equal to nnz for a permutation).
+#include <vector>
+
+#include "internal.hpp"
+
+namespace xspmm {
+namespace detail {
+
+namespace {
+
+class StageTimer {
+public:
+    StageTimer(bool on, hipStream_t s) : on_(on), s_(s) {
+        if (on_) {
+            XSPMM_HIP_CHECK(hipEventCreate(&a_));
+            XSPMM_HIP_CHECK(hipEventCreate(&b_));
+        }
+    }
+    ~StageTimer() {
+        if (on_) {
+            (void)hipEventDestroy(a_);
+            (void)hipEventDestroy(b_);
+        }
+    }
+    void start() {
+        if (on_) XSPMM_HIP_CHECK(hipEventRecord(a_, s_));
+    }
+    void stop(double* out) {
+        if (!on_) return;
+        XSPMM_HIP_CHECK(hipEventRecord(b_, s_));
+        XSPMM_HIP_CHECK(hipEventSynchronize(b_));
+        float ms = 0.f;
+        XSPMM_HIP_CHECK(hipEventElapsedTime(&ms, a_, b_));
+        *out = (double)ms;
+    }
+
+private:
+    bool on_;
+    hipStream_t s_;
+    hipEvent_t a_ = nullptr, b_ = nullptr;
+};
+
+}  // namespace
+
+template <typename T, typename I>
+void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const T* vals,
+                   const T* B, float* C, int64_t N, int64_t hw, bool optimize_pattern,
+                   double* tm, hipStream_t s)
+{
+    if (M < 0 || K < 0 || nnz < 0 || N < 0)
+        throw std::invalid_argument("CSR dimensions must be non-negative.");
+    if (hw != 16)
+        throw std::invalid_argument("xSpMM: the MFMA tile kernel requires hw_block_size == 16.");
+    const bool timed = tm != nullptr;
+    StageTimer total(timed, s), step(timed, s);
+    total.start();
+    const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
+
+    if (optimize_pattern) {
+        // 1. Clustering (host).
+        step.start();
+        Scratch d_perm((size_t)(M > 0 ? M : 1) * sizeof(I), s);
+        if (M > 0) {
+            std::vector<I> h_rp((size_t)M + 1), h_ci((size_t)(nnz > 0 ? nnz : 1)), h_perm((size_t)M);
+            XSPMM_HIP_CHECK(hipMemcpyAsync(h_rp.data(), rp, sizeof(I) * (size_t)(M + 1),
+                                           hipMemcpyDeviceToHost, s));
+            if (nnz > 0)
+                XSPMM_HIP_CHECK(hipMemcpyAsync(h_ci.data(), ci, sizeof(I) * (size_t)nnz,
+                                               hipMemcpyDeviceToHost, s));
+            XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+            jaccard_clustering_host<I>(M, K, h_rp.data(), h_ci.data(), 0.5f, hw, h_perm.data(), 0);
+            XSPMM_HIP_CHECK(hipMemcpyAsync(d_perm.get(), h_perm.data(), sizeof(I) * (size_t)M,
+                                           hipMemcpyHostToDevice, s));
+            XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+        }
+        if (timed) step.stop(&tm[0]);
+
+        // 2. Permutation.
+        step.start();
+        Scratch nrp((size_t)(M + 1) * sizeof(I), s);
+        Scratch nci((size_t)(nnz > 0 ? nnz : 1) * sizeof(I), s);
+        Scratch nvals((size_t)(nnz > 0 ? nnz : 1) * sizeof(T), s);
+        apply_permutation<T, I>(M, nnz, rp, ci, vals, d_perm.as<I>(), nrp.as<I>(), nci.as<I>(),
+                                nvals.as<T>(), s);
+        if (timed) step.stop(&tm[1]);
+
+        // 3. Conversion.
+        step.start();
+        Scratch brp((size_t)(Mb + 1) * sizeof(I), s);
+        const int64_t nnzb = csr_to_bcsr_count<I>(M, K, nnz, nrp.as<I>(), nci.as<I>(), 16, 16,
+                                                  brp.as<I>(), s);
+        Scratch bci((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I), s);
+        Scratch bvals((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T), s);
+        csr_to_bcsr_fill<T, I>(M, K, nnz, nrp.as<I>(), nci.as<I>(), nvals.as<T>(), 16, 16,
+                               brp.as<I>(), bci.as<I>(), bvals.as<T>(), s);
+        if (timed) step.stop(&tm[2]);
+
+        // 4. SpMM into the permuted-order temporary.
+        Scratch c_tmp((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float), s);
+        step.start();
+        bcsr_spmm<T, I>(M, K, Mb, Kb, nnzb, brp.as<I>(), bci.as<I>(), bvals.as<T>(), B,
+                        c_tmp.as<float>(), N, s);
+        if (timed) step.stop(&tm[3]);
+
+        // 5. Un-permutation.
+        step.start();
+        unpermute_dense<I>(c_tmp.as<float>(), C, d_perm.as<I>(), M, N, s);
+        if (timed) step.stop(&tm[4]);
+    } else {
+        step.start();
+        Scratch brp((size_t)(Mb + 1) * sizeof(I), s);
+        const int64_t nnzb = csr_to_bcsr_count<I>(M, K, nnz, rp, ci, 16, 16, brp.as<I>(), s);
+        Scratch bci((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I), s);
+        Scratch bvals((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T), s);
+        csr_to_bcsr_fill<T, I>(M, K, nnz, rp, ci, vals, 16, 16, brp.as<I>(), bci.as<I>(),
+                               bvals.as<T>(), s);
+        if (timed) step.stop(&tm[2]);
+
+        step.start();
+        bcsr_spmm<T, I>(M, K, Mb, Kb, nnzb, brp.as<I>(), bci.as<I>(), bvals.as<T>(), B, C, N, s);
+        if (timed) step.stop(&tm[3]);
+    }
+    if (timed) total.stop(&tm[5]);
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+#define XSPMM_INST_PIPE(T, I)                                                                 \
+    template void spmm_pipeline<T, I>(int64_t, int64_t, int64_t, const I*, const I*, const T*, \
+                                      const T*, float*, int64_t, int64_t, bool, double*,       \
+                                      hipStream_t);
+XSPMM_INST_PIPE(uint16_t, int32_t)
+XSPMM_INST_PIPE(uint16_t, int64_t)
+XSPMM_INST_PIPE(float, int32_t)
+XSPMM_INST_PIPE(float, int64_t)
+#undef XSPMM_INST_PIPE
+
+}  // namespace detail
+}  // namespace xspmm
