@@ -7,8 +7,8 @@ from 1024 column-pattern templates, shuffled; B = 16384 x 128 fp16; C fp32.
 The Tier-2 preparation runs once, untimed by the step loop and reported
 separately: host Jaccard clustering (threshold 0.5, width 16) -> GPU row
 permutation -> GPU CSR->BCSR.  A step is one Tier-1 SpMM call
-C = A_bcsr * B on device-resident inputs (the B-panel repack and the MFMA
-tile kernel).  `value` is the effective throughput 2*nnz*N / t.
+C = A_bcsr * B on device-resident inputs (for fp16 one launch of the gather
+MFMA kernel).  `value` is the effective throughput 2*nnz*N / t.
 
 The JSON line also carries:
   roofline      algorithmic HBM bytes per call / measured call time vs 8 TB/s;
@@ -80,6 +80,19 @@ def cpu_baseline(p, N, nnz, seconds):
                   f"{t * 1e3:.1f} ms/call; BCSR tile product with fp32 accumulation "
                   f"(oracle/oracle.c xo_bcsr_spmm_f32)",
     }
+
+
+def tier1_kernel(value_bytes, K, N):
+    """Name of the kernel one Tier-1 call launches (the launcher's own rule in
+    xspmm_amd/csrc/spmm.hip: fp16 uses the gather kernel when N is even and B
+    and the block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL=panel)."""
+    if value_bytes == 4:
+        return "spmm_f32_kernel"
+    Kb = (K + 15) // 16
+    if (os.environ.get("XSPMM_SPMM_KERNEL", "") != "panel" and N % 2 == 0
+            and K * N * 2 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20):
+        return "spmm_f16_gather_kernel"
+    return "pack_b_panels + spmm_f16_kernel"
 
 
 def load_traffic(config):
@@ -165,11 +178,13 @@ def main():
     print(f"[bench] {args.steps} steps, {ms:.4f} ms/step", file=sys.stderr, flush=True)
 
     # spot check of C on sampled rows against an fp64 numpy product
+    # (C is in the permuted row order: its row r is row perm[r] of A * B)
     rows = np.random.default_rng(0).choice(M, size=min(256, M), replace=False)
     Ch = C.cpu().numpy()[rows].astype(np.float64)
     Bf = p.B.astype(np.float64)
     vf = p.vals.astype(np.float64)
-    ref = np.stack([vf[p.rp[r]:p.rp[r + 1]] @ Bf[p.ci[p.rp[r]:p.rp[r + 1]]] for r in rows])
+    src = perm[rows]
+    ref = np.stack([vf[p.rp[r]:p.rp[r + 1]] @ Bf[p.ci[p.rp[r]:p.rp[r + 1]]] for r in src])
     spot = float(np.linalg.norm(Ch - ref) / max(np.linalg.norm(ref), 1e-300))
 
     sT = p.vals.dtype.itemsize
@@ -216,7 +231,7 @@ def main():
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": load_traffic(args.config),
-            "kernel": "Tier-1 call: pack_b_panels + spmm_f16_kernel",
+            "kernel": tier1_kernel(sT, K, N),
             "alg_bytes_per_call": alg_bytes,
         },
         "padded_tflops": padded,

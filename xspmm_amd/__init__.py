@@ -21,7 +21,8 @@ from dataclasses import dataclass
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libxspmm.so")
+# XSPMM_LIBRARY selects another build of the library (same C ABI).
+LIB_PATH = os.environ.get("XSPMM_LIBRARY") or os.path.join(HERE, "libxspmm.so")
 
 F32, F16 = 0, 1
 I32, I64 = 0, 1

@@ -4,7 +4,7 @@
 // src/common/permutation.hpp:15-66): new row i = old row perm[i], entries of a
 // row keep their order.  Here the new row_ptr is a device scan of the gathered
 // row lengths (no separate lengths array, no host round trip), and the gather
-// is flattened: each workgroup owns 256 consecutive new rows, i.e. one
+// is flattened: each workgroup owns 32 consecutive new rows, i.e. one
 // contiguous output range, and every thread copies output entries, locating
 // its row by binary search over the workgroup's row starts held in LDS.
 // Writes are fully coalesced; reads are contiguous within each source row.
@@ -21,7 +21,7 @@ namespace detail {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerGroup = 256;
+constexpr int kRowsPerGroup = 32;
 
 template <typename I>
 struct PermutedRowLength {

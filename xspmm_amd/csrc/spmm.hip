@@ -23,6 +23,9 @@
 // Work split: one workgroup per block-row (grid.x), its waves own disjoint
 // groups of NTW 16-column tiles of C (grid.y covers wide N).  All waves of a
 // workgroup walk the same A blocks, which stay in the CU's L1.
+#include <cstdlib>
+#include <string>
+
 #include "internal.hpp"
 
 namespace xspmm {
@@ -140,6 +143,327 @@ __global__ __launch_bounds__(256) void spmm_f16_kernel(const I* __restrict__ brp
 }
 
 // ---------------------------------------------------------------------------
+// fp16 "gather" tile kernel: the default for fp16.
+//
+// A block usually touches far fewer than its 16 columns (0.7 % fill at the
+// headline configuration), and only the B rows of touched columns can change
+// C.  Per pair of blocks the wave therefore
+//   1. loads the A pair in MFMA operand layout (16 bytes per lane);
+//   2. forms the 32-bit slot mask of columns with a non-zero entry (each lane
+//      flags its non-zero halves, a 16-lane OR gives the mask of its k group);
+//   3. lists the masked slots in lane order (lane p ranks its bit and forwards
+//      p to lane rank) and computes every listed row's byte offset in B in
+//      its own lane;
+//   4. issues exactly F row loads (F masked rows; unused ones re-read row 0,
+//      further ones take a slower path), one dword per lane = two columns of
+//      its 128-column chunk -- a fixed count keeps the in-order load counter
+//      waits static, so rows stay in flight across pairs;
+//   5. transposes the rows through a per-wave LDS tile T[n][slot] into the
+//      MFMA B operand (one ds_read_b128 per 16x32 fragment) and clears the
+//      written slots again after the reads, so unmasked slots always hold
+//      zeros (stale data could be non-finite; A is zero there anyway);
+//   6. issues one v_mfma_f32_16x16x32_f16 per 16-column tile.
+// Every non-empty block still feeds an MFMA; what is skipped is the B traffic
+// of all-zero columns.  A runs three pairs ahead of the multiply and B rows
+// two.  On CDNA a wave64 VALU instruction holds the SIMD for four cycles, so
+// the per-pair bookkeeping is kept to a few dozen vector instructions.
+// The four waves of a workgroup split the block-row's pairs evenly (balancing
+// long rows) and their partial 16 x 128 tiles are summed in LDS.
+// grid = (block-rows, ceil(N / 128)); N even and B < 4 GiB on this path.
+// ---------------------------------------------------------------------------
+// Per-wave LDS tile: two sub-tiles (even / odd columns n = 2*lam, 2*lam+1)
+// of 64 rows x 16 dwords (32 slots).  The 16-byte chunk c of row lam sits at
+// chunk c ^ ((lam >> 2) & 3), and the odd sub-tile starts 8 banks after a
+// 64-bank boundary: the 16 lanes of a fragment read then hit 16 disjoint
+// 4-bank groups, and a row write (64 lanes, one slot) is 4-way.  8.2 KB per
+// wave, so four workgroups fit in the 160 KB of a CU.
+constexpr int kTileQ = 16;
+constexpr int kOddBase = 64 * kTileQ + 8;
+// dwords per wave, padded so every wave's tile starts on a 64-byte boundary
+constexpr int kTileWords = ((kOddBase + 64 * kTileQ + 15) / 16) * 16;
+// B row loads issued per pair (a pair's further masked rows take a slower
+// path).  At the headline configuration 98 % of pairs need at most 6 rows.
+#ifndef XSPMM_GATHER_ROWS
+#define XSPMM_GATHER_ROWS 6
+#endif
+constexpr int kGatherRows = XSPMM_GATHER_ROWS;
+
+typedef uint16_t ushort2_t __attribute__((ext_vector_type(2)));
+
+struct GatherA {
+    half8_t a;      // A operand of the pair (in flight)
+    uint32_t colv;  // block column of this lane's block (in flight)
+};
+
+template <int F>
+struct GatherRows {
+    half8_t a;
+    uint32_t mask;     // 32-bit slot mask (wave-uniform)
+    uint32_t cnt;      // masked slots (wave-uniform)
+    uint32_t slotv;    // lane r < cnt: (B row << 5) | slot of the pair's r-th masked row
+    uint32_t offv;     // lane r < cnt: byte offset of that row in B (else: past B)
+    uint32_t rows[F];  // B row r < F: columns n0+2*lane, n0+2*lane+1
+};
+
+// Buffer resource word 3 for raw (untyped, unswizzled) dword access on gfx9.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             kRawBufferWord3);
+}
+
+// Low dword of a block column; an int64 index with a non-zero high dword
+// reads as 0xffffffff (never a valid block column).
+template <typename I>
+__device__ __forceinline__ uint32_t load_block_col(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                   uint32_t soff)
+{
+    if constexpr (sizeof(I) == 4) {
+        return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+    } else {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+        return v.y == 0u ? v.x : 0xffffffffu;
+    }
+}
+
+template <typename I, int NT, int F>
+__global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restrict__ brp,
+                                                              const I* __restrict__ bci,
+                                                              const uint16_t* __restrict__ vals,
+                                                              const uint16_t* __restrict__ B,
+                                                              float* __restrict__ C, int64_t M,
+                                                              int64_t K, int64_t N, int64_t Kb)
+{
+    __shared__ __align__(16) uint32_t tiles[4 * kTileWords];
+    const int lane = threadIdx.x & (kWave - 1);
+    // wave-uniform (the compiler cannot infer it from threadIdx.x), so all
+    // block bookkeeping below stays in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    uint32_t* T = tiles + wave * kTileWords;
+
+    const int64_t br = blockIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * 128;
+    const int64_t rs = brp[br];
+    const int64_t re = brp[br + 1];
+    const int64_t npairs = (re - rs + 1) >> 1;
+    const int64_t q0 = npairs * wave / 4;
+    const int64_t q1 = npairs * (wave + 1) / 4;
+
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int sel = lane >> 5;
+    const int kh = g & 1;
+
+    // --- loop-invariant quantities ------------------------------------------
+    // This wave's blocks [wb0, wb1) are read through buffer resources: a read
+    // past them (the missing second block of an odd row, the pairs after q1
+    // that the software pipeline runs into) returns zeros, which give an empty
+    // slot mask.  Pair q sits at byte (q - q0) * 1024 of the A resource.  All
+    // offsets go into the per-lane offset operand, which the range check
+    // covers.
+    const int64_t wb0 = rs + 2 * q0;
+    const int64_t wb1 = (rs + 2 * q1 < re) ? rs + 2 * q1 : re;
+    const uint32_t nblk = (uint32_t)(wb1 > wb0 ? wb1 - wb0 : 0);
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + wb0 * 256, nblk * 512u);
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(bci + wb0, nblk * (uint32_t)sizeof(I));
+    // B: K * N * 2 <= 2^31 on this path, so an offset of b_bytes plus a lane
+    // offset neither wraps nor lands inside B: rows at that offset read as zero
+    // without touching memory.
+    const uint32_t b_bytes = (uint32_t)(K * N * 2);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
+    // A operand: block (lane >> 5) of the pair, row li, halves 8*kh .. +8
+    const uint32_t a_voff = (uint32_t)(sel * 512 + li * 32 + kh * 16);
+    const uint32_t c_voff = (uint32_t)(sel * sizeof(I));
+    // B rows: this lane reads columns n0 + 2*lane and +1 as one dword.  Past N
+    // the offset is clamped into the row: such elements land in tile columns
+    // >= N, which are never stored.
+    const uint32_t lane_off =
+        (uint32_t)(2 * ((n0 + 2 * lane + 1 < N) ? n0 + 2 * lane : N - 2));
+    const uint32_t rowbytes = (uint32_t)(2 * N);  // < 2^23 on this path
+    // slot listing: lane p < 32 owns mask bit p, i.e. column p & 15 of block
+    // (p >> 4) of the pair, and sends ((16 * block column + (p & 15)) << 5) | p
+    const uint32_t p_bit = (uint32_t)lane & 31u;
+    const uint32_t below_p = (1u << p_bit) - 1u;
+    const uint32_t p_code = ((p_bit & 15u) << 5) | p_bit;
+    const bool p_hi = (p_bit & 16u) != 0u;
+    // LDS tile: slot s of this lane's even row is at byte lane_base ^ (2 * s)
+    // of the workgroup's tiles, i.e. chunk (s >> 3) ^ swizzle, half s & 7 of
+    // row lane (the wave's tile starts on a 64-byte boundary).
+    const uint32_t lane_base = 4u * (uint32_t)(wave * kTileWords) + 64u * (uint32_t)lane +
+                               16u * (uint32_t)((lane >> 2) & 3);
+    constexpr uint32_t kOddDelta = 4 * kOddBase;
+    char* const Lc = reinterpret_cast<char*>(tiles);
+    char* const Tc = reinterpret_cast<char*>(T);
+    // fragment j of this lane: row lam = 8j + li/2 of the even/odd sub-tile,
+    // chunk g (swizzled)
+    uint32_t frag_off[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int lam = 8 * j + (li >> 1);
+        frag_off[j] = 4u * (uint32_t)(((li & 1) ? kOddBase : 0) + lam * kTileQ +
+                                      4 * ((g ^ (lam >> 2)) & 3));
+    }
+    // 0x00010001, hidden from the optimiser: min(x, one) on the two halves
+    // then stays one packed integer instruction instead of two compares
+    uint32_t one;
+    asm("s_mov_b32 %0, 0x10001" : "=s"(one));
+    const uint32_t kb32 = (uint32_t)Kb;  // < 2^20 on this path: B rows < 2^24
+
+    // the tile starts (and, after every pair, returns to) all zeros
+    for (int w = lane; w < kTileWords / 4; w += kWave)
+        reinterpret_cast<u32x4_t*>(T)[w] = u32x4_t{0u, 0u, 0u, 0u};
+
+    float4_t acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Stage A: issue the loads of pair q's A operand and block columns.
+    auto stage_a = [&](int64_t q, GatherA& P) {
+        const uint32_t pq = (uint32_t)(q - q0);
+        P.a = __builtin_bit_cast(
+            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, 0));
+        P.colv = load_block_col<I>(c_rsrc, c_voff + pq * 2u * (uint32_t)sizeof(I), 0u);
+    };
+    // Stage R: mask, listed slots, row offsets, then the F row loads.
+    auto stage_rows = [&](const GatherA& P, GatherRows<F>& R) {
+        const uint32_t c0 = (uint32_t)__builtin_amdgcn_readlane((int)P.colv, 0);
+        const uint32_t c1 = (uint32_t)__builtin_amdgcn_readlane((int)P.colv, 32);
+        R.a = P.a;
+        const u32x4_t w = __builtin_bit_cast(u32x4_t, R.a);
+        // per 16-bit half: 1 if |x| != 0
+        uint32_t nz[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const ushort2_t h = __builtin_bit_cast(ushort2_t, w[d] & 0x7fff7fffu);
+            nz[d] = __builtin_bit_cast(
+                uint32_t, __builtin_elementwise_min(h, __builtin_bit_cast(ushort2_t, one)));
+        }
+        // element e = 2d (+1 for the high half) -> bit e
+        uint32_t v = nz[0] | (nz[1] << 2) | (nz[2] << 4) | (nz[3] << 6);
+        v = (v | (v >> 15)) & 0xffu;
+        // OR over the 16 lanes of the k group: DPP row rotations by 1, 2, 4, 8
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+        // a block column past Kb (malformed input) lists no rows: its block
+        // meets only zero slots
+        const uint32_t valid = (c0 < kb32 ? 0x0000ffffu : 0u) | (c1 < kb32 ? 0xffff0000u : 0u);
+        const uint32_t m = ((uint32_t)__builtin_amdgcn_readlane((int)v, 0) |
+                            ((uint32_t)__builtin_amdgcn_readlane((int)v, 16) << 8) |
+                            ((uint32_t)__builtin_amdgcn_readlane((int)v, 32) << 16) |
+                            ((uint32_t)__builtin_amdgcn_readlane((int)v, 48) << 24)) &
+                           valid;
+        R.mask = m;
+        R.cnt = (uint32_t)__builtin_popcount(m);
+        const bool send = lane < 32 && ((m >> p_bit) & 1u);
+        const uint32_t rank = (uint32_t)__builtin_popcount(m & below_p);
+        const uint32_t code = ((p_hi ? c1 : c0) << 9) + p_code;
+        // lanes with nothing to send all target lane 63, which is never read
+        const uint32_t sv =
+            (uint32_t)__builtin_amdgcn_ds_permute((int)((send ? rank : 63u) * 4u), (int)code);
+        R.slotv = sv;
+        // rows of a malformed block that run past K read zeros
+        R.offv = ((uint32_t)lane < R.cnt) ? __umul24(sv >> 5, rowbytes) : b_bytes;
+#pragma unroll
+        for (int r = 0; r < F; ++r)
+            R.rows[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                b_rsrc, (int)(lane_off + (uint32_t)__builtin_amdgcn_readlane((int)R.offv, r)), 0, 0);
+    };
+    auto put = [&](uint32_t addr, uint32_t r) {
+        *reinterpret_cast<uint16_t*>(Lc + addr) = (uint16_t)(r & 0xffffu);
+        *reinterpret_cast<uint16_t*>(Lc + addr + kOddDelta) = (uint16_t)(r >> 16);
+    };
+    auto slot_addr = [&](const GatherRows<F>& R, int r) -> uint32_t {
+        return lane_base ^ (2u * ((uint32_t)__builtin_amdgcn_readlane((int)R.slotv, r) & 31u));
+    };
+    // Stage M: rows into the tile, fragments out, multiply, clear the slots.
+    auto stage_mma = [&](const GatherRows<F>& R) {
+        if (R.mask == 0u) return;
+        uint32_t addr[F];
+#pragma unroll
+        for (int r = 0; r < F; ++r) {
+            addr[r] = slot_addr(R, r);
+            if ((uint32_t)r < R.cnt) put(addr[r], R.rows[r]);
+        }
+        for (uint32_t r = F; r < R.cnt; ++r)  // rare: more than F rows
+            put(slot_addr(R, (int)r),
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    b_rsrc,
+                    (int)(lane_off + (uint32_t)__builtin_amdgcn_readlane((int)R.offv, (int)r)), 0,
+                    0));
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(Tc + frag_off[j]);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(R.a, __builtin_bit_cast(half8_t, raw),
+                                                           acc[j], 0, 0, 0);
+        }
+        // LDS executes a wave's operations in order: these clears land after
+        // the fragment reads above.
+#pragma unroll
+        for (int r = 0; r < F; ++r)
+            if ((uint32_t)r < R.cnt) put(addr[r], 0u);
+        for (uint32_t r = F; r < R.cnt; ++r) put(slot_addr(R, (int)r), 0u);
+    };
+
+    if (q0 < q1) {
+        // A (and block columns) run three pairs ahead of the multiply, B rows
+        // two pairs ahead.  Pairs past q1 are empty and cost no row traffic.
+        GatherA A0, A1, A2;
+        GatherRows<F> X, Y, Z;
+        stage_a(q0, A0);
+        stage_a(q0 + 1, A1);
+        stage_a(q0 + 2, A2);
+        stage_rows(A0, X);
+        stage_rows(A1, Y);
+        for (int64_t q = q0; q < q1; q += 3) {
+            stage_a(q + 3, A0);
+            stage_mma(X);
+            stage_rows(A2, Z);
+            stage_a(q + 4, A1);
+            stage_mma(Y);
+            stage_rows(A0, X);
+            stage_a(q + 5, A2);
+            stage_mma(Z);
+            stage_rows(A1, Y);
+        }
+    }
+
+    // Sum the four waves' partial tiles through LDS and store C.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(tiles);  // 4 x [16][128] fp32 = 32 KB
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave * 2048 + (4 * g + r) * 128 + 16 * j + li] = acc[j][r];
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int row = t >> 4;
+    const int c0 = (t & 15) * 8;
+    const int64_t grow = br * 16 + row;
+    if (grow < M && c0 < NT * 16) {
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int o = row * 128 + c0 + e;
+            out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
+        }
+        float* dst = C + grow * N + n0 + c0;
+        if (n0 + c0 + 8 <= N && (N & 3) == 0) {
+            *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (n0 + c0 + e < N) dst[e] = out[e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 x fp32 -> fp32 tile kernel.
 // ---------------------------------------------------------------------------
 template <typename I, int NTW>
@@ -214,6 +538,20 @@ Geometry pick_geometry(int ntiles)
     return g;
 }
 
+// fp16 kernel family: "gather" (masked B-row gather, default for even N) or
+// "panel" (whole 16-row B panels from a repacked copy of B; odd N).
+// XSPMM_SPMM_KERNEL=panel forces the panel kernel.
+enum class Fp16Kernel { kGather, kPanel };
+
+Fp16Kernel fp16_kernel_choice()
+{
+    static const Fp16Kernel k = [] {
+        const char* e = std::getenv("XSPMM_SPMM_KERNEL");
+        return (e && std::string(e) == "panel") ? Fp16Kernel::kPanel : Fp16Kernel::kGather;
+    }();
+    return k;
+}
+
 void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N)
 {
     if (M < 0 || K < 0 || Mb < 0 || Kb < 0 || nnzb < 0 || N < 0)
@@ -240,17 +578,33 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
     const dim3 block(geo.waves * kWave);
 
     if constexpr (sizeof(T) == 2) {
+        const uint16_t* v = reinterpret_cast<const uint16_t*>(bvals);
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(B);
+        // gather path: byte offsets into B, and a wave's A range, fit 32 bits
+        if (fp16_kernel_choice() == Fp16Kernel::kGather && N % 2 == 0 &&
+            K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
+            Kb < (int64_t(1) << 20)) {
+            const int64_t chunks = (N + 127) / 128;
+            if (chunks > 65535) throw std::invalid_argument("xSpMM: N too large.");
+            const dim3 ggrid((unsigned)Mb, (unsigned)chunks);
+            if (N <= 64)
+                hipLaunchKernelGGL((spmm_f16_gather_kernel<I, 4, kGatherRows>), ggrid, dim3(256), 0, s, brp, bci,
+                                   v, b, C, M, K, N, Kb);
+            else
+                hipLaunchKernelGGL((spmm_f16_gather_kernel<I, 8, kGatherRows>), ggrid, dim3(256), 0, s, brp, bci,
+                                   v, b, C, M, K, N, Kb);
+            XSPMM_LAUNCH_CHECK();
+            return;
+        }
         const int64_t Np = ntiles64 * 16;
         Scratch bt((size_t)(Kb > 0 ? Kb : 1) * (size_t)Np * 16 * sizeof(uint16_t), s);
         if (Kb > 0) {
             const int64_t per_kb = Np * 2;
             const dim3 pg((unsigned)((per_kb + 255) / 256), (unsigned)(Kb < 65535 ? Kb : 65535));
-            hipLaunchKernelGGL(pack_b_panels, pg, dim3(256), 0, s,
-                               reinterpret_cast<const uint16_t*>(B), bt.as<uint16_t>(), K, N, Kb,
+            hipLaunchKernelGGL(pack_b_panels, pg, dim3(256), 0, s, b, bt.as<uint16_t>(), K, N, Kb,
                                Np);
             XSPMM_LAUNCH_CHECK();
         }
-        const uint16_t* v = reinterpret_cast<const uint16_t*>(bvals);
         switch (geo.ntw) {
         case 4:
             hipLaunchKernelGGL((spmm_f16_kernel<I, 4>), grid, block, 0, s, brp, bci, v,
