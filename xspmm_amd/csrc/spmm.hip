@@ -464,6 +464,276 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
 }
 
 // ---------------------------------------------------------------------------
+// fp16 "column batch" tile kernel.
+//
+// All blocks of a block-row add into the same 16 rows of C, so the K extent
+// of a multiply does not have to follow block boundaries: the non-zero
+// columns of any blocks of the row can be stacked into one K = 32 operand.
+// Each wave streams its share of the row's block pairs and
+//   1. loads a pair in MFMA A-operand layout (16 bytes per lane), four pairs
+//      ahead of use;
+//   2. forms the pair's 32-bit mask of columns holding a non-zero (per-lane
+//      8-bit masks OR-ed over the 16 lanes of a k group by DPP);
+//   3. appends the masked columns to a batch of 32 K slots: the 16 values of
+//      each column go to A'[row][slot] in LDS (written by the 16 lanes that
+//      hold them, zeros included, so slots never need clearing) and the
+//      column's B row index to a slot list;
+//   4. when a pair does not fit the batch, starts the batch: reads its A'
+//      operand and issues the 16-byte loads of its 32 B rows (unused slots
+//      get an out-of-range offset, which reads zeros without touching memory);
+//   5. one batch later (so the row loads have long arrived) writes those rows
+//      row-major into an LDS tile, reads them back with the gfx950 transpose
+//      read ds_read_b64_tr_b16 as MFMA B operands and issues one
+//      v_mfma_f32_16x16x32_f16 per 16-column tile.
+// Every masked column of every block goes through an MFMA; columns that are
+// zero in all 16 rows of a block are skipped, as they add exact zeros.
+// The four waves of a workgroup split the row's pairs evenly and their
+// partial tiles are summed in LDS.  grid = (block-rows, ceil(N / 128));
+// N % 8 == 0 and K * N * 2 <= 2^31 on this path.
+//
+// Per-wave LDS: B' tile 32 rows x 256 B (16-byte chunk c of row e stored at
+// chunk c ^ swz(e), which spreads the 16 rows one transpose read touches over
+// all banks), A' 16 rows x 80 B (32 slots + pad), slot list 32 x 4 B.
+// ---------------------------------------------------------------------------
+constexpr int kBtRow = 256;
+constexpr int kBtBytes = 32 * kBtRow;
+constexpr int kApStride = 80;
+constexpr int kApOff = kBtBytes;
+constexpr int kSlotOff = kApOff + 16 * kApStride;
+constexpr int kBatchWaveLds = kSlotOff + 32 * 4;
+constexpr int kBatchDepth = 4;  // A pairs in flight per wave
+
+// swizzle of row e: even values 0..14, each used by two of the 16 rows a
+// transpose read touches
+__device__ __forceinline__ uint32_t bt_swz(uint32_t e)
+{
+    return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+template <typename I, int NT>
+__global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict__ brp,
+                                                             const I* __restrict__ bci,
+                                                             const uint16_t* __restrict__ vals,
+                                                             const uint16_t* __restrict__ B,
+                                                             float* __restrict__ C, int64_t M,
+                                                             int64_t K, int64_t N, int64_t Kb)
+{
+    static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
+    constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
+    constexpr int RPL = 64 / CPR;  // B rows per load instruction
+    __shared__ __align__(16) unsigned char smem[4 * kBatchWaveLds];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    unsigned char* const W = smem + wave * kBatchWaveLds;
+
+    const int64_t br = blockIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * 128;
+    const int64_t rs = brp[br];
+    const int64_t re = brp[br + 1];
+    const int64_t npairs = (re - rs + 1) >> 1;
+    const int64_t q0 = npairs * wave / 4;
+    const int64_t q1 = npairs * (wave + 1) / 4;
+
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int sel = lane >> 5;
+    const int kh = g & 1;
+
+    // --- buffer resources (reads past them return zeros) ---------------------
+    const int64_t wb0 = rs + 2 * q0;
+    const int64_t wb1 = (rs + 2 * q1 < re) ? rs + 2 * q1 : re;
+    const uint32_t nblk = (uint32_t)(wb1 > wb0 ? wb1 - wb0 : 0);
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + wb0 * 256, nblk * 512u);
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(bci + wb0, nblk * (uint32_t)sizeof(I));
+    const uint32_t b_bytes = (uint32_t)(K * N * 2);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
+    const uint32_t a_voff = (uint32_t)(sel * 512 + li * 32 + kh * 16);
+    const uint32_t c_voff = (uint32_t)(sel * sizeof(I));
+    const uint32_t kb32 = (uint32_t)Kb;
+    const uint32_t k32 = (uint32_t)K;
+    const uint32_t rowbytes = (uint32_t)(2 * N);
+
+    // --- per-lane constants --------------------------------------------------
+    // A' slot writes: row li, byte li * kApStride + 2 * slot
+    const uint32_t ap_row = (uint32_t)(kApOff + li * kApStride);
+    // groups below this lane's group in the 32-bit pair mask
+    const uint32_t below_group = (1u << (8 * g)) - 1u;
+    // B row loads: load t moves row t * RPL + lane / CPR, chunk lane % CPR
+    const uint32_t ld_c = (uint32_t)(lane % CPR);
+    const uint32_t ld_r = (uint32_t)(lane / CPR);
+    const uint32_t ld_off = (uint32_t)(2 * n0) + 16u * ld_c;
+    // transpose reads: row 8g + 4h + (li >> 2), 8-byte piece of chunk
+    // 2j + ((li & 3) >> 1), byte 8 * (li & 1) within the chunk
+    const uint32_t tr_e0 = (uint32_t)(8 * g + (li >> 2));
+    const uint32_t tr_e1 = tr_e0 + 4u;
+    const uint32_t tr_base0 = tr_e0 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
+    const uint32_t tr_base1 = tr_e1 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
+    const uint32_t tr_swz0 = bt_swz(tr_e0);
+    const uint32_t tr_swz1 = bt_swz(tr_e1);
+
+    // A' starts as zeros: a partial batch multiplies its unused slots (B rows
+    // read as zeros) and uninitialised LDS could hold non-finite bit patterns.
+    // Later batches leave finite values from earlier batches there.
+    for (int i = lane; i < 16 * kApStride / 4; i += kWave)
+        reinterpret_cast<uint32_t*>(W + kApOff)[i] = 0u;
+
+    float4_t acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    u32x4_t bv[NT];      // B rows of the started batch (in flight)
+    half8_t aop{};       // A' operand of the started batch
+    bool started = false;
+    uint32_t pending = 0;  // slots filled in the open batch (wave-uniform)
+
+    // Multiply the started batch: rows into the tile, transpose reads, MFMA.
+    auto finish = [&]() {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+            *reinterpret_cast<u32x4_t*>(W + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[t];
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_short4_t*)(W + tr_base0 + (((uint32_t)(2 * j) ^ tr_swz0) << 4)));
+            const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_short4_t*)(W + tr_base1 + (((uint32_t)(2 * j) ^ tr_swz1) << 4)));
+            const half8_t bop = __builtin_bit_cast(
+                half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
+        }
+    };
+    // Close the open batch of `cnt` slots: multiply the previous one, then
+    // read this one's A' operand and issue its row loads.
+    auto start = [&](uint32_t cnt) {
+        if (started) finish();
+        aop = __builtin_bit_cast(half8_t,
+                                 *reinterpret_cast<const u32x4_t*>(W + ap_row + 16u * (uint32_t)g));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+            const uint32_t row = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * e);
+            const uint32_t off = (e < cnt && row < k32) ? __umul24(row, rowbytes) + ld_off
+                                                        : b_bytes + ld_off;
+            bv[t] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+        }
+        started = true;
+    };
+
+    auto stage_a = [&](int64_t q, GatherA& P) {
+        const uint32_t pq = (uint32_t)(q - q0);
+        P.a = __builtin_bit_cast(
+            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, 0));
+        P.colv = load_block_col<I>(c_rsrc, c_voff + pq * 2u * (uint32_t)sizeof(I), 0u);
+    };
+
+    auto process = [&](const GatherA& P) {
+        const uint32_t c0 = (uint32_t)__builtin_amdgcn_readlane((int)P.colv, 0);
+        const uint32_t c1 = (uint32_t)__builtin_amdgcn_readlane((int)P.colv, 32);
+        const u32x4_t w = __builtin_bit_cast(u32x4_t, P.a);
+        // bit e: half e of this lane's 8 is non-zero (a -0.0 counts as an
+        // entry; it adds an exact zero).  Plain compares: hipcc 7.2 folds the
+        // packed-min form (min(halves, {1, 1})) in this loop into a test of
+        // the first dword only.
+        uint32_t v = 0u;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            v |= ((w[d] & 0xffffu) != 0u ? 1u : 0u) << (2 * d);
+            v |= ((w[d] >> 16) != 0u ? 1u : 0u) << (2 * d + 1);
+        }
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+        // a block column outside the grid (malformed input) contributes nothing
+        const uint32_t valid = (c0 < kb32 ? 0x0000ffffu : 0u) | (c1 < kb32 ? 0xffff0000u : 0u);
+        const uint32_t pm = ((uint32_t)__builtin_amdgcn_readlane((int)v, 0) |
+                             ((uint32_t)__builtin_amdgcn_readlane((int)v, 16) << 8) |
+                             ((uint32_t)__builtin_amdgcn_readlane((int)v, 32) << 16) |
+                             ((uint32_t)__builtin_amdgcn_readlane((int)v, 48) << 24)) &
+                            valid;
+        if (pm == 0u) return;
+        const uint32_t cnt = (uint32_t)__builtin_popcount(pm);
+        if (pending + cnt > 32u) {
+            start(pending);
+            pending = 0;
+        }
+        // this lane's group: its columns take consecutive slots from `base`
+        uint32_t rem = (pm >> (8 * g)) & 0xffu;
+        const uint32_t base = pending + (uint32_t)__builtin_popcount(pm & below_group);
+        const uint32_t colbase = 16u * (sel ? c1 : c0) + 8u * (uint32_t)kh;
+        uint32_t slot = base;
+        do {
+            if (rem != 0u) {
+                const uint32_t b = (uint32_t)__builtin_ctz(rem);
+                rem &= rem - 1u;
+                const uint32_t word = (b & 4u) ? ((b & 2u) ? w[3] : w[2]) : ((b & 2u) ? w[1] : w[0]);
+                const uint16_t val = (uint16_t)(word >> ((b & 1u) << 4));
+                *reinterpret_cast<uint16_t*>(W + ap_row + 2u * slot) = val;
+                if (li == 0) *reinterpret_cast<uint32_t*>(W + kSlotOff + 4u * slot) = colbase + b;
+                ++slot;
+            }
+        } while (__builtin_amdgcn_ballot_w64(rem != 0u) != 0);
+        pending += cnt;
+    };
+
+    if (q0 < q1) {
+        GatherA P0, P1, P2, P3;
+        stage_a(q0, P0);
+        stage_a(q0 + 1, P1);
+        stage_a(q0 + 2, P2);
+        stage_a(q0 + 3, P3);
+        for (int64_t q = q0; q < q1; q += kBatchDepth) {
+            process(P0);
+            stage_a(q + 4, P0);
+            process(P1);
+            stage_a(q + 5, P1);
+            process(P2);
+            stage_a(q + 6, P2);
+            process(P3);
+            stage_a(q + 7, P3);
+        }
+        if (pending > 0u) start(pending);
+        if (started) finish();
+    }
+
+    // Sum the four waves' partial tiles through LDS and store C.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);  // 4 x [16][128] fp32 = 32 KB
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave * 2048 + (4 * g + r) * 128 + 16 * j + li] = acc[j][r];
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int row = t >> 4;
+    const int c0 = (t & 15) * 8;
+    const int64_t grow = br * 16 + row;
+    if (grow < M && c0 < NT * 16) {
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int o = row * 128 + c0 + e;
+            out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
+        }
+        float* dst = C + grow * N + n0 + c0;
+        if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
+            *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (n0 + c0 + e < N) dst[e] = out[e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 x fp32 -> fp32 tile kernel.
 // ---------------------------------------------------------------------------
 template <typename I, int NTW>
@@ -538,16 +808,22 @@ Geometry pick_geometry(int ntiles)
     return g;
 }
 
-// fp16 kernel family: "gather" (masked B-row gather, default for even N) or
-// "panel" (whole 16-row B panels from a repacked copy of B; odd N).
-// XSPMM_SPMM_KERNEL=panel forces the panel kernel.
-enum class Fp16Kernel { kGather, kPanel };
+// fp16 kernel family: "batch" (column batches, default where N % 8 == 0),
+// "gather" (per-pair masked B-row gather) or "panel" (whole 16-row B panels
+// from a repacked copy of B; any N).  XSPMM_SPMM_KERNEL=batch|gather|panel
+// forces one where its shape conditions hold.
+enum class Fp16Kernel { kAuto, kBatch, kGather, kPanel };
 
 Fp16Kernel fp16_kernel_choice()
 {
     static const Fp16Kernel k = [] {
         const char* e = std::getenv("XSPMM_SPMM_KERNEL");
-        return (e && std::string(e) == "panel") ? Fp16Kernel::kPanel : Fp16Kernel::kGather;
+        if (!e) return Fp16Kernel::kAuto;
+        const std::string v(e);
+        if (v == "panel") return Fp16Kernel::kPanel;
+        if (v == "gather") return Fp16Kernel::kGather;
+        if (v == "batch") return Fp16Kernel::kBatch;
+        return Fp16Kernel::kAuto;
     }();
     return k;
 }
@@ -580,13 +856,32 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
     if constexpr (sizeof(T) == 2) {
         const uint16_t* v = reinterpret_cast<const uint16_t*>(bvals);
         const uint16_t* b = reinterpret_cast<const uint16_t*>(B);
-        // gather path: byte offsets into B, and a wave's A range, fit 32 bits
-        if (fp16_kernel_choice() == Fp16Kernel::kGather && N % 2 == 0 &&
-            K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
-            Kb < (int64_t(1) << 20)) {
-            const int64_t chunks = (N + 127) / 128;
-            if (chunks > 65535) throw std::invalid_argument("xSpMM: N too large.");
-            const dim3 ggrid((unsigned)Mb, (unsigned)chunks);
+        // batch and gather paths: byte offsets into B, and a wave's A range,
+        // fit 32 bits; B row indices fit 24 bits
+        const Fp16Kernel choice = fp16_kernel_choice();
+        const bool offsets32 = K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
+                               Kb < (int64_t(1) << 20);
+        const int64_t chunks = (N + 127) / 128;
+        if (chunks > 65535) throw std::invalid_argument("xSpMM: N too large.");
+        const dim3 ggrid((unsigned)Mb, (unsigned)chunks);
+        if ((choice == Fp16Kernel::kAuto || choice == Fp16Kernel::kBatch) && N % 8 == 0 &&
+            offsets32) {
+            if (N <= 16)
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
+                                   v, b, C, M, K, N, Kb);
+            else if (N <= 32)
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
+                                   v, b, C, M, K, N, Kb);
+            else if (N <= 64)
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
+                                   v, b, C, M, K, N, Kb);
+            else
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
+                                   v, b, C, M, K, N, Kb);
+            XSPMM_LAUNCH_CHECK();
+            return;
+        }
+        if (choice == Fp16Kernel::kGather && N % 2 == 0 && offsets32) {
             if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_gather_kernel<I, 4, kGatherRows>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb);
