@@ -205,6 +205,9 @@ struct GatherRows {
     uint32_t rows[F];  // B row r < F: columns n0+2*lane, n0+2*lane+1
 };
 
+// Cache-policy operand of the buffer-load builtins: non-temporal (nt).
+constexpr int kNonTemporal = 2;
+
 // Buffer resource word 3 for raw (untyped, unswizzled) dword access on gfx9.
 constexpr int kRawBufferWord3 = 0x00020000;
 
@@ -487,7 +490,7 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
 //      v_mfma_f32_16x16x32_f16 per 16-column tile.
 // Every masked column of every block goes through an MFMA; columns that are
 // zero in all 16 rows of a block are skipped, as they add exact zeros.
-// The four waves of a workgroup split the row's pairs evenly and their
+// The four waves of a workgroup take the row's pairs in turn and their
 // partial tiles are summed in LDS.  grid = (block-rows, ceil(N / 128));
 // N % 8 == 0 and K * N * 2 <= 2^31 on this path.
 //
@@ -501,7 +504,14 @@ constexpr int kApStride = 80;
 constexpr int kApOff = kBtBytes;
 constexpr int kSlotOff = kApOff + 16 * kApStride;
 constexpr int kBatchWaveLds = kSlotOff + 32 * 4;
-constexpr int kBatchDepth = 4;  // A pairs in flight per wave
+#ifndef XSPMM_BATCH_DEPTH
+#define XSPMM_BATCH_DEPTH 5
+#endif
+#ifndef XSPMM_BATCH_MIN_WAVES
+#define XSPMM_BATCH_MIN_WAVES 1
+#endif
+constexpr int kBatchDepth = XSPMM_BATCH_DEPTH;  // A pairs in flight per wave (4..6)
+static_assert(kBatchDepth >= 4 && kBatchDepth <= 6, "batch depth must be 4, 5 or 6");
 
 // swizzle of row e: even values 0..14, each used by two of the 16 rows a
 // transpose read touches
@@ -510,11 +520,25 @@ __device__ __forceinline__ uint32_t bt_swz(uint32_t e)
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
 }
 
+struct BatchA {
+    half8_t a;    // A operand of the pair (in flight)
+    uint32_t c0;  // block columns of its two blocks (wave-uniform)
+    uint32_t c1;
+};
+
+// Low dword of a block column read with a wave-uniform address; an int64
+// index with a non-zero high dword becomes 0xffffffff (never a valid column).
+__device__ __forceinline__ uint32_t block_col_scalar(int32_t c) { return (uint32_t)c; }
+__device__ __forceinline__ uint32_t block_col_scalar(int64_t c)
+{
+    return ((uint64_t)c >> 32) == 0u ? (uint32_t)c : 0xffffffffu;
+}
+
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 template <typename I, int NT>
-__global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict__ brp,
+__global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_kernel(const I* __restrict__ brp,
                                                              const I* __restrict__ bci,
                                                              const uint16_t* __restrict__ vals,
                                                              const uint16_t* __restrict__ B,
@@ -534,8 +558,6 @@ __global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict
     const int64_t rs = brp[br];
     const int64_t re = brp[br + 1];
     const int64_t npairs = (re - rs + 1) >> 1;
-    const int64_t q0 = npairs * wave / 4;
-    const int64_t q1 = npairs * (wave + 1) / 4;
 
     const int li = lane & 15;
     const int g = lane >> 4;
@@ -543,15 +565,14 @@ __global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict
     const int kh = g & 1;
 
     // --- buffer resources (reads past them return zeros) ---------------------
-    const int64_t wb0 = rs + 2 * q0;
-    const int64_t wb1 = (rs + 2 * q1 < re) ? rs + 2 * q1 : re;
-    const uint32_t nblk = (uint32_t)(wb1 > wb0 ? wb1 - wb0 : 0);
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + wb0 * 256, nblk * 512u);
-    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(bci + wb0, nblk * (uint32_t)sizeof(I));
+    // The four waves take the row's pairs in turn (wave w: pairs w, w + 4,
+    // ...), so the workgroup reads the row front to back.  A is read with the
+    // non-temporal hint: it is used once and should not push B out of L2.
+    const uint32_t nblk = (uint32_t)(re - rs);
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + rs * 256, nblk * 512u);
     const uint32_t b_bytes = (uint32_t)(K * N * 2);
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
     const uint32_t a_voff = (uint32_t)(sel * 512 + li * 32 + kh * 16);
-    const uint32_t c_voff = (uint32_t)(sel * sizeof(I));
     const uint32_t kb32 = (uint32_t)Kb;
     const uint32_t k32 = (uint32_t)K;
     const uint32_t rowbytes = (uint32_t)(2 * N);
@@ -568,11 +589,14 @@ __global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict
     // transpose reads: row 8g + 4h + (li >> 2), 8-byte piece of chunk
     // 2j + ((li & 3) >> 1), byte 8 * (li & 1) within the chunk
     const uint32_t tr_e0 = (uint32_t)(8 * g + (li >> 2));
-    const uint32_t tr_e1 = tr_e0 + 4u;
-    const uint32_t tr_base0 = tr_e0 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
-    const uint32_t tr_base1 = tr_e1 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
-    const uint32_t tr_swz0 = bt_swz(tr_e0);
-    const uint32_t tr_swz1 = bt_swz(tr_e1);
+    // rows e and e + 4 share the swizzle (e & 4 == 0 here), so the second
+    // read of a tile sits 4 rows (1 KB) after the first
+    const uint32_t tr_base = tr_e0 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
+    const uint32_t tr_swz16 = bt_swz(tr_e0) << 4;
+    // 0x00010001 from an SGPR the optimiser cannot see through, so
+    // min(halves, one) stays a single packed integer instruction
+    uint32_t one;
+    asm("s_mov_b32 %0, 0x10001" : "=s"(one));
 
     // A' starts as zeros: a partial batch multiplies its unused slots (B rows
     // read as zeros) and uninitialised LDS could hold non-finite bit patterns.
@@ -598,10 +622,10 @@ __global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict
         }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_short4_t*)(W + tr_base0 + (((uint32_t)(2 * j) ^ tr_swz0) << 4)));
-            const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_short4_t*)(W + tr_base1 + (((uint32_t)(2 * j) ^ tr_swz1) << 4)));
+            const uint32_t a = tr_base + ((uint32_t)(32 * j) ^ tr_swz16);
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a));
+            const short4_t hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a + 4 * kBtRow));
             const half8_t bop = __builtin_bit_cast(
                 half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
@@ -613,39 +637,56 @@ __global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict
         if (started) finish();
         aop = __builtin_bit_cast(half8_t,
                                  *reinterpret_cast<const u32x4_t*>(W + ap_row + 16u * (uint32_t)g));
+        // all slot rows first (one LDS wait), then the loads
+        uint32_t row[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            row[t] = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * ld_r +
+                                                        4u * (uint32_t)(t * RPL));
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint32_t e = (uint32_t)(t * RPL) + ld_r;
-            const uint32_t row = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * e);
-            const uint32_t off = (e < cnt && row < k32) ? __umul24(row, rowbytes) + ld_off
-                                                        : b_bytes + ld_off;
+            // slot t * RPL + ld_r is filled iff ld_r < cnt - t * RPL
+            const bool use = ((int)ld_r < (int)cnt - t * RPL) & (row[t] < k32);
+            const uint32_t at = __umul24(row[t], rowbytes) + ld_off;
+            const uint32_t off = use ? at : b_bytes + ld_off;
             bv[t] = __builtin_bit_cast(
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
         }
         started = true;
     };
 
-    auto stage_a = [&](int64_t q, GatherA& P) {
-        const uint32_t pq = (uint32_t)(q - q0);
+    // Stage A: the pair's A operand (buffer load, zeros past this wave's
+    // blocks) and its two block columns (scalar loads at indices clamped into
+    // this wave's blocks; a clamped column only meets zero A data).
+    auto stage_a = [&](int64_t q, BatchA& P) {
+        const uint32_t pq = (uint32_t)q;
         P.a = __builtin_bit_cast(
-            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, 0));
-        P.colv = load_block_col<I>(c_rsrc, c_voff + pq * 2u * (uint32_t)sizeof(I), 0u);
+            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, kNonTemporal));
+        const int64_t i0 = rs + ((int64_t)(2 * pq) < (int64_t)nblk ? (int64_t)(2 * pq) : (int64_t)nblk - 1);
+        const int64_t i1 = rs + ((int64_t)(2 * pq + 1) < (int64_t)nblk ? (int64_t)(2 * pq + 1) : (int64_t)nblk - 1);
+        P.c0 = block_col_scalar(bci[i0]);
+        P.c1 = block_col_scalar(bci[i1]);
     };
 
-    auto process = [&](const GatherA& P) {
-        const uint32_t c0 = (uint32_t)__builtin_amdgcn_readlane((int)P.colv, 0);
-        const uint32_t c1 = (uint32_t)__builtin_amdgcn_readlane((int)P.colv, 32);
+    auto process = [&](const BatchA& P) {
+        const uint32_t c0 = P.c0;
+        const uint32_t c1 = P.c1;
         const u32x4_t w = __builtin_bit_cast(u32x4_t, P.a);
         // bit e: half e of this lane's 8 is non-zero (a -0.0 counts as an
-        // entry; it adds an exact zero).  Plain compares: hipcc 7.2 folds the
-        // packed-min form (min(halves, {1, 1})) in this loop into a test of
-        // the first dword only.
-        uint32_t v = 0u;
+        // entry; it adds an exact zero).  min(halves, 1) per dword is one
+        // packed instruction.  Each dword is copied to a scalar first:
+        // hipcc 7.2 compiles __builtin_bit_cast of a vector element w[d] as a
+        // read of element 0.
+        uint32_t nz[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            v |= ((w[d] & 0xffffu) != 0u ? 1u : 0u) << (2 * d);
-            v |= ((w[d] >> 16) != 0u ? 1u : 0u) << (2 * d + 1);
+            const uint32_t x = w[d];
+            nz[d] = __builtin_bit_cast(
+                uint32_t, __builtin_elementwise_min(__builtin_bit_cast(ushort2_t, x),
+                                                    __builtin_bit_cast(ushort2_t, one)));
         }
+        uint32_t v = nz[0] | (nz[1] << 2) | (nz[2] << 4) | (nz[3] << 6);
+        v = (v | (v >> 15)) & 0xffu;
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
@@ -682,21 +723,37 @@ __global__ __launch_bounds__(256) void spmm_f16_batch_kernel(const I* __restrict
         pending += cnt;
     };
 
-    if (q0 < q1) {
-        GatherA P0, P1, P2, P3;
+    if (wave < npairs) {
+        // The ring is spelled out as separate variables: written as an
+        // unrolled loop over an array, hipcc 7.2 waits for every outstanding
+        // load at the top of each iteration instead of only for the oldest.
+        BatchA P0, P1, P2, P3, P4, P5;
+        constexpr int S = 4;                   // pair stride of a wave
+        constexpr int A = S * kBatchDepth;     // prefetch distance in pairs
+        const int64_t q0 = wave;
         stage_a(q0, P0);
-        stage_a(q0 + 1, P1);
-        stage_a(q0 + 2, P2);
-        stage_a(q0 + 3, P3);
-        for (int64_t q = q0; q < q1; q += kBatchDepth) {
+        stage_a(q0 + S, P1);
+        stage_a(q0 + 2 * S, P2);
+        stage_a(q0 + 3 * S, P3);
+        if constexpr (kBatchDepth > 4) stage_a(q0 + 4 * S, P4);
+        if constexpr (kBatchDepth > 5) stage_a(q0 + 5 * S, P5);
+        for (int64_t q = q0; q < npairs; q += A) {
             process(P0);
-            stage_a(q + 4, P0);
+            stage_a(q + A, P0);
             process(P1);
-            stage_a(q + 5, P1);
+            stage_a(q + A + S, P1);
             process(P2);
-            stage_a(q + 6, P2);
+            stage_a(q + A + 2 * S, P2);
             process(P3);
-            stage_a(q + 7, P3);
+            stage_a(q + A + 3 * S, P3);
+            if constexpr (kBatchDepth > 4) {
+                process(P4);
+                stage_a(q + A + 4 * S, P4);
+            }
+            if constexpr (kBatchDepth > 5) {
+                process(P5);
+                stage_a(q + A + 5 * S, P5);
+            }
         }
         if (pending > 0u) start(pending);
         if (started) finish();
