@@ -96,13 +96,38 @@ def tier1_kernel(value_bytes, K, N):
 
 
 def load_traffic(config):
+    """HBM bytes per SpMM launch from the committed rocprofv3 counter runs
+    (profiles/spmm_traffic.json): FETCH_SIZE and WRITE_SIZE in KiB per
+    dispatch, each scaled by what the same counter reads for a plain copy of
+    known size (`bench.py --calibrate-copy`).  None when not profiled."""
     path = os.path.join(ROOT, "profiles", "spmm_traffic.json")
     try:
         with open(path) as f:
             d = json.load(f)
-        return d.get(config)
     except (OSError, ValueError):
         return None
+    e = d.get("configs", {}).get(config)
+    cal = d.get("calibration")
+    if not e or not cal:
+        return None
+    return (e["fetch_kib"] * cal["fetch_scale"] + e["write_kib"] * cal["write_scale"]) * 1024.0
+
+
+def calibrate_copy():
+    """A plain device copy of known size, for scaling the rocprofv3 byte
+    counters: 3 launches of dst.copy_(src) over 512 MiB (512 MiB read and
+    512 MiB written per launch)."""
+    import torch
+
+    n = 512 << 20
+    src = torch.ones(n // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes_read": n, "calibration_copy_bytes_written": n,
+                      "launches": 3}), flush=True)
 
 
 def main():
@@ -114,6 +139,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pipeline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only the known-size copy used to scale byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -130,6 +157,9 @@ def main():
         print("bench.py needs an MI355X", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     X.load()
 
     print(f"[bench] generating {args.config}", file=sys.stderr, flush=True)
