@@ -7,8 +7,8 @@ from 1024 column-pattern templates, shuffled; B = 16384 x 128 fp16; C fp32.
 The Tier-2 preparation runs once, untimed by the step loop and reported
 separately: host Jaccard clustering (threshold 0.5, width 16) -> GPU row
 permutation -> GPU CSR->BCSR.  A step is one Tier-1 SpMM call
-C = A_bcsr * B on device-resident inputs (for fp16 one launch of the gather
-MFMA kernel).  `value` is the effective throughput 2*nnz*N / t.
+C = A_bcsr * B on device-resident inputs (for fp16 one launch of the
+column-batch MFMA kernel).  `value` is the effective throughput 2*nnz*N / t.
 
 The JSON line also carries:
   roofline      algorithmic HBM bytes per call / measured call time vs 8 TB/s;
@@ -84,13 +84,17 @@ def cpu_baseline(p, N, nnz, seconds):
 
 def tier1_kernel(value_bytes, K, N):
     """Name of the kernel one Tier-1 call launches (the launcher's own rule in
-    xspmm_amd/csrc/spmm.hip: fp16 uses the gather kernel when N is even and B
-    and the block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL=panel)."""
+    xspmm_amd/csrc/spmm.hip: fp16 takes the column-batch kernel when N % 8 == 0
+    and B and the block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL
+    selects another one)."""
     if value_bytes == 4:
         return "spmm_f32_kernel"
     Kb = (K + 15) // 16
-    if (os.environ.get("XSPMM_SPMM_KERNEL", "") != "panel" and N % 2 == 0
-            and K * N * 2 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20):
+    fits = K * N * 2 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20
+    choice = os.environ.get("XSPMM_SPMM_KERNEL", "")
+    if choice in ("", "batch") and N % 8 == 0 and fits:
+        return "spmm_f16_batch_kernel"
+    if choice == "gather" and N % 2 == 0 and fits:
         return "spmm_f16_gather_kernel"
     return "pack_b_panels + spmm_f16_kernel"
 

@@ -11,7 +11,7 @@
  * widen int32 data first.  Value arrays are moved as raw bytes of `vsz` bytes
  * (2 = fp16, 4 = fp32) wherever the reference only copies them.
  *
- * Pinning status (what checks each function; see tests/test_oracle_*.py):
+ * Pinning status (what checks each function; see tests/test_oracle.py):
  *   xo_bcsr_count / xo_bcsr_fill  -- golden vectors from the compiled
  *       reference (oracle/_ref), dense(BCSR) == dense(CSR) bit-exact,
  *       brute-force tiny cases, duplicate/ragged/unsorted fixtures.
