@@ -45,7 +45,7 @@ def rel_frob(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
 
 
-@pytest.mark.parametrize("name", ["blocks", "templates"])
+@pytest.mark.parametrize("name", ["blocks", "templates", "pruned"])
 def test_full_size_tier1(torch, name):
     p = synth.CONFIGS[name]()
     print(f"full-size {name}: M={p.M} K={p.K} N={p.N} nnz={p.nnz}", flush=True)

@@ -147,6 +147,37 @@ def test_spmm_ragged_n_banded(torch, N):
         check_c(host(C), np.repeat(rs[:, None], N, axis=1), dtype)
 
 
+DENSE_SHAPES = [(16, 16, 8), (128, 64, 256), (130, 47, 72), (256, 512, 264), (300, 33, 520),
+                (48, 160, 16)]
+
+
+@pytest.mark.parametrize("itype", [np.int32, np.int64])
+@pytest.mark.parametrize("shape", DENSE_SHAPES, ids=[f"{m}x{k}xN{n}" for m, k, n in DENSE_SHAPES])
+def test_spmm_full_block_grid(torch, shape, itype):
+    # every 16x16 block present (nnzb == Mb * Kb): the GEMM-tiled fp16 kernel;
+    # ragged M and K, odd Kb, N not a multiple of the 256-column tile
+    M, K, N = shape
+    rng = np.random.default_rng(M + K + N)
+    D = rng.standard_normal((M, K)).astype(np.float16)
+    D[rng.random((M, K)) < 0.5] = 0
+    for i in range(0, M, 16):                # at least one entry per block
+        for j in range(0, K, 16):
+            D[i, j] = np.float16(1.0)
+    rp = np.zeros(M + 1, np.int64)
+    rp[1:] = np.cumsum((D != 0).sum(axis=1))
+    ci = np.nonzero(D)[1].astype(itype)
+    vals = D[D != 0]
+    B = rng.standard_normal((K, N)).astype(np.float16)
+    note(f"full block grid M={M} K={K} N={N} {itype.__name__}")
+    A = X.CSRMatrix.from_host(M, K, rp.astype(itype), ci, vals)
+    Bm = X.csr_to_bcsr(A)
+    assert Bm.num_blocks == Bm.num_block_rows * Bm.num_block_cols
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    X.spmm(Bm, dev(torch, B), C, N)
+    torch.cuda.synchronize()
+    check_c(host(C), D.astype(np.float64) @ B.astype(np.float64), np.float16)
+
+
 def test_spmm_empty_and_odd_block_rows(torch):
     # block-rows with 0, 1, 2, 3 blocks; C must be overwritten (zeros where empty)
     rows = []

@@ -73,6 +73,12 @@ template <typename T, typename I>
 void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
                const I* bci, const T* bvals, const T* B, float* C, int64_t N, hipStream_t s);
 
+// Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb).
+// Returns false (and launches nothing) when the shape is not covered.
+bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
+                         const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
+                         hipStream_t s);
+
 // CSR -> BCSR.  count writes brp[Mb+1] and returns nnzb (synchronizes `s`);
 // it throws std::invalid_argument on an out-of-range column index.
 template <typename I>

@@ -1,0 +1,321 @@
+// spmm_dense.hip -- Tier-1 BCSR SpMM for a fully populated block grid (fp16).
+//
+// When nnzb == Mb * Kb every block-row holds all Kb blocks, and since block
+// columns are strictly ascending within a row (the layout csr_to_bcsr
+// produces, reference src/core/conversion.cpp:61), block (br, c) sits at
+// index br * Kb + c.  The BCSR values array is then a block-tiled dense
+// matrix and the product is GEMM-shaped: it is bound by the matrix cores, not
+// by HBM.  Semantics are those of the tile kernel (reference
+// src/common/spmm_math.hpp:20-146): blocks accumulate in column order, fp32
+// accumulators, C overwritten; rows >= M and columns >= N are not stored and
+// B rows >= K contribute nothing.
+//
+// Tiling.  A workgroup (4 waves) owns 8 block-rows (128 rows of C) and 256
+// columns; wave w owns columns 64w .. 64w + 63 of that, i.e. 8 x 4 MFMA tiles
+// of 16 x 16 (128 fp32 accumulators per lane).  K advances 32 at a time (two
+// block columns):
+//   * the 8 block-rows' two blocks (8 KB, contiguous per block-row) and the
+//     32 x 256 B panel (16 KB) go straight from HBM into an LDS stage with
+//     direct-to-LDS buffer loads (no staging registers); the next step's
+//     loads are in flight while the current step multiplies;
+//   * a wave reads each block-row's A operand with one ds_read_b128 (the two
+//     blocks' rows in v_mfma_f32_16x16x32_f16 operand order, as loaded) and
+//     each of its four B operands with two ds_read_b64_tr_b16 from the
+//     row-major panel, then issues 32 MFMAs;
+//   * C leaves through LDS, one block-row at a time, as 16-byte stores.
+// grid: one workgroup per (row group, column group), ordered so that the
+// column groups of a row group run on the same XCD and meet its A tile in that
+// XCD's L2.
+#include "internal.hpp"
+
+namespace xspmm {
+namespace detail {
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+#ifndef XSPMM_DENSE_DR
+#define XSPMM_DENSE_DR 8
+#endif
+#ifndef XSPMM_DENSE_MINW
+#define XSPMM_DENSE_MINW 2
+#endif
+#ifndef XSPMM_DENSE_STAGES
+#define XSPMM_DENSE_STAGES 2
+#endif
+#ifndef XSPMM_DENSE_EPI
+#define XSPMM_DENSE_EPI 2
+#endif
+constexpr int kDR = XSPMM_DENSE_DR;          // block-rows per workgroup
+constexpr int kDN = 256;                     // columns per workgroup
+constexpr int kDTiles = 4;                   // 16-column tiles per wave
+constexpr int kABytes = kDR * 1024;          // A stage: 8 block-rows x 2 blocks
+constexpr int kBRow = kDN * 2;               // B panel row: 512 bytes
+constexpr int kBBytes = 32 * kBRow;          // B stage: 32 rows
+constexpr int kStage = kABytes + kBBytes;    // 24 KB (three stages: 72 KB)
+constexpr int kAU = kDR / 4;                 // A block-rows loaded per wave
+constexpr int kLoadsPerStep = kAU + 4;       // direct-to-LDS loads per wave per K step
+constexpr int kRawWord3 = 0x00020000;        // raw dword buffer access (gfx9)
+constexpr int kXcds = 8;                     // accelerator dies of an MI355X
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (4 SGPRs) over [base, base + bytes): loads at offsets
+// past `bytes` return zeros without touching memory.
+__device__ __forceinline__ i32x4_t raw_rsrc(const void* base, uint32_t bytes)
+{
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4_t r;
+    r.x = (int)(uint32_t)a;
+    r.y = (int)(uint32_t)((a >> 32) & 0xffffu);  // stride 0
+    r.z = (int)bytes;
+    r.w = kRawWord3;
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One direct-to-LDS load: lane l's 16 bytes at byte `off` of the buffer land
+// at LDS address lds + 16 l (buffer_load_dwordx4 ... lds, address base in M0).
+// Issued as inline assembly so that the compiler adds no wait of its own: the
+// callers wait with explicit s_waitcnt vmcnt.
+__device__ __forceinline__ void load_to_lds(uint32_t lds, uint32_t off, i32x4_t rsrc)
+{
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(off), "s"(rsrc)
+                 : "memory", "m0");
+}
+
+// 16-byte chunk c of B panel row e is stored at chunk c ^ swz(e): the 16 rows
+// one transpose read touches spread over all banks.
+__device__ __forceinline__ uint32_t panel_swz(uint32_t e)
+{
+    return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
+}
+
+__global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const uint16_t* __restrict__ vals,
+                                                                 const uint16_t* __restrict__ B,
+                                                                 float* __restrict__ C,
+                                                                 int64_t M, int64_t K,
+                                                                 int64_t N, int64_t Mb,
+                                                                 int64_t Kb)
+{
+    constexpr int NS = XSPMM_DENSE_STAGES;
+    static_assert(NS == 2 || NS == 3, "2 or 3 LDS stages");
+    __shared__ __align__(16) unsigned char smem[NS * kStage];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+
+    // XCD-aware tile order.  Workgroup w runs on XCD w % 8 (round-robin
+    // dispatch); the column groups of one row group get ids that share that
+    // residue and are consecutive in dispatch order, so they meet the row
+    // group's A tile in the same L2.
+    int64_t rg, cg;
+    {
+        const int64_t w = blockIdx.x;
+        const int64_t slot = w / kXcds, xcd = w % kXcds;
+        const int64_t ncg = (N + kDN - 1) / kDN;
+        rg = (slot / ncg) * kXcds + xcd;
+        cg = slot % ncg;
+    }
+    if (rg * kDR >= Mb) return;  // padding workgroups of the last row-group band
+    const int64_t n0 = cg * kDN;
+    const int64_t br0 = rg * kDR;
+
+    const uint32_t a_bytes = (uint32_t)(Mb * Kb * 512);
+    const i32x4_t a_rsrc = raw_rsrc(vals, a_bytes);
+    const uint32_t b_bytes = (uint32_t)(K * N * 2);
+    const i32x4_t b_rsrc = raw_rsrc(B, b_bytes);
+    const uint32_t lds0 = lds_address(smem);
+
+    // --- direct-to-LDS loads of one K step (6 per wave) ----------------------
+    // A: wave w moves block-rows 2w and 2w + 1: 1 KB each, the two consecutive
+    // blocks of the step, lane l -> bytes 16l .. 16l + 15 (lanes >= 32 hold the
+    // second block, which does not exist in the last step of an odd Kb).
+    // B: wave w moves panel rows 8w + 2u and + 1 (u = 0..3): lane l lands at
+    // chunk position l & 31 of row 8w + 2u + (l >> 5) and therefore loads
+    // global chunk (l & 31) ^ swz(row).
+    uint32_t a_off[kAU];
+    bool a_row_ok[kAU];
+#pragma unroll
+    for (int u = 0; u < kAU; ++u) {
+        const int64_t br = br0 + kAU * wave + u;
+        a_row_ok[u] = br < Mb;
+        a_off[u] = (uint32_t)((a_row_ok[u] ? br : 0) * Kb * 512) + 16u * (uint32_t)lane;
+    }
+    const bool a_second = lane >= 32;
+    uint32_t b_row[4];
+    uint32_t b_col_off[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t row = (uint32_t)(8 * wave + 2 * u + (lane >> 5));
+        const uint32_t ch = (uint32_t)(lane & 31) ^ panel_swz(row);
+        const int64_t col = n0 + 8 * (int64_t)ch;
+        b_row[u] = row;
+        b_col_off[u] = col < N ? (uint32_t)(2 * col) : 0xffffffffu;
+    }
+    const int64_t steps = (Kb + 1) / 2;
+    auto issue_step = [&](int64_t s) {
+        const uint32_t base = lds0 + (uint32_t)((s % NS) * kStage);
+#pragma unroll
+        for (int u = 0; u < kAU; ++u) {
+            const bool ok = a_row_ok[u] && (!a_second || 2 * s + 1 < Kb);
+            const uint32_t off = ok ? a_off[u] + (uint32_t)(s * 1024) : a_bytes;
+            load_to_lds(base + (uint32_t)((kAU * wave + u) * 1024), off, a_rsrc);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t k = 32 * s + b_row[u];
+            const uint32_t off = (k < K && b_col_off[u] != 0xffffffffu)
+                                     ? (uint32_t)(k * N * 2) + b_col_off[u]
+                                     : b_bytes;
+            load_to_lds(base + (uint32_t)(kABytes + (8 * wave + 2 * u) * kBRow), off, b_rsrc);
+        }
+    };
+
+    // --- operand reads --------------------------------------------------------
+    // transpose reads: rows 8g + (li >> 2) and + 4, chunk 2 * tile + ((li & 3) >> 1)
+    const uint32_t tr_e = (uint32_t)(8 * g + (li >> 2));
+    const uint32_t tr_base = (uint32_t)kABytes + tr_e * kBRow + 8u * (uint32_t)(li & 1);
+    const uint32_t tr_swz = panel_swz(tr_e);
+    const uint32_t tr_cc = (uint32_t)((li & 3) >> 1);
+    // A operand of a pair: block lane >> 5, row li, halves 8 * ((lane >> 4) & 1) .. +8
+    const uint32_t a_lane = (uint32_t)((lane >> 5) * 512 + li * 32 + ((lane >> 4) & 1) * 16);
+
+    float4_t acc[kDR][kDTiles];
+#pragma unroll
+    for (int r = 0; r < kDR; ++r)
+#pragma unroll
+        for (int j = 0; j < kDTiles; ++j) acc[r][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int stage) {
+        const unsigned char* S = smem + stage * kStage;
+        half8_t bop[kDTiles];
+#pragma unroll
+        for (int j = 0; j < kDTiles; ++j) {
+            const uint32_t c = (uint32_t)(2 * (kDTiles * wave + j)) + tr_cc;
+            const uint32_t a = tr_base + ((c ^ tr_swz) << 4);
+            unsigned char* P = const_cast<unsigned char*>(S) + a;
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)P);
+            const short4_t hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(P + 4 * kBRow));
+            bop[j] = __builtin_bit_cast(half8_t,
+                                        __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+#pragma unroll
+        for (int r = 0; r < kDR; ++r) {
+            const half8_t aop = __builtin_bit_cast(
+                half8_t, *reinterpret_cast<const u32x4_t*>(S + r * 1024 + a_lane));
+#pragma unroll
+            for (int j = 0; j < kDTiles; ++j)
+                acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[r][j], 0, 0, 0);
+        }
+    };
+
+    // LDS ring of NS stages (two by default: with two workgroups per CU that
+    // measured faster than three).  Every wave issues exactly kLoadsPerStep
+    // loads per step and no other vector-memory loads, so "at most
+    // kLoadsPerStep outstanding" (three stages) or "none outstanding" (two)
+    // means this wave's loads of step s have landed; the barrier then makes
+    // every wave's visible and guarantees that the stage step s + NS - 1 is
+    // loaded into, last read at step s - 1, is free.
+    if (steps > 0) issue_step(0);
+    if (NS == 3 && steps > 1) issue_step(1);
+    for (int64_t s = 0; s < steps; ++s) {
+        if (NS == 3 && s + 1 < steps)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStep) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (s + NS - 1 < steps) issue_step(s + NS - 1);
+        compute((int)(s % NS));
+    }
+
+    // --- store: lane holds C[16 br + 4g + q][16 tile + li] ------------------
+    if constexpr (XSPMM_DENSE_EPI == 2) {
+        // Through LDS, one block-row at a time: the workgroup's 16 x 256 fp32
+        // slice is written to LDS in MFMA order and read back row-major, so
+        // every lane stores 16 contiguous bytes (rows of 1 KB per workgroup).
+        __syncthreads();  // the last step's operand reads are done
+        float* T = reinterpret_cast<float*>(smem);  // [16][256 + 4] fp32
+        constexpr int TS = kDN + 4;
+        const int row_l = t >> 4;                  // 0..15
+        const int col_l = (t & 15) * 4;            // 0..60, +64 per pass
+#pragma unroll
+        for (int r = 0; r < kDR; ++r) {
+#pragma unroll
+            for (int j = 0; j < kDTiles; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    T[(4 * g + q) * TS + 64 * wave + 16 * j + li] = acc[r][j][q];
+            __syncthreads();
+            const int64_t row = 16 * (br0 + r) + row_l;
+#pragma unroll
+            for (int p = 0; p < kDN / 64; ++p) {
+                const int c = col_l + 64 * p;
+                const float4_t v = *reinterpret_cast<const float4_t*>(T + row_l * TS + c);
+                const int64_t col = n0 + c;
+                if (row < M && col < N) {
+                    if (col + 4 <= N && (N & 3) == 0)
+                        __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(C + row * N + col));
+                    else
+                        for (int e = 0; e < 4 && col + e < N; ++e) C[row * N + col + e] = v[e];
+                }
+            }
+            __syncthreads();
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kDR; ++r) {
+            const int64_t row0 = 16 * (br0 + r) + 4 * g;
+#pragma unroll
+            for (int j = 0; j < kDTiles; ++j) {
+                const int64_t col = n0 + 64 * wave + 16 * j + li;
+                if (col >= N) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (row0 + q < M) {
+                        if constexpr (XSPMM_DENSE_EPI == 1)
+                            __builtin_nontemporal_store(acc[r][j][q], C + (row0 + q) * N + col);
+                        else
+                            C[(row0 + q) * N + col] = acc[r][j][q];
+                    }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
+                         const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
+                         hipStream_t s)
+{
+    if (nnzb != Mb * Kb || Mb <= 0 || Kb <= 0 || N <= 0) return false;
+    if (N % 8 != 0) return false;
+    if (Mb * Kb * 512 >= (int64_t(1) << 31) || K * N * 2 >= (int64_t(1) << 31)) return false;
+    const int64_t ncg = (N + kDN - 1) / kDN;
+    const int64_t nrg = (Mb + kDR - 1) / kDR;
+    // row groups padded to a multiple of the XCD count; padding groups exit
+    const int64_t groups = ((nrg + kXcds - 1) / kXcds) * kXcds * ncg;
+    if (groups > 0x7fffffffLL) return false;
+    hipLaunchKernelGGL(spmm_f16_dense_kernel, dim3((unsigned)groups), dim3(256), 0, s, bvals, B, C,
+                       M, K, N, Mb, Kb);
+    XSPMM_LAUNCH_CHECK();
+    return true;
+}
+
+}  // namespace detail
+}  // namespace xspmm
