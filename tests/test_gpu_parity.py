@@ -178,6 +178,28 @@ def test_spmm_full_block_grid(torch, shape, itype):
     check_c(host(C), D.astype(np.float64) @ B.astype(np.float64), np.float16)
 
 
+@pytest.mark.parametrize("N", [64, 128])
+def test_spmm_many_skewed_block_rows(torch, N):
+    # Mb = 3000 > 2048 block-rows with power-law lengths: the launcher orders
+    # rows longest-first before the column-batch kernel
+    rng = np.random.default_rng(N)
+    M, K = 48000, 4096
+    deg = np.minimum((rng.pareto(1.2, M) + 1) * 3, K).astype(np.int64)
+    rows = [np.sort(rng.choice(K, size=d, replace=False)) for d in deg]
+    rp = np.zeros(M + 1, np.int64); rp[1:] = np.cumsum(deg)
+    ci = np.concatenate(rows).astype(np.int32)
+    vals = rng.uniform(-1, 1, len(ci)).astype(np.float16)
+    B = rng.standard_normal((K, N)).astype(np.float16)
+    note(f"skewed rows M={M} nnz={len(ci)} N={N}")
+    A = X.CSRMatrix.from_host(M, K, rp.astype(np.int32), ci, vals)
+    Bm = X.csr_to_bcsr(A)
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    X.spmm(Bm, dev(torch, B), C, N)
+    torch.cuda.synchronize()
+    ref = oracle.csr_spmm_f64(M, N, rp, ci, vals, B)
+    check_c(host(C), ref, np.float16)
+
+
 def test_spmm_empty_and_odd_block_rows(torch):
     # block-rows with 0, 1, 2, 3 blocks; C must be overwritten (zeros where empty)
     rows = []

@@ -543,7 +543,8 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
                                                              const uint16_t* __restrict__ vals,
                                                              const uint16_t* __restrict__ B,
                                                              float* __restrict__ C, int64_t M,
-                                                             int64_t K, int64_t N, int64_t Kb)
+                                                             int64_t K, int64_t N, int64_t Kb,
+                                                             const int32_t* __restrict__ order)
 {
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
@@ -553,7 +554,8 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     unsigned char* const W = smem + wave * kBatchWaveLds;
 
-    const int64_t br = blockIdx.x;
+    // block-row: in dispatch order, or longest rows first when `order` is given
+    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
     const int64_t n0 = (int64_t)blockIdx.y * 128;
     const int64_t rs = brp[br];
     const int64_t re = brp[br + 1];
@@ -791,6 +793,49 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
 }
 
 // ---------------------------------------------------------------------------
+// Dispatch order for skewed block-rows: one 1024-thread workgroup buckets the
+// block-rows by the bit length of their block count (longest bucket first) and
+// writes the row ids in that order.  Workgroups are dispatched in id order, so
+// long rows start first instead of trailing the grid.  Only scheduling
+// changes: each row's result is computed exactly as before.
+// ---------------------------------------------------------------------------
+constexpr int kOrderThreads = 1024;
+constexpr int64_t kOrderMinRows = 2048;
+constexpr int kOrderBuckets = 33;
+
+template <typename I>
+__global__ __launch_bounds__(kOrderThreads) void order_rows_kernel(const I* __restrict__ brp,
+                                                                   int64_t Mb,
+                                                                   int32_t* __restrict__ order)
+{
+    __shared__ uint32_t count[kOrderBuckets];
+    __shared__ uint32_t next[kOrderBuckets];
+    const int t = threadIdx.x;
+    if (t < kOrderBuckets) count[t] = 0u;
+    __syncthreads();
+    auto bucket = [&](int64_t r) -> int {
+        const int64_t len = (int64_t)brp[r + 1] - (int64_t)brp[r];
+        const uint64_t u = len > 0 ? (uint64_t)len : 0u;
+        const int bits = u ? 64 - __builtin_clzll(u) : 0;  // 0..33
+        return bits > 32 ? 32 : bits;
+    };
+    for (int64_t r = t; r < Mb; r += kOrderThreads) atomicAdd(&count[bucket(r)], 1u);
+    __syncthreads();
+    if (t == 0) {
+        uint32_t run = 0;
+        for (int b = kOrderBuckets - 1; b >= 0; --b) {  // longest bucket first
+            next[b] = run;
+            run += count[b];
+        }
+    }
+    __syncthreads();
+    for (int64_t r = t; r < Mb; r += kOrderThreads) {
+        const uint32_t pos = atomicAdd(&next[bucket(r)], 1u);
+        order[pos] = (int32_t)r;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 x fp32 -> fp32 tile kernel.
 // ---------------------------------------------------------------------------
 template <typename I, int NTW>
@@ -927,18 +972,29 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
         const dim3 ggrid((unsigned)Mb, (unsigned)chunks);
         if ((choice == Fp16Kernel::kAuto || choice == Fp16Kernel::kBatch) && N % 8 == 0 &&
             offsets32) {
+            // more block-rows than resident workgroups (4 per CU on 256 CUs,
+            // times two): dispatch the longest rows first
+            Scratch order_buf;
+            const int32_t* order = nullptr;
+            if (Mb > kOrderMinRows && Mb <= 0x7fffffffLL) {
+                order_buf = Scratch((size_t)Mb * sizeof(int32_t), s);
+                hipLaunchKernelGGL((order_rows_kernel<I>), dim3(1), dim3(kOrderThreads), 0, s, brp,
+                                   Mb, order_buf.as<int32_t>());
+                XSPMM_LAUNCH_CHECK();
+                order = order_buf.as<int32_t>();
+            }
             if (N <= 16)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb);
+                                   v, b, C, M, K, N, Kb, order);
             else if (N <= 32)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb);
+                                   v, b, C, M, K, N, Kb, order);
             else if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb);
+                                   v, b, C, M, K, N, Kb, order);
             else
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb);
+                                   v, b, C, M, K, N, Kb, order);
             XSPMM_LAUNCH_CHECK();
             return;
         }
