@@ -484,6 +484,9 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
 //   4. when a pair does not fit the batch, starts the batch: reads its A'
 //      operand and issues the 16-byte loads of its 32 B rows (unused slots
 //      get an out-of-range offset, which reads zeros without touching memory);
+//      A pair with more than 24 non-zero columns is a batch by itself: its
+//      A registers are stored as the 32 slots in one go and its B rows are
+//      the two blocks' 16-row panels;
 //   5. one batch later (so the row loads have long arrived) writes those rows
 //      row-major into an LDS tile, reads them back with the gfx950 transpose
 //      read ds_read_b64_tr_b16 as MFMA B operands and issues one
@@ -511,6 +514,8 @@ constexpr int kBatchWaveLds = kSlotOff + 32 * 4;
 #define XSPMM_BATCH_MIN_WAVES 1
 #endif
 constexpr int kBatchDepth = XSPMM_BATCH_DEPTH;  // A pairs in flight per wave (4..6)
+// a pair with more non-zero columns than this multiplies as a whole
+constexpr uint32_t kFullPairCols = 24;
 static_assert(kBatchDepth >= 4 && kBatchDepth <= 6, "batch depth must be 4, 5 or 6");
 
 // swizzle of row e: even values 0..14, each used by two of the 16 rows a
@@ -702,12 +707,25 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
                             valid;
         if (pm == 0u) return;
         const uint32_t cnt = (uint32_t)__builtin_popcount(pm);
-        if (pending + cnt > 32u) {
+        // A pair with more than kFullPairCols columns is a batch by itself:
+        // its A registers fill all 32 slots (slot e = column e of the pair,
+        // one 16-byte store per lane) and slot e's B row is row e & 15 of
+        // block e >> 4.  It stays open until the next pair or the end of the
+        // row, so a pair never starts two batches.
+        const bool full = cnt > kFullPairCols;
+        const uint32_t take = full ? 32u : cnt;
+        if (pending + take > 32u) {
             start(pending);
             pending = 0;
         }
+        if (full) {
+            *reinterpret_cast<u32x4_t*>(W + ap_row + 16u * (uint32_t)g) = w;
+            if (lane < 32)
+                *reinterpret_cast<uint32_t*>(W + kSlotOff + 4u * (uint32_t)lane) =
+                    16u * (lane >= 16 ? c1 : c0) + (uint32_t)(lane & 15);
+        }
         // this lane's group: its columns take consecutive slots from `base`
-        uint32_t rem = (pm >> (8 * g)) & 0xffu;
+        uint32_t rem = full ? 0u : (pm >> (8 * g)) & 0xffu;
         const uint32_t base = pending + (uint32_t)__builtin_popcount(pm & below_group);
         const uint32_t colbase = 16u * (sel ? c1 : c0) + 8u * (uint32_t)kh;
         uint32_t slot = base;
@@ -722,7 +740,7 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
                 ++slot;
             }
         } while (__builtin_amdgcn_ballot_w64(rem != 0u) != 0);
-        pending += cnt;
+        pending += take;
     };
 
     if (wave < npairs) {
