@@ -10,19 +10,22 @@
 // accumulators, C overwritten; rows >= M and columns >= N are not stored and
 // B rows >= K contribute nothing.
 //
-// Tiling.  A workgroup (4 waves) owns 8 block-rows (128 rows of C) and 256
-// columns; wave w owns columns 64w .. 64w + 63 of that, i.e. 8 x 4 MFMA tiles
-// of 16 x 16 (128 fp32 accumulators per lane).  K advances 32 at a time (two
+// Tiling.  A workgroup (8 waves, a 2 x 4 wave grid) owns 16 block-rows
+// (256 rows of C) and 256 columns; each wave owns 8 block-rows x 64 columns,
+// i.e. 8 x 4 MFMA tiles of 16 x 16 (128 fp32 accumulators per lane).  The
+// 256 x 256 tile keeps the cache traffic per MFMA low: every K step moves
+// 16 KB of A and 16 KB of B for 4.2 MFLOP.  K advances 32 at a time (two
 // block columns):
-//   * the 8 block-rows' two blocks (8 KB, contiguous per block-row) and the
-//     32 x 256 B panel (16 KB) go straight from HBM into an LDS stage with
+//   * the 16 block-rows' two blocks (16 KB, contiguous per block-row) and the
+//     32 x 256 B panel (16 KB) go straight from memory into an LDS stage with
 //     direct-to-LDS buffer loads (no staging registers); the next step's
 //     loads are in flight while the current step multiplies;
-//   * a wave reads each block-row's A operand with one ds_read_b128 (the two
-//     blocks' rows in v_mfma_f32_16x16x32_f16 operand order, as loaded) and
-//     each of its four B operands with two ds_read_b64_tr_b16 from the
-//     row-major panel, then issues 32 MFMAs;
-//   * C leaves through LDS, one block-row at a time, as 16-byte stores.
+//   * a wave reads each of its block-rows' A operand with one ds_read_b128
+//     (the two blocks' rows in v_mfma_f32_16x16x32_f16 operand order, as
+//     loaded) and each of its four B operands with two ds_read_b64_tr_b16
+//     from the row-major panel, then issues 32 MFMAs;
+//   * C leaves through LDS, one block-row per wave row at a time, as 16-byte
+//     stores.
 // grid: one workgroup per (row group, column group), ordered so that the
 // column groups of a row group run on the same XCD and meet its A tile in that
 // XCD's L2.
@@ -40,7 +43,7 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 #ifndef XSPMM_DENSE_DR
-#define XSPMM_DENSE_DR 8
+#define XSPMM_DENSE_DR 16
 #endif
 #ifndef XSPMM_DENSE_MINW
 #define XSPMM_DENSE_MINW 2
@@ -53,13 +56,24 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 #endif
 constexpr int kDR = XSPMM_DENSE_DR;          // block-rows per workgroup
 constexpr int kDN = 256;                     // columns per workgroup
-constexpr int kDTiles = 4;                   // 16-column tiles per wave
+#ifndef XSPMM_DENSE_WAVES
+#define XSPMM_DENSE_WAVES 8
+#endif
+constexpr int kDW = XSPMM_DENSE_WAVES;       // waves per workgroup (4 or 8)
+constexpr int kDThreads = 64 * kDW;
+// waves form a kWR x kWC grid; each owns 8 block-rows x kDTiles column tiles
+constexpr int kWR = kDR / 8;
+constexpr int kWC = kDW / kWR;
+constexpr int kDTiles = 16 / kWC;            // 16-column tiles per wave
+static_assert(kDR % 8 == 0 && kDW % kWR == 0 && 16 % kWC == 0, "wave grid");
 constexpr int kABytes = kDR * 1024;          // A stage: 8 block-rows x 2 blocks
 constexpr int kBRow = kDN * 2;               // B panel row: 512 bytes
 constexpr int kBBytes = 32 * kBRow;          // B stage: 32 rows
 constexpr int kStage = kABytes + kBBytes;    // 24 KB (three stages: 72 KB)
-constexpr int kAU = kDR / 4;                 // A block-rows loaded per wave
-constexpr int kLoadsPerStep = kAU + 4;       // direct-to-LDS loads per wave per K step
+constexpr int kAU = kDR / kDW;               // A block-rows loaded per wave
+constexpr int kBU = 16 / kDW;                // B panel row pairs loaded per wave
+constexpr int kLoadsPerStep = kAU + kBU;     // direct-to-LDS loads per wave per K step
+static_assert(kDR % kDW == 0 && kAU >= 1, "block-rows must split evenly over waves");
 constexpr int kRawWord3 = 0x00020000;        // raw dword buffer access (gfx9)
 constexpr int kXcds = 8;                     // accelerator dies of an MI355X
 
@@ -102,7 +116,7 @@ __device__ __forceinline__ uint32_t panel_swz(uint32_t e)
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
 }
 
-__global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const uint16_t* __restrict__ vals,
+__global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const uint16_t* __restrict__ vals,
                                                                  const uint16_t* __restrict__ B,
                                                                  float* __restrict__ C,
                                                                  int64_t M, int64_t K,
@@ -115,6 +129,8 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wr = wave / kWC;  // this wave's block-rows: 8 wr .. 8 wr + 7
+    const int wc = wave % kWC;  // and column tiles kDTiles wc .. + kDTiles - 1
     const int li = lane & 15;
     const int g = lane >> 4;
 
@@ -156,11 +172,11 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
         a_off[u] = (uint32_t)((a_row_ok[u] ? br : 0) * Kb * 512) + 16u * (uint32_t)lane;
     }
     const bool a_second = lane >= 32;
-    uint32_t b_row[4];
-    uint32_t b_col_off[4];
+    uint32_t b_row[kBU];
+    uint32_t b_col_off[kBU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const uint32_t row = (uint32_t)(8 * wave + 2 * u + (lane >> 5));
+    for (int u = 0; u < kBU; ++u) {
+        const uint32_t row = (uint32_t)(2 * kBU * wave + 2 * u + (lane >> 5));
         const uint32_t ch = (uint32_t)(lane & 31) ^ panel_swz(row);
         const int64_t col = n0 + 8 * (int64_t)ch;
         b_row[u] = row;
@@ -176,12 +192,12 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
             load_to_lds(base + (uint32_t)((kAU * wave + u) * 1024), off, a_rsrc);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kBU; ++u) {
             const int64_t k = 32 * s + b_row[u];
             const uint32_t off = (k < K && b_col_off[u] != 0xffffffffu)
                                      ? (uint32_t)(k * N * 2) + b_col_off[u]
                                      : b_bytes;
-            load_to_lds(base + (uint32_t)(kABytes + (8 * wave + 2 * u) * kBRow), off, b_rsrc);
+            load_to_lds(base + (uint32_t)(kABytes + (2 * kBU * wave + 2 * u) * kBRow), off, b_rsrc);
         }
     };
 
@@ -194,9 +210,9 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
     // A operand of a pair: block lane >> 5, row li, halves 8 * ((lane >> 4) & 1) .. +8
     const uint32_t a_lane = (uint32_t)((lane >> 5) * 512 + li * 32 + ((lane >> 4) & 1) * 16);
 
-    float4_t acc[kDR][kDTiles];
+    float4_t acc[8][kDTiles];
 #pragma unroll
-    for (int r = 0; r < kDR; ++r)
+    for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int j = 0; j < kDTiles; ++j) acc[r][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -205,7 +221,7 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
         half8_t bop[kDTiles];
 #pragma unroll
         for (int j = 0; j < kDTiles; ++j) {
-            const uint32_t c = (uint32_t)(2 * (kDTiles * wave + j)) + tr_cc;
+            const uint32_t c = (uint32_t)(2 * (kDTiles * wc + j)) + tr_cc;
             const uint32_t a = tr_base + ((c ^ tr_swz) << 4);
             unsigned char* P = const_cast<unsigned char*>(S) + a;
             const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)P);
@@ -215,9 +231,9 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
                                         __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
 #pragma unroll
-        for (int r = 0; r < kDR; ++r) {
+        for (int r = 0; r < 8; ++r) {
             const half8_t aop = __builtin_bit_cast(
-                half8_t, *reinterpret_cast<const u32x4_t*>(S + r * 1024 + a_lane));
+                half8_t, *reinterpret_cast<const u32x4_t*>(S + (8 * wr + r) * 1024 + a_lane));
 #pragma unroll
             for (int j = 0; j < kDTiles; ++j)
                 acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[r][j], 0, 0, 0);
@@ -245,26 +261,29 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
 
     // --- store: lane holds C[16 br + 4g + q][16 tile + li] ------------------
     if constexpr (XSPMM_DENSE_EPI == 2) {
-        // Through LDS, one block-row at a time: the workgroup's 16 x 256 fp32
-        // slice is written to LDS in MFMA order and read back row-major, so
-        // every lane stores 16 contiguous bytes (rows of 1 KB per workgroup).
+        // Through LDS, eight rounds: in round r every wave writes its r-th
+        // block-row (16 x kDTiles*16 fp32, MFMA order) and the workgroup reads
+        // the kWR * 16 rows back row-major, so every lane stores 16 contiguous
+        // bytes (1 KB rows per workgroup).
         __syncthreads();  // the last step's operand reads are done
-        float* T = reinterpret_cast<float*>(smem);  // [16][256 + 4] fp32
+        float* T = reinterpret_cast<float*>(smem);  // [kWR * 16][256 + 4] fp32
         constexpr int TS = kDN + 4;
-        const int row_l = t >> 4;                  // 0..15
-        const int col_l = (t & 15) * 4;            // 0..60, +64 per pass
+        constexpr int TR = kWR * 16;               // rows staged per round
+        constexpr int TPR = kDThreads / TR;        // threads per row
+        const int row_l = t / TPR;
+        const int col_l = (t % TPR) * 4;           // +4 * TPR per pass
 #pragma unroll
-        for (int r = 0; r < kDR; ++r) {
+        for (int r = 0; r < 8; ++r) {
 #pragma unroll
             for (int j = 0; j < kDTiles; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    T[(4 * g + q) * TS + 64 * wave + 16 * j + li] = acc[r][j][q];
+                    T[(16 * wr + 4 * g + q) * TS + 16 * kDTiles * wc + 16 * j + li] = acc[r][j][q];
             __syncthreads();
-            const int64_t row = 16 * (br0 + r) + row_l;
+            const int64_t row = 16 * (br0 + 8 * (row_l / 16) + r) + (row_l % 16);
 #pragma unroll
-            for (int p = 0; p < kDN / 64; ++p) {
-                const int c = col_l + 64 * p;
+            for (int p = 0; p < kDN / (4 * TPR); ++p) {
+                const int c = col_l + 4 * TPR * p;
                 const float4_t v = *reinterpret_cast<const float4_t*>(T + row_l * TS + c);
                 const int64_t col = n0 + c;
                 if (row < M && col < N) {
@@ -278,11 +297,11 @@ __global__ __launch_bounds__(256, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(c
         }
     } else {
 #pragma unroll
-        for (int r = 0; r < kDR; ++r) {
-            const int64_t row0 = 16 * (br0 + r) + 4 * g;
+        for (int r = 0; r < 8; ++r) {
+            const int64_t row0 = 16 * (br0 + 8 * wr + r) + 4 * g;
 #pragma unroll
             for (int j = 0; j < kDTiles; ++j) {
-                const int64_t col = n0 + 64 * wave + 16 * j + li;
+                const int64_t col = n0 + 16 * kDTiles * wc + 16 * j + li;
                 if (col >= N) continue;
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
@@ -311,7 +330,7 @@ bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t n
     // row groups padded to a multiple of the XCD count; padding groups exit
     const int64_t groups = ((nrg + kXcds - 1) / kXcds) * kXcds * ncg;
     if (groups > 0x7fffffffLL) return false;
-    hipLaunchKernelGGL(spmm_f16_dense_kernel, dim3((unsigned)groups), dim3(256), 0, s, bvals, B, C,
+    hipLaunchKernelGGL(spmm_f16_dense_kernel, dim3((unsigned)groups), dim3(kDThreads), 0, s, bvals, B, C,
                        M, K, N, Mb, Kb);
     XSPMM_LAUNCH_CHECK();
     return true;
