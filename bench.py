@@ -82,14 +82,18 @@ def cpu_baseline(p, N, nnz, seconds):
     }
 
 
-def tier1_kernel(value_bytes, K, N):
+def tier1_kernel(value_bytes, K, N, nnzb, Mb):
     """Name of the kernel one Tier-1 call launches (the launcher's own rule in
-    xspmm_amd/csrc/spmm.hip: fp16 takes the column-batch kernel when N % 8 == 0
-    and B and the block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL
-    selects another one)."""
+    xspmm_amd/csrc/spmm.hip: fp16 takes the GEMM-tiled kernel when every block
+    is present, else the column-batch kernel when N % 8 == 0 and B and the
+    block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL selects
+    another one)."""
     if value_bytes == 4:
         return "spmm_f32_kernel"
     Kb = (K + 15) // 16
+    if (nnzb == Mb * Kb and N % 8 == 0 and Mb * Kb * 512 < 1 << 31 and K * N * 2 < 1 << 31
+            and os.environ.get("XSPMM_SPMM_KERNEL", "") == ""):
+        return "spmm_f16_dense_kernel"
     fits = K * N * 2 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20
     choice = os.environ.get("XSPMM_SPMM_KERNEL", "")
     if choice in ("", "batch") and N % 8 == 0 and fits:
@@ -228,6 +232,18 @@ def main():
     eff = 2.0 * nnz * N / t / 1e12
     padded = 2.0 * nnzb * 256 * N / t / 1e12
     mfma_peak = FP16_PEAK_TFLOPS if sT == 2 else FP32_MFMA_PEAK_TFLOPS
+    # bound: padded flops per algorithmic byte against the ridge point
+    ridge = mfma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
+    mfma_bound = 2.0 * nnzb * 256 * N / alg_bytes > ridge
+    if mfma_bound:
+        roofline = {"bound": "mfma", "achieved": padded, "peak": mfma_peak, "unit": "TFLOP/s",
+                    "frac": padded / mfma_peak}
+    else:
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBS}
+    roofline.update({"traffic": load_traffic(args.config), "kernel": tier1_kernel(sT, K, N, nnzb, Mb),
+                     "alg_bytes_per_call": alg_bytes,
+                     "padded_flops_per_call": 2.0 * nnzb * 256 * N})
 
     stages = None
     if not args.no_pipeline:
@@ -258,16 +274,9 @@ def main():
             "index": "int32", "accumulate": "fp32",
             "clustering": bool(p.cluster),
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": load_traffic(args.config),
-            "kernel": tier1_kernel(sT, K, N),
-            "alg_bytes_per_call": alg_bytes,
-        },
+        "roofline": roofline,
+        "hbm_gbs": achieved,
+        "hbm_frac": achieved / HBM_PEAK_GBS,
         "padded_tflops": padded,
         "mfma_frac": padded / mfma_peak,
         "wall_s_timed_region": wall,
