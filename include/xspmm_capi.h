@@ -104,8 +104,25 @@ int xspmm_jaccard_clustering_host(int itype, int64_t M, int64_t K, const void* r
                                   void* perm_out, int nthreads);
 
 /*
+ * GPU Jaccard row clustering on DEVICE arrays rp[M+1], ci[nnz]; writes the
+ * device array perm_out[M].  The same permutation as
+ * xspmm_jaccard_clustering_host (the reference's greedy,
+ * src/cpu/clustering_sylos_labini.cpp:51-120), computed by one workgroup that
+ * commits joins in the reference's visiting order.  engine_used (nullable,
+ * host) receives 0 (closed form: dist_thresh outside [0, 1)), 1 (scan engine)
+ * or 2 (row-list engine).  Synchronizes `stream`.  Limits: M < 2^31, at most
+ * 524288 column blocks, M * ceil(blocks / 64) * 8 bytes of row bitmaps
+ * within 16 GiB; beyond them it returns XSPMM_ERR_INVALID.
+ * Replaces xspmm::compute_1d_jaccard_clustering for device matrices
+ * (reference include/xspmm/clustering.hpp:19-25, src/xspmm.cpp:57-67).
+ */
+int xspmm_jaccard_clustering(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
+                             const void* ci, float dist_thresh, int64_t block_width,
+                             void* perm_out, int* engine_used, void* stream);
+
+/*
  * Tier-2 pipeline on device CSR arrays rp/ci/vals, device B and C.
- * hw_block_size must be 16.  With optimize_pattern != 0: cluster (host) ->
+ * hw_block_size must be 16.  With optimize_pattern != 0: cluster ->
  * permute -> convert -> SpMM -> unpermute; else convert -> SpMM.  timings
  * (nullable, host) receives the six SpMMTimings fields in declaration order:
  * clustering, permutation, conversion, spmm, unpermutation, total (ms);

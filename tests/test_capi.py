@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     assert len(syms) >= 9
     for s in syms:
         assert hasattr(L, s), s
-    assert L.xspmm_abi_version() == 1
+    assert L.xspmm_abi_version() == 2
     assert L.xspmm_last_error() == b""
 
 
@@ -73,6 +73,18 @@ def test_host_clustering_error_paths():
                                         np.array([0], np.int32), block_width=0)
     assert len(X.compute_1d_jaccard_clustering(0, 16, np.array([0], np.int32),
                                                np.zeros(0, np.int32))) == 0
+
+
+def test_device_clustering_argument_errors_without_gpu():
+    L = X.load()
+    f = L.xspmm_jaccard_clustering
+    assert f(X.I32, -1, 16, 0, None, None, 0.5, 16, None, None, None) == X.ERR_INVALID
+    assert f(X.I32, 4, -16, 0, None, None, 0.5, 16, None, None, None) == X.ERR_INVALID
+    assert f(X.I32, 1, 16, 0, None, None, 0.5, 0, None, None, None) == X.ERR_INVALID
+    assert b"block_width" in L.xspmm_last_error()
+    assert f(9, 1, 16, 0, None, None, 0.5, 16, None, None, None) == X.ERR_INVALID
+    # M = 0: nothing to cluster, no device work
+    assert f(X.I64, 0, 16, 0, None, None, 0.5, 16, None, None, None) == X.OK
 
 
 JAC = golden_cases("jaccard")

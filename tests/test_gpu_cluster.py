@@ -1,0 +1,191 @@
+"""GPU parity of the device Jaccard clustering (xspmm_jaccard_clustering).
+
+The permutation must equal the reference's bit for bit:
+  * against the golden permutations written by the compiled reference
+    (ties inter/union = 1/2, thresholds 0 / 0.3 / 0.75 / 1 / negative, block
+    widths 1 and 4, more than one bitmap word per row), with each engine
+    forced and with the automatic choice;
+  * against the oracle's greedy on seeded random, template-like, skewed and
+    empty-row inputs, int32 and int64, both engines;
+  * at the headline size (templates, 16384 rows) against the oracle, and on
+    the 131072-row power-law graph against the product's host engine (the
+    oracle's scan would take minutes there; the host engine is pinned to the
+    reference by the CPU tests).
+All calls go through the C ABI of libxspmm.so.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import xspmm_amd as X
+from tests.helpers import golden_cases, widen
+from xspmm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need an MI355X (torch.cuda.is_available() is False)")
+    X.load()
+    return torch
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def csr(torch, M, K, rp, ci, itype=None):
+    it = itype or np.asarray(rp).dtype
+    rp = np.ascontiguousarray(rp).astype(it)
+    ci = np.ascontiguousarray(ci).astype(it)
+    t = torch.int32 if np.dtype(it) == np.int32 else torch.int64
+    return X.CSRMatrix(int(M), int(K), torch.as_tensor(rp).cuda().to(t),
+                       torch.as_tensor(ci).cuda().to(t),
+                       torch.zeros(max(len(ci), 0), dtype=torch.float16, device="cuda"))
+
+
+def gpu_perm(torch, M, K, rp, ci, thr=0.5, bw=16, itype=None):
+    A = csr(torch, M, K, rp, ci, itype)
+    perm, engine = X.jaccard_clustering(A, thr, bw, return_engine=True)
+    torch.cuda.synchronize()
+    return perm.cpu().numpy(), engine
+
+
+def expected_engine(forced, thr):
+    if not (0.0 <= thr < 1.0):  # NaN too
+        return "closed-form"
+    return forced
+
+
+JAC = golden_cases("jaccard")
+
+
+@pytest.mark.parametrize("engine", ["scan", "index", "auto"])
+@pytest.mark.parametrize("case", JAC, ids=[c["name"] for c in JAC])
+def test_gpu_clustering_matches_reference_golden(torch, case, engine, monkeypatch):
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    thr = float(case["thresh"])
+    note(f"golden {case['name']} engine={engine} M={int(case['M'])} thr={thr}")
+    perm, used = gpu_perm(torch, int(case["M"]), int(case["K"]), case["rp"], case["ci"], thr,
+                          int(case["bw"]))
+    assert perm.dtype == case["rp"].dtype
+    np.testing.assert_array_equal(widen(perm), widen(case["perm"]))
+    if engine != "auto":
+        assert used == expected_engine(engine, thr)
+
+
+def skewed_csr(rng, M, K):
+    rows = []
+    for r in range(M):
+        kind = rng.integers(0, 10)
+        if kind == 0:
+            rows.append(np.zeros(0, np.int64))  # empty row
+        elif kind == 1:
+            rows.append(rng.integers(0, K, size=int(rng.integers(50, 400))))  # long row
+        else:
+            rows.append(rng.integers(0, K, size=int(rng.integers(1, 12))))
+    rp = np.zeros(M + 1, np.int64)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    ci = np.concatenate(rows) if rp[-1] else np.zeros(0, np.int64)
+    return rp, ci
+
+
+@pytest.mark.parametrize("itype", [np.int32, np.int64])
+@pytest.mark.parametrize("engine", ["scan", "index"])
+@pytest.mark.parametrize("seed", range(6))
+def test_gpu_clustering_matches_oracle_random(torch, seed, engine, itype, monkeypatch):
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    rng = np.random.default_rng(900 + seed)
+    thr = [0.5, 0.4, 0.0, 0.5, 0.25, 0.7][seed]
+    bw = [16, 8, 16, 3, 16, 1][seed]
+    if seed % 3 == 0:
+        M, K = int(rng.integers(100, 3000)), int(rng.integers(64, 5000))
+        p = synth.random_csr(M, K, 4, float(rng.uniform(0.001, 0.02)), seed=seed,
+                             dtype=np.float32, unsorted=bool(seed % 2))
+        rp, ci = p.rp, p.ci
+    elif seed % 3 == 1:
+        p = synth.templates(M=1024 + 512 * seed, n_templates=64, seed=seed)
+        M, K, rp, ci = p.M, p.K, p.rp, p.ci
+    else:
+        M, K = int(rng.integers(500, 2500)), int(rng.integers(100, 3000))
+        rp, ci = skewed_csr(rng, M, K)
+    note(f"random seed={seed} engine={engine} itype={np.dtype(itype).name} M={M} K={K} thr={thr} bw={bw}")
+    want = oracle.jaccard(M, K, rp, ci, thr, bw)
+    got, used = gpu_perm(torch, M, K, rp, ci, thr, bw, itype)
+    assert got.dtype == itype
+    np.testing.assert_array_equal(widen(got), want)
+    assert used == engine
+
+
+@pytest.mark.parametrize("thr", [-0.25, 1.0, 1.5, float("nan")])
+def test_gpu_clustering_thresholds_outside_unit_interval(torch, thr):
+    # d <= thr never holds (thr < 0, NaN) or always holds (thr >= 1)
+    rng = np.random.default_rng(5)
+    rp, ci = skewed_csr(rng, 700, 900)
+    want = oracle.jaccard(700, 900, rp, ci, thr, 16)
+    got, used = gpu_perm(torch, 700, 900, rp, ci, thr)
+    np.testing.assert_array_equal(widen(got), want)
+    np.testing.assert_array_equal(widen(got), np.arange(699, -1, -1))
+    assert used == "closed-form"
+
+
+@pytest.mark.parametrize("engine", ["scan", "index"])
+def test_gpu_clustering_degenerate_shapes(torch, engine, monkeypatch):
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    # one row
+    got, _ = gpu_perm(torch, 1, 16, np.array([0, 2]), np.array([3, 9]))
+    np.testing.assert_array_equal(got, [0])
+    # no column at all (K = 0): every row is empty
+    got, _ = gpu_perm(torch, 37, 0, np.zeros(38, np.int64), np.zeros(0, np.int64))
+    np.testing.assert_array_equal(widen(got), oracle.jaccard(37, 0, np.zeros(38, np.int64),
+                                                             np.zeros(0, np.int64)))
+    # only empty rows but K > 0, and a mix of identical rows
+    rp = np.array([0, 0, 0, 2, 2, 4, 4], np.int64)
+    ci = np.array([5, 40, 5, 40], np.int64)
+    got, _ = gpu_perm(torch, 6, 64, rp, ci)
+    np.testing.assert_array_equal(widen(got), oracle.jaccard(6, 64, rp, ci))
+    # more than 1024 rows join the first cluster (several 1024-position steps)
+    M = 5000
+    rp = np.arange(M + 1, dtype=np.int64)
+    ci = np.full(M, 7, np.int64)
+    got, _ = gpu_perm(torch, M, 32, rp, ci)
+    np.testing.assert_array_equal(widen(got), oracle.jaccard(M, 32, rp, ci))
+
+
+def test_gpu_clustering_rejects_bad_input(torch):
+    with pytest.raises(X.XspmmInvalidArgument):
+        gpu_perm(torch, 2, 16, np.array([0, 1, 2]), np.array([0, 99]))
+    with pytest.raises(X.XspmmInvalidArgument):
+        gpu_perm(torch, 2, 16, np.array([0, 1, 2]), np.array([0, -1]))
+    with pytest.raises(X.XspmmInvalidArgument):
+        gpu_perm(torch, 1, 16, np.array([0, 1]), np.array([0]), bw=0)
+
+
+def test_gpu_clustering_headline_size_matches_oracle(torch):
+    p = synth.templates()
+    note(f"templates M={p.M} nnz={int(p.rp[-1])}")
+    want = oracle.jaccard(p.M, p.K, p.rp, p.ci)
+    for engine in ("auto", "scan", "index"):
+        os.environ["XSPMM_CLUSTER_ENGINE"] = engine
+        try:
+            got, used = gpu_perm(torch, p.M, p.K, p.rp, p.ci)
+        finally:
+            del os.environ["XSPMM_CLUSTER_ENGINE"]
+        note(f"templates engine={engine} ran={used}")
+        np.testing.assert_array_equal(widen(got), want)
+
+
+def test_gpu_clustering_power_law_graph_matches_host_engine(torch):
+    p = synth.gnn()
+    note(f"gnn M={p.M} nnz={int(p.rp[-1])}")
+    want = X.compute_1d_jaccard_clustering(p.M, p.K, p.rp, p.ci)
+    got, used = gpu_perm(torch, p.M, p.K, p.rp, p.ci)
+    note(f"gnn engine={used}")
+    np.testing.assert_array_equal(widen(got), widen(want))

@@ -73,6 +73,9 @@ def load():
     L.xspmm_unpermute_dense.argtypes = [i32, p, p, p, i64, i64, p]
     L.xspmm_jaccard_clustering_host.restype = i32
     L.xspmm_jaccard_clustering_host.argtypes = [i32, i64, i64, p, p, C.c_float, i64, p, i32]
+    L.xspmm_jaccard_clustering.restype = i32
+    L.xspmm_jaccard_clustering.argtypes = [i32, i64, i64, i64, p, p, C.c_float, i64, p,
+                                           C.POINTER(C.c_int), p]
     L.xspmm_spmm_pipeline.restype = i32
     L.xspmm_spmm_pipeline.argtypes = [i32, i32, i64, i64, i64, p, p, p, p, p, i64, i64, i32,
                                       C.POINTER(C.c_double), p]
@@ -237,6 +240,30 @@ def compute_1d_jaccard_clustering(M, K, rp, ci, dist_thresh=0.5, block_width=16,
                                            C.c_float(dist_thresh), int(block_width),
                                            perm.ctypes.data_as(C.c_void_p), int(nthreads)))
     return perm[: int(M)]
+
+
+CLUSTER_ENGINES = {0: "closed-form", 1: "scan", 2: "index"}
+
+
+def jaccard_clustering(A: CSRMatrix, dist_thresh=0.5, block_width=16, return_engine=False):
+    """GPU Jaccard clustering of a device CSR matrix -> device perm tensor
+    (perm[new] = old), the same permutation as the host greedy
+    (reference include/xspmm/clustering.hpp:19-25, src/cpu/clustering_sylos_labini.cpp:51-120).
+    Synchronizes torch's current stream.  With return_engine, also returns
+    the engine that ran ("closed-form", "scan" or "index")."""
+    torch = _torch()
+    L = load()
+    M = int(A.num_rows)
+    perm = torch.empty(max(M, 1), dtype=A.row_ptr.dtype, device=A.row_ptr.device)
+    used = C.c_int(-1)
+    _check(L.xspmm_jaccard_clustering(icode(A.row_ptr.dtype), M, int(A.num_cols), A.nnz,
+                                      _ptr(A.row_ptr), _ptr(A.col_ind) if A.nnz else None,
+                                      C.c_float(dist_thresh), int(block_width), _ptr(perm),
+                                      C.byref(used), _stream()))
+    perm = perm[:M]
+    if return_engine:
+        return perm, CLUSTER_ENGINES.get(used.value, "none")
+    return perm
 
 
 def apply_permutation(A: CSRMatrix, perm) -> CSRMatrix:

@@ -174,7 +174,8 @@ void spmm(const BCSRMatrix<InputType, IndexType>& A, const InputType* B, OutputT
 }
 
 // ---------------------------------------------------------------------------
-// Clustering (host algorithm for every executor, as in the reference)
+// Clustering: on the GPU for a HipExecutor (same permutation as the
+// reference's host greedy), on the host for a CpuExecutor
 // ---------------------------------------------------------------------------
 template <typename ValueType, typename IndexType>
 void compute_1d_jaccard_clustering(std::shared_ptr<const Executor> exec,
@@ -183,6 +184,16 @@ void compute_1d_jaccard_clustering(std::shared_ptr<const Executor> exec,
 {
     const int64_t M = A.get_num_rows();
     if (M == 0) return;
+    if (const HipExecutor* h = as_hip(exec)) {
+        // perm_out lives on the executor's device; the GPU engine gives the
+        // host greedy's permutation
+        use_device(h);
+        DeviceCsr<ValueType, IndexType> v;
+        device_view(A, v);
+        detail::jaccard_clustering_dispatch<IndexType>(M, A.get_num_cols(), A.get_nnz(), v.d_rp, v.d_ci,
+                                                       dist_thresh, block_width, perm_out, kStream);
+        return;
+    }
     std::vector<IndexType> rp, ci, perm((size_t)M);
     host_csr<ValueType, IndexType>(A, rp, ci, nullptr);
     detail::jaccard_clustering_host<IndexType>(M, A.get_num_cols(), rp.data(), ci.data(), dist_thresh,

@@ -73,7 +73,7 @@ extern "C" {
 
 const char* xspmm_last_error(void) { return g_last_error.c_str(); }
 
-int xspmm_abi_version(void) { return 1; }
+int xspmm_abi_version(void) { return 2; }
 
 int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
                     int64_t nnzb, const void* brp, const void* bci, const void* bvals,
@@ -158,6 +158,20 @@ int xspmm_jaccard_clustering_host(int itype, int64_t M, int64_t K, const void* r
             using I = typename decltype(ti)::type;
             jaccard_clustering_host<I>(M, K, static_cast<const I*>(rp), static_cast<const I*>(ci),
                                        dist_thresh, block_width, static_cast<I*>(perm_out), nthreads);
+        });
+    });
+}
+
+int xspmm_jaccard_clustering(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
+                             const void* ci, float dist_thresh, int64_t block_width,
+                             void* perm_out, int* engine_used, void* stream)
+{
+    return guarded([&] {
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            jaccard_clustering_device<I>(M, K, nnz, static_cast<const I*>(rp),
+                                         static_cast<const I*>(ci), dist_thresh, block_width,
+                                         static_cast<I*>(perm_out), as_stream(stream), engine_used);
         });
     });
 }

@@ -1,0 +1,620 @@
+// cluster_gpu.hip -- exact 1-D Jaccard ("Sylos Labini") row clustering on the GPU.
+//
+// Same greedy, same visiting order and same float comparison as the
+// reference (src/cpu/clustering_sylos_labini.cpp:51-120) and as the host
+// engines in cluster.cpp, so the permutation is identical bit for bit:
+//   q_r = set of block_width-wide column blocks row r touches (:13-33);
+//   unclustered = [0..M-1]; while non-empty: seed = pop_back(); p = q_seed;
+//   for i = size-1 down to 0: cand = unclustered[i];
+//     d = |p|q| == 0 ? 0 : 1 - (float)|p&q| / (float)|p|q|          (:35-46)
+//     if d <= dist_thresh: join, p |= q_cand, swap-remove position i (:97-104)
+//
+// The greedy is sequential in its commits: whether a candidate joins depends
+// on every join before it.  It runs in ONE workgroup of 1024 threads, which
+// evaluates many candidates at once against the current pattern and commits
+// the first joiner in visiting order (the highest position), then goes on
+// below it -- the candidates above it were tested against the right pattern.
+// All threads keep the loop state (counts, positions) in registers as
+// identical copies: every decision comes out of a block reduction.  Thread 0
+// alone writes the shared arrays (permutation, positions).
+//
+// Two engines, picked from the pattern statistics (or XSPMM_CLUSTER_ENGINE):
+//  * scan:  each step tests 1024 consecutive positions below the last commit
+//           with popcounts of the row bitmaps (a popcount bound first);
+//  * index: only rows that share a block with the pattern can join (d = 1
+//           otherwise, and dist_thresh < 1), so the workgroup keeps
+//           |p & q_r| per row, raised through per-block row lists whenever a
+//           block enters the pattern, and tests only those rows;
+//           |p | q_r| = |p| + |q_r| - |p & q_r|.
+// Every loop of the clustering kernel ends: each commit removes a row and
+// lowers the scan limit, and each step without a commit lowers it by 1024.
+//
+// Preparation (all rows in parallel): row bitmaps by atomic OR, their
+// popcounts, each row's block list, and the per-block row lists (counts,
+// exclusive scan, scatter).
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+#include "scan.hpp"
+
+namespace xspmm {
+namespace detail {
+
+namespace {
+
+constexpr int kClThreads = 1024;
+constexpr int kClWaves = kClThreads / 64;
+constexpr int kPatternWords32 = 16384;        // LDS pattern bitmap: 64 KB
+constexpr int64_t kMaxGpuBlocks = 32LL * kPatternWords32;  // 524288 column blocks
+constexpr int kPrepThreads = 256;
+constexpr int kEngineAuto = 0, kEngineScan = 1, kEngineIndex = 2;
+
+// Jaccard distance exactly as the reference evaluates it: int -> float
+// conversions and an IEEE division (round to nearest).
+__device__ __forceinline__ float jaccard_distance(int inter, int uni)
+{
+    if (uni == 0) return 0.0f;
+    return 1.0f - __fdiv_rn((float)inter, (float)uni);
+}
+
+// Agent-scope fence plus barrier: global stores, atomics and plain loads of
+// every wave are ordered across the phase boundary.
+__device__ __forceinline__ void phase_sync()
+{
+    __threadfence();
+    __syncthreads();
+}
+
+__device__ __forceinline__ int wave_max(int v)
+{
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = max(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v)
+{
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// Block-wide reductions over the 1024 threads (two barriers each).
+__device__ __forceinline__ int block_max(int v, int* red)
+{
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int m = red[0];
+#pragma unroll
+    for (int w = 1; w < kClWaves; ++w) m = max(m, red[w]);
+    __syncthreads();
+    return m;
+}
+
+__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* red)
+{
+    v = wave_sum64(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int64_t s = 0;
+#pragma unroll
+    for (int w = 0; w < kClWaves; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+// Exclusive scan over the 1024 threads; *total gets the sum (two barriers).
+__device__ __forceinline__ int64_t block_exscan64(int64_t v, int64_t* total, int64_t* red)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int64_t incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    if (lane == 63) red[wave] = incl;
+    __syncthreads();
+    int64_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kClWaves; ++w) {
+        const int64_t x = red[w];
+        if (w < wave) before += x;
+        all += x;
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - v;
+}
+
+// --- preparation kernels (one wave per row) ---------------------------------
+
+template <typename I>
+__global__ __launch_bounds__(kPrepThreads) void pattern_bits_kernel(const I* __restrict__ rp,
+                                                                    const I* __restrict__ ci,
+                                                                    int64_t M, int64_t K,
+                                                                    int64_t nnz, int64_t bw,
+                                                                    int64_t W, uint64_t* bits,
+                                                                    int* bad)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * (kPrepThreads / 64);
+    for (int64_t r = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) >> 6; r < M; r += nw) {
+        int64_t s = (int64_t)rp[r], e = (int64_t)rp[r + 1];
+        s = s < 0 ? 0 : s;
+        e = e > nnz ? nnz : e;
+        uint64_t* q = bits + r * W;
+        for (int64_t j = s + lane; j < e; j += 64) {
+            const int64_t c = (int64_t)ci[j];
+            if (c < 0 || c >= K) {
+                *bad = 1;
+                continue;
+            }
+            const int64_t b = c / bw;
+            atomicOr((unsigned long long*)(q + (b >> 6)), 1ULL << (b & 63));
+        }
+    }
+}
+
+__global__ __launch_bounds__(kPrepThreads) void pattern_count_kernel(const uint64_t* __restrict__ bits,
+                                                                     int64_t M, int64_t W,
+                                                                     int32_t* count)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * (kPrepThreads / 64);
+    for (int64_t r = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) >> 6; r < M; r += nw) {
+        int64_t n = 0;
+        for (int64_t w = lane; w < W; w += 64) n += __popcll(bits[r * W + w]);
+        n = wave_sum64(n);
+        if (lane == 0) count[r] = (int32_t)n;
+    }
+}
+
+// Row r's blocks, ascending, at rb[rb_start[r] ...]; counts rows per block.
+__global__ __launch_bounds__(kPrepThreads) void row_lists_kernel(const uint64_t* __restrict__ bits,
+                                                                 int64_t M, int64_t W,
+                                                                 const int64_t* __restrict__ rb_start,
+                                                                 int32_t* rb, int32_t* bl_count)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * (kPrepThreads / 64);
+    for (int64_t r = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) >> 6; r < M; r += nw) {
+        int64_t at = rb_start[r];
+        for (int64_t w0 = 0; w0 < W; w0 += 64) {
+            const int64_t w = w0 + lane;
+            uint64_t x = w < W ? bits[r * W + w] : 0ULL;
+            const int64_t n = __popcll(x);
+            int64_t incl = n;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int64_t t = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += t;
+            }
+            int64_t o = at + incl - n;
+            for (; x; x &= x - 1) {
+                const int32_t b = (int32_t)(w * 64 + __builtin_ctzll(x));
+                rb[o++] = b;
+                atomicAdd(&bl_count[b], 1);
+            }
+            at += __shfl(incl, 63, 64);
+        }
+    }
+}
+
+// Row lists per block: bl_rows[bl_start[b] ...] (order within a list is free).
+__global__ __launch_bounds__(kPrepThreads) void block_lists_kernel(int64_t M,
+                                                                   const int64_t* __restrict__ rb_start,
+                                                                   const int32_t* __restrict__ rb,
+                                                                   const int64_t* __restrict__ bl_start,
+                                                                   int32_t* bl_fill, int32_t* bl_rows)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * (kPrepThreads / 64);
+    for (int64_t r = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) >> 6; r < M; r += nw) {
+        for (int64_t k = rb_start[r] + lane; k < rb_start[r + 1]; k += 64) {
+            const int32_t b = rb[k];
+            const int32_t at = atomicAdd(&bl_fill[b], 1);
+            bl_rows[bl_start[b] + at] = (int32_t)r;
+        }
+    }
+}
+
+template <typename I>
+__global__ void reversed_perm_kernel(I* perm, int64_t M)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < M; i += stride)
+        perm[i] = (I)(M - 1 - i);
+}
+
+struct ClusterArgs {
+    int64_t M, W, Kb;
+    float thresh;
+    int engine;
+    const uint64_t* bits;     // M x W row bitmaps (scan engine)
+    const int32_t* count;     // |q_r|
+    const int64_t* rb_start;  // M + 1
+    const int32_t* rb;        // row block lists
+    const int64_t* bl_start;  // Kb + 1
+    const int32_t* bl_rows;   // block row lists
+    int32_t* un;              // unclustered rows by position
+    int32_t* pos;             // position of each row, -1 once clustered
+    int32_t* cnt;             // |p & q_r| (index engine), zero between clusters
+    int32_t* log;             // rows with cnt > 0
+    int32_t* cand_a;          // candidate lists (compacted each round)
+    int32_t* cand_b;
+    int32_t* plist;           // blocks of the pattern
+    int* engine_used;
+};
+
+// --- the clustering kernel ----------------------------------------------------
+
+template <typename I>
+__global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* __restrict__ perm)
+{
+    __shared__ uint32_t p32[kPatternWords32];  // pattern bitmap
+    __shared__ int red[kClWaves];
+    __shared__ int64_t red64[kClWaves];
+    __shared__ int s_cnt[4];                   // append counters: log, candidates, pattern
+    __shared__ int32_t s_blk[kClThreads];      // touch: blocks of the current chunk
+    __shared__ int64_t s_pre[kClThreads + 1];  // touch: their list offsets
+    __shared__ uint8_t s_flag[kClThreads];
+
+    const int t = threadIdx.x;
+    const int M = (int)a.M;
+    const int W = (int)a.W;  // 64-bit words per row bitmap
+    const float thr = a.thresh;
+    uint64_t* p64 = reinterpret_cast<uint64_t*>(p32);
+
+    for (int i = t; i < M; i += kClThreads) {
+        a.un[i] = i;
+        a.pos[i] = i;
+    }
+    for (int i = t; i < kPatternWords32; i += kClThreads) p32[i] = 0u;
+    if (t < 4) s_cnt[t] = 0;
+
+    int engine = a.engine;
+    if (engine == kEngineAuto) {
+        // work estimates: scan ~ M^2 * W / 2 word tests, index ~ 3 * sum over
+        // blocks of (rows in the block)^2 counter updates
+        int64_t sq = 0;
+        for (int64_t b = t; b < a.Kb; b += kClThreads) {
+            const int64_t v = a.bl_start[b + 1] - a.bl_start[b];
+            sq += v * v;
+        }
+        const double s = (double)block_sum64(sq, red64);
+        engine = 3.0 * s < 0.5 * (double)M * (double)M * (double)W ? kEngineIndex : kEngineScan;
+    }
+    if (t == 0) *a.engine_used = engine;
+    phase_sync();
+
+    int n_un = M;  // every thread holds the same loop state
+    int out = 0;
+
+    if (engine == kEngineScan) {
+        while (n_un > 0) {
+            const int seed = a.un[n_un - 1];
+            --n_un;
+            if (t == 0) perm[out] = (I)seed;
+            ++out;
+            for (int w = t; w < W; w += kClThreads) p64[w] = a.bits[(int64_t)seed * W + w];
+            int pc = a.count[seed];
+            int hi = n_un - 1;  // highest position not yet visited
+            __syncthreads();
+            while (hi >= 0) {
+                const int at = hi - t;
+                int key = -1;
+                if (at >= 0) {
+                    const int c = a.un[at];
+                    const int qc = a.count[c];
+                    const int mn = qc < pc ? qc : pc, mx = qc < pc ? pc : qc;
+                    if (jaccard_distance(mn, mx) <= thr) {  // |p&q| <= mn, |p|q| >= mx
+                        const uint64_t* q = a.bits + (int64_t)c * W;
+                        int inter = 0, uni = 0;
+                        for (int w = 0; w < W; ++w) {
+                            const uint64_t x = q[w], y = p64[w];
+                            inter += __popcll(x & y);
+                            uni += __popcll(x | y);
+                        }
+                        if (jaccard_distance(inter, uni) <= thr) key = at;
+                    }
+                }
+                const int best = block_max(key, red);
+                if (best < 0) {
+                    hi -= kClThreads;
+                    continue;
+                }
+                const int c = a.un[best];
+                int64_t add = 0;
+                for (int w = t; w < W; w += kClThreads) {
+                    const uint64_t q = a.bits[(int64_t)c * W + w], o = p64[w];
+                    add += __popcll(q & ~o);
+                    p64[w] = o | q;
+                }
+                pc += (int)block_sum64(add, red64);
+                if (t == 0) {
+                    perm[out] = (I)c;
+                    a.un[best] = a.un[n_un - 1];
+                }
+                ++out;
+                --n_un;
+                hi = best - 1;
+                phase_sync();
+            }
+            __syncthreads();
+        }
+        return;
+    }
+
+    // ---- index engine (0 <= dist_thresh < 1) ----
+    // Raise cnt of the not-yet-visited rows of the lists of plist[b0, b1);
+    // rows whose cnt leaves zero are logged and appended to `cand`.
+    auto touch = [&](int b0, int b1, int limit, int32_t* cand) {
+        for (int c0 = b0; c0 < b1; c0 += kClThreads) {
+            const int nb = b1 - c0 < kClThreads ? b1 - c0 : kClThreads;
+            int64_t len = 0;
+            if (t < nb) {
+                const int32_t b = a.plist[c0 + t];
+                s_blk[t] = b;
+                len = a.bl_start[b + 1] - a.bl_start[b];
+            }
+            int64_t total;
+            const int64_t ex = block_exscan64(len, &total, red64);
+            if (t < nb) s_pre[t] = ex;
+            if (t == 0) s_pre[nb] = total;
+            __syncthreads();
+            for (int64_t e = t; e < total; e += kClThreads) {
+                int lo = 0, hi = nb - 1;  // last j with s_pre[j] <= e
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (s_pre[mid] <= e) lo = mid;
+                    else hi = mid - 1;
+                }
+                const int32_t r = a.bl_rows[a.bl_start[s_blk[lo]] + (e - s_pre[lo])];
+                const int pr = a.pos[r];
+                if (pr < 0 || pr >= limit) continue;  // clustered or already visited
+                if (atomicAdd(&a.cnt[r], 1) == 0) {
+                    a.log[atomicAdd(&s_cnt[0], 1)] = r;
+                    cand[atomicAdd(&s_cnt[1], 1)] = r;
+                }
+            }
+            __syncthreads();
+        }
+    };
+
+    while (n_un > 0) {
+        const int seed = a.un[n_un - 1];
+        --n_un;
+        if (t == 0) {
+            perm[out] = (I)seed;
+            a.pos[seed] = -1;
+        }
+        ++out;
+        phase_sync();
+
+        if (a.count[seed] == 0) {
+            // Empty pattern: the remaining empty rows join, in descending
+            // position order, and the pattern stays empty.  A swap-remove at
+            // position i moves in a row from above i, already visited.
+            for (int hi = n_un - 1; hi >= 0; hi -= kClThreads) {
+                const int at = hi - t;
+                s_flag[t] = (at >= 0 && a.count[a.un[at]] == 0) ? 1 : 0;
+                __syncthreads();
+                if (t == 0) {
+                    int o = out, n = n_un;
+                    for (int k = 0; k < kClThreads && hi - k >= 0; ++k) {
+                        if (!s_flag[k]) continue;
+                        const int i = hi - k;
+                        const int r = a.un[i];
+                        perm[o++] = (I)r;
+                        a.pos[r] = -1;
+                        const int moved = a.un[n - 1];
+                        a.un[i] = moved;
+                        a.pos[moved] = i;
+                        --n;
+                    }
+                    red[0] = o;
+                    red[1] = n;
+                }
+                phase_sync();
+                out = red[0];
+                n_un = red[1];
+                __syncthreads();
+            }
+            continue;
+        }
+
+        // pattern := blocks of the seed
+        {
+            const int64_t rs = a.rb_start[seed];
+            const int n = (int)(a.rb_start[seed + 1] - rs);
+            for (int k = t; k < n; k += kClThreads) {
+                const int32_t b = a.rb[rs + k];
+                a.plist[k] = b;
+                atomicOr(&p32[b >> 5], 1u << (b & 31));
+            }
+        }
+        int pc = a.count[seed];
+        int limit = n_un;  // positions below limit are not yet visited
+        int32_t* cur = a.cand_a;
+        int32_t* nxt = a.cand_b;
+        phase_sync();
+        touch(0, pc, limit, cur);
+        phase_sync();
+
+        for (;;) {
+            const int ncand = s_cnt[1];
+            __syncthreads();
+            if (t == 0) s_cnt[1] = 0;
+            __syncthreads();
+            // test the candidates, keeping those still below the limit
+            int key = -1;
+            for (int k = t; k < ncand; k += kClThreads) {
+                const int32_t r = cur[k];
+                const int pr = a.pos[r];
+                if (pr < 0 || pr >= limit) continue;
+                nxt[atomicAdd(&s_cnt[1], 1)] = r;
+                const int inter = __hip_atomic_load(&a.cnt[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int uni = pc + a.count[r] - inter;
+                if (jaccard_distance(inter, uni) <= thr && pr > key) key = pr;
+            }
+            const int best = block_max(key, red);
+            int32_t* sw = cur;
+            cur = nxt;
+            nxt = sw;
+            if (best < 0) break;
+            const int r = a.un[best];
+            if (t == 0) {
+                perm[out] = (I)r;
+                const int moved = a.un[n_un - 1];
+                a.un[best] = moved;
+                a.pos[moved] = best;
+                a.pos[r] = -1;
+            }
+            ++out;
+            --n_un;
+            limit = best;
+            if (t == 0) s_cnt[2] = pc;
+            phase_sync();
+            // blocks of r not yet in the pattern
+            const int64_t rs = a.rb_start[r];
+            const int n = (int)(a.rb_start[r + 1] - rs);
+            for (int k = t; k < n; k += kClThreads) {
+                const int32_t b = a.rb[rs + k];
+                const uint32_t bit = 1u << (b & 31);
+                if ((atomicOr(&p32[b >> 5], bit) & bit) == 0u) a.plist[atomicAdd(&s_cnt[2], 1)] = b;
+            }
+            phase_sync();
+            const int pc_new = s_cnt[2];
+            touch(pc, pc_new, limit, cur);  // new candidates join the compacted list
+            pc = pc_new;
+            phase_sync();
+        }
+
+        // reset the counters and the pattern
+        const int nlog = s_cnt[0];
+        for (int k = t; k < nlog; k += kClThreads)
+            __hip_atomic_store(&a.cnt[a.log[k]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = t; k < pc; k += kClThreads) {
+            const int32_t b = a.plist[k];
+            p32[b >> 5] = 0u;
+        }
+        phase_sync();
+        if (t < 4) s_cnt[t] = 0;
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+template <typename I>
+void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                               float dist_thresh, int64_t block_width, I* perm, hipStream_t s,
+                               int* engine_used)
+{
+    if (M < 0 || K < 0 || nnz < 0) throw std::invalid_argument("CSR dimensions must be non-negative.");
+    if (M == 0) return;  // reference :63
+    if (block_width <= 0) throw std::invalid_argument("clustering: block_width must be positive.");
+    const int64_t Kb = (K + block_width - 1) / block_width;
+    if (!clustering_device_supported(M, K, block_width))
+        throw std::invalid_argument("clustering: shape beyond the GPU engine's limits.");
+    const int64_t W = Kb > 0 ? (Kb + 63) / 64 : 1;
+
+    Scratch bad_d(sizeof(int) * 2, s);
+    XSPMM_HIP_CHECK(hipMemsetAsync(bad_d.get(), 0, sizeof(int) * 2, s));
+    int* bad = bad_d.as<int>();
+    Scratch bits((size_t)(M * W) * sizeof(uint64_t), s);
+    XSPMM_HIP_CHECK(hipMemsetAsync(bits.get(), 0, (size_t)(M * W) * sizeof(uint64_t), s));
+    const unsigned grid = (unsigned)std::min<int64_t>((M + 3) / 4, 65536);
+    hipLaunchKernelGGL(pattern_bits_kernel<I>, dim3(grid), dim3(kPrepThreads), 0, s, rp, ci, M, K,
+                       nnz, block_width, W, bits.as<uint64_t>(), bad);
+    XSPMM_LAUNCH_CHECK();
+    int h_bad = 0;
+    XSPMM_HIP_CHECK(hipMemcpyAsync(&h_bad, bad, sizeof(int), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    if (h_bad) throw std::invalid_argument("clustering: column index out of range.");
+
+    // d <= t never holds for t < 0 (or NaN) and always holds for t >= 1:
+    // no row joins, or every row joins the first cluster in visiting order;
+    // either way perm = [M-1, ..., 0].
+    if (!(dist_thresh >= 0.0f && dist_thresh < 1.0f)) {
+        hipLaunchKernelGGL(reversed_perm_kernel<I>, dim3((unsigned)std::min<int64_t>((M + 255) / 256, 4096)),
+                           dim3(256), 0, s, perm, M);
+        XSPMM_LAUNCH_CHECK();
+        if (engine_used) *engine_used = 0;
+        return;
+    }
+
+    Scratch count((size_t)M * sizeof(int32_t), s);
+    hipLaunchKernelGGL(pattern_count_kernel, dim3(grid), dim3(kPrepThreads), 0, s,
+                       bits.as<uint64_t>(), M, W, count.as<int32_t>());
+    XSPMM_LAUNCH_CHECK();
+    Scratch rb_start((size_t)(M + 1) * sizeof(int64_t), s);
+    device_exclusive_scan(ArrayValue<int32_t>{count.as<int32_t>()}, M, rb_start.as<int64_t>(), s);
+    int64_t nrb = 0;
+    XSPMM_HIP_CHECK(hipMemcpyAsync(&nrb, rb_start.as<int64_t>() + M, sizeof(int64_t),
+                                   hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    const int64_t nb = Kb > 0 ? Kb : 1;
+    Scratch rb((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
+    Scratch bl_count((size_t)nb * sizeof(int32_t), s);
+    XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
+    hipLaunchKernelGGL(row_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, bits.as<uint64_t>(),
+                       M, W, rb_start.as<int64_t>(), rb.as<int32_t>(), bl_count.as<int32_t>());
+    XSPMM_LAUNCH_CHECK();
+    Scratch bl_start((size_t)(nb + 1) * sizeof(int64_t), s);
+    device_exclusive_scan(ArrayValue<int32_t>{bl_count.as<int32_t>()}, nb, bl_start.as<int64_t>(), s);
+    XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
+    Scratch bl_rows((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
+    hipLaunchKernelGGL(block_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, M,
+                       rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
+                       bl_count.as<int32_t>(), bl_rows.as<int32_t>());
+    XSPMM_LAUNCH_CHECK();
+
+    Scratch un((size_t)M * sizeof(int32_t), s), pos((size_t)M * sizeof(int32_t), s);
+    Scratch cnt((size_t)M * sizeof(int32_t), s), logb((size_t)M * sizeof(int32_t), s);
+    Scratch ca((size_t)M * sizeof(int32_t), s), cb((size_t)M * sizeof(int32_t), s);
+    Scratch plist((size_t)nb * sizeof(int32_t), s);
+    XSPMM_HIP_CHECK(hipMemsetAsync(cnt.get(), 0, (size_t)M * sizeof(int32_t), s));
+
+    int engine = kEngineAuto;
+    if (const char* e = std::getenv("XSPMM_CLUSTER_ENGINE")) {
+        if (std::strcmp(e, "scan") == 0) engine = kEngineScan;
+        else if (std::strcmp(e, "index") == 0) engine = kEngineIndex;
+    }
+    ClusterArgs args{M, W, Kb, dist_thresh, engine, bits.as<uint64_t>(), count.as<int32_t>(),
+                     rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
+                     bl_rows.as<int32_t>(), un.as<int32_t>(), pos.as<int32_t>(),
+                     cnt.as<int32_t>(), logb.as<int32_t>(), ca.as<int32_t>(), cb.as<int32_t>(),
+                     plist.as<int32_t>(), bad + 1};
+    hipLaunchKernelGGL(cluster_kernel<I>, dim3(1), dim3(kClThreads), 0, s, args, perm);
+    XSPMM_LAUNCH_CHECK();
+    if (engine_used) {
+        XSPMM_HIP_CHECK(hipMemcpyAsync(engine_used, bad + 1, sizeof(int), hipMemcpyDeviceToHost, s));
+        XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    }
+}
+
+bool clustering_device_supported(int64_t M, int64_t K, int64_t block_width)
+{
+    if (block_width <= 0 || M >= (int64_t)1 << 31) return false;
+    const int64_t Kb = (K + block_width - 1) / block_width;
+    if (Kb > kMaxGpuBlocks) return false;
+    const int64_t W = Kb > 0 ? (Kb + 63) / 64 : 1;
+    return (double)M * (double)W * 8.0 <= 16.0 * (1ULL << 30);  // row bitmaps <= 16 GiB
+}
+
+template void jaccard_clustering_device<int32_t>(int64_t, int64_t, int64_t, const int32_t*,
+                                                 const int32_t*, float, int64_t, int32_t*,
+                                                 hipStream_t, int*);
+template void jaccard_clustering_device<int64_t>(int64_t, int64_t, int64_t, const int64_t*,
+                                                 const int64_t*, float, int64_t, int64_t*,
+                                                 hipStream_t, int*);
+
+}  // namespace detail
+}  // namespace xspmm

@@ -104,6 +104,24 @@ template <typename I>
 void jaccard_clustering_host(int64_t M, int64_t K, const I* rp, const I* ci, float dist_thresh,
                              int64_t block_width, I* perm, int nthreads);
 
+// GPU Jaccard clustering on device CSR arrays; writes perm[M] on the device.
+// The same permutation as jaccard_clustering_host.  Synchronizes `s`.
+// engine_used (nullable, host) receives 0 (closed form), 1 (scan) or 2 (index).
+template <typename I>
+void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                               float dist_thresh, int64_t block_width, I* perm, hipStream_t s,
+                               int* engine_used);
+// Whether the GPU engine covers the shape (M < 2^31, at most 524288 column
+// blocks, row bitmaps within 16 GiB).
+bool clustering_device_supported(int64_t M, int64_t K, int64_t block_width);
+
+// Clustering of device CSR arrays into the device array d_perm: the GPU
+// engine, or the host greedy on copies when XSPMM_CLUSTER_DEVICE=host or the
+// shape is beyond the GPU engine.  Synchronizes `s`.
+template <typename I>
+void jaccard_clustering_dispatch(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                                 float dist_thresh, int64_t block_width, I* d_perm, hipStream_t s);
+
 // Tier-2 pipeline on raw device pointers.  `timings` may be null; it points
 // at six doubles laid out like SpMMTimings.
 template <typename T, typename I>

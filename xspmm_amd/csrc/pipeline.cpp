@@ -2,17 +2,22 @@
 //
 // Stage order, thresholds and timing fields follow the reference
 // (src/hip/unstructured_mtx_mul.hip:31-100):
-//   clustering on : cluster (host, threshold 0.5, width hw_block_size) ->
+//   clustering on : cluster (threshold 0.5, width hw_block_size) ->
 //                   permute rows -> CSR->BCSR -> SpMM into C_temp ->
 //                   un-permute C_temp into C;
 //   clustering off: CSR->BCSR -> SpMM into C.
-// Every stage except clustering runs on the GPU.  Each timed stage is
+// Every stage runs on the GPU: clustering too (the same permutation as the
+// reference's host greedy), unless XSPMM_CLUSTER_DEVICE=host or the shape is
+// beyond the GPU engine's limits, where the host greedy runs on copies of
+// row_ptr/col_ind.  Each timed stage is
 // bracketed by HIP events on the pipeline stream and waited for, so host work
 // inside a bracket counts too (the reference's HipTimer does the same).
 // Differences from the reference, with identical results: C / C_temp are not
 // memset first (the SpMM overwrites every element), temporaries come from the
 // stream-ordered pool instead of hipMalloc/hipFree, and permuted row_ptr[M]
 // is the sum of the gathered lengths (equal to nnz for a permutation).
+#include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "internal.hpp"
@@ -56,6 +61,40 @@ private:
 
 }  // namespace
 
+template <typename I>
+void jaccard_clustering_dispatch(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                                 float dist_thresh, int64_t block_width, I* d_perm, hipStream_t s)
+{
+    if (M < 0 || K < 0 || nnz < 0) throw std::invalid_argument("CSR dimensions must be non-negative.");
+    if (M == 0) return;
+    if (block_width <= 0) throw std::invalid_argument("clustering: block_width must be positive.");
+    const char* where = std::getenv("XSPMM_CLUSTER_DEVICE");
+    const bool host = where && std::strcmp(where, "host") == 0;
+    if (!host && clustering_device_supported(M, K, block_width)) {
+        jaccard_clustering_device<I>(M, K, nnz, rp, ci, dist_thresh, block_width, d_perm, s, nullptr);
+        return;
+    }
+    std::vector<I> h_rp((size_t)M + 1), h_ci((size_t)(nnz > 0 ? nnz : 1)), h_perm((size_t)M);
+    XSPMM_HIP_CHECK(hipMemcpyAsync(h_rp.data(), rp, sizeof(I) * (size_t)(M + 1),
+                                   hipMemcpyDeviceToHost, s));
+    if (nnz > 0)
+        XSPMM_HIP_CHECK(hipMemcpyAsync(h_ci.data(), ci, sizeof(I) * (size_t)nnz,
+                                       hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    jaccard_clustering_host<I>(M, K, h_rp.data(), h_ci.data(), dist_thresh, block_width,
+                               h_perm.data(), 0);
+    XSPMM_HIP_CHECK(hipMemcpyAsync(d_perm, h_perm.data(), sizeof(I) * (size_t)M,
+                                   hipMemcpyHostToDevice, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+template void jaccard_clustering_dispatch<int32_t>(int64_t, int64_t, int64_t, const int32_t*,
+                                                   const int32_t*, float, int64_t, int32_t*,
+                                                   hipStream_t);
+template void jaccard_clustering_dispatch<int64_t>(int64_t, int64_t, int64_t, const int64_t*,
+                                                   const int64_t*, float, int64_t, int64_t*,
+                                                   hipStream_t);
+
 template <typename T, typename I>
 void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const T* vals,
                    const T* B, float* C, int64_t N, int64_t hw, bool optimize_pattern,
@@ -71,22 +110,10 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
 
     if (optimize_pattern) {
-        // 1. Clustering (host).
+        // 1. Clustering.
         step.start();
         Scratch d_perm((size_t)(M > 0 ? M : 1) * sizeof(I), s);
-        if (M > 0) {
-            std::vector<I> h_rp((size_t)M + 1), h_ci((size_t)(nnz > 0 ? nnz : 1)), h_perm((size_t)M);
-            XSPMM_HIP_CHECK(hipMemcpyAsync(h_rp.data(), rp, sizeof(I) * (size_t)(M + 1),
-                                           hipMemcpyDeviceToHost, s));
-            if (nnz > 0)
-                XSPMM_HIP_CHECK(hipMemcpyAsync(h_ci.data(), ci, sizeof(I) * (size_t)nnz,
-                                               hipMemcpyDeviceToHost, s));
-            XSPMM_HIP_CHECK(hipStreamSynchronize(s));
-            jaccard_clustering_host<I>(M, K, h_rp.data(), h_ci.data(), 0.5f, hw, h_perm.data(), 0);
-            XSPMM_HIP_CHECK(hipMemcpyAsync(d_perm.get(), h_perm.data(), sizeof(I) * (size_t)M,
-                                           hipMemcpyHostToDevice, s));
-            XSPMM_HIP_CHECK(hipStreamSynchronize(s));
-        }
+        jaccard_clustering_dispatch<I>(M, K, nnz, rp, ci, 0.5f, hw, d_perm.as<I>(), s);
         if (timed) step.stop(&tm[0]);
 
         // 2. Permutation.
