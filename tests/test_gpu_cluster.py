@@ -67,10 +67,12 @@ def expected_engine(forced, thr):
 JAC = golden_cases("jaccard")
 
 
+@pytest.mark.parametrize("partners", ["on", "off"])
 @pytest.mark.parametrize("engine", ["scan", "index", "auto"])
 @pytest.mark.parametrize("case", JAC, ids=[c["name"] for c in JAC])
-def test_gpu_clustering_matches_reference_golden(torch, case, engine, monkeypatch):
+def test_gpu_clustering_matches_reference_golden(torch, case, engine, partners, monkeypatch):
     monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    monkeypatch.setenv("XSPMM_CLUSTER_PARTNERS", partners)
     thr = float(case["thresh"])
     note(f"golden {case['name']} engine={engine} M={int(case['M'])} thr={thr}")
     perm, used = gpu_perm(torch, int(case["M"]), int(case["K"]), case["rp"], case["ci"], thr,
@@ -97,15 +99,29 @@ def skewed_csr(rng, M, K):
     return rp, ci
 
 
+@pytest.mark.parametrize("partners", ["on", "off"])
 @pytest.mark.parametrize("itype", [np.int32, np.int64])
 @pytest.mark.parametrize("engine", ["scan", "index"])
-@pytest.mark.parametrize("seed", range(6))
-def test_gpu_clustering_matches_oracle_random(torch, seed, engine, itype, monkeypatch):
+@pytest.mark.parametrize("seed", range(8))
+def test_gpu_clustering_matches_oracle_random(torch, seed, engine, itype, partners, monkeypatch):
     monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    monkeypatch.setenv("XSPMM_CLUSTER_PARTNERS", partners)
     rng = np.random.default_rng(900 + seed)
-    thr = [0.5, 0.4, 0.0, 0.5, 0.25, 0.7][seed]
-    bw = [16, 8, 16, 3, 16, 1][seed]
-    if seed % 3 == 0:
+    thr = [0.5, 0.4, 0.0, 0.5, 0.25, 0.7, 0.75, 0.6][seed]
+    bw = [16, 8, 16, 3, 16, 1, 16, 32][seed]
+    if seed >= 6:
+        # many joins: rows drawn from a few patterns with small perturbations
+        M, K = 3000, 2048 if seed == 6 else 9000
+        base = [rng.choice(K, size=int(rng.integers(5, 40)), replace=False) for _ in range(40)]
+        rows = []
+        for r in range(M):
+            b = base[int(rng.integers(0, len(base)))]
+            keep = b[rng.random(len(b)) < 0.9]
+            rows.append(np.concatenate([keep, rng.integers(0, K, size=int(rng.integers(0, 3)))]))
+        rp = np.zeros(M + 1, np.int64)
+        rp[1:] = np.cumsum([len(x) for x in rows])
+        ci = np.concatenate(rows).astype(np.int64)
+    elif seed % 3 == 0:
         M, K = int(rng.integers(100, 3000)), int(rng.integers(64, 5000))
         p = synth.random_csr(M, K, 4, float(rng.uniform(0.001, 0.02)), seed=seed,
                              dtype=np.float32, unsorted=bool(seed % 2))
@@ -116,7 +132,8 @@ def test_gpu_clustering_matches_oracle_random(torch, seed, engine, itype, monkey
     else:
         M, K = int(rng.integers(500, 2500)), int(rng.integers(100, 3000))
         rp, ci = skewed_csr(rng, M, K)
-    note(f"random seed={seed} engine={engine} itype={np.dtype(itype).name} M={M} K={K} thr={thr} bw={bw}")
+    note(f"random seed={seed} engine={engine} partners={partners} itype={np.dtype(itype).name} "
+         f"M={M} K={K} thr={thr} bw={bw}")
     want = oracle.jaccard(M, K, rp, ci, thr, bw)
     got, used = gpu_perm(torch, M, K, rp, ci, thr, bw, itype)
     assert got.dtype == itype

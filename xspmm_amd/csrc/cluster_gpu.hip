@@ -30,8 +30,11 @@
 // lowers the scan limit, and each step without a commit lowers it by 1024.
 //
 // Preparation (all rows in parallel): row bitmaps by atomic OR, their
-// popcounts, each row's block list, and the per-block row lists (counts,
-// exclusive scan, scatter).
+// popcounts, each row's block list, the per-block row lists (counts,
+// exclusive scan, scatter) and each row's partners -- the rows close enough
+// to join it while the pattern is still its own.  A seed whose partners are
+// all clustered forms a cluster of one without a scan, and any other seed
+// starts its scan at its highest-positioned partner.
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -60,11 +63,16 @@ __device__ __forceinline__ float jaccard_distance(int inter, int uni)
     return 1.0f - __fdiv_rn((float)inter, (float)uni);
 }
 
-// Agent-scope fence plus barrier: global stores, atomics and plain loads of
-// every wave are ordered across the phase boundary.
+// Phase boundary of the clustering workgroup: every wave waits until its
+// global stores and atomics are acknowledged, then the barrier.  All waves
+// share one CU, so plain loads after the barrier see plain stores from
+// before it; the counters (cnt) live at L2 and are only touched by L2
+// atomics and L1-bypassing atomic loads/stores.  (An agent-scope fence
+// would also write back and invalidate the L2 -- far slower, and not
+// needed inside one workgroup.)
 __device__ __forceinline__ void phase_sync()
 {
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 }
 
@@ -232,6 +240,145 @@ __global__ void reversed_perm_kernel(I* perm, int64_t M)
         perm[i] = (I)(M - 1 - i);
 }
 
+// --- partner lists -------------------------------------------------------------
+// Row j is a partner of row i (j != i) when d(q_i, q_j) <= dist_thresh.  Until
+// the first join of a cluster the pattern is exactly q_seed, so its first
+// joiner is the highest-position unclustered partner of the seed, and a seed
+// without one stays alone.  Lists hold up to kPartnerCap rows; pn[i] = -1
+// marks a row whose list was not computed or overflowed (it then takes the
+// full path).  Partnership is symmetric and fixed, so the lists are computed
+// for all rows at once, in parallel.
+
+constexpr int kPartnerCap = 32;
+constexpr int kPairRows = 64;    // bitmap method: rows i per workgroup
+constexpr int kPairTile = 128;   // rows j per LDS tile
+constexpr int kHashSlots = 16384;
+
+// All pairs by bitmap popcounts (row bitmaps of at most MAXW words).
+// 256 threads: 64 rows i, four threads per row splitting each tile.
+template <int MAXW>
+__global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __restrict__ bits,
+                                                              const int32_t* __restrict__ count,
+                                                              int M, int W, float thr,
+                                                              int32_t* pn, int32_t* partners)
+{
+    __shared__ uint64_t tile[kPairTile * MAXW];
+    __shared__ int32_t tcount[kPairTile];
+    __shared__ int32_t npart[kPairRows];
+    const int t = threadIdx.x;
+    const int li = t & (kPairRows - 1);
+    const int part = t / kPairRows;
+    const int i = blockIdx.x * kPairRows + li;
+    const bool vi = i < M;
+    uint64_t q[MAXW];
+#pragma unroll
+    for (int w = 0; w < MAXW; ++w) q[w] = (vi && w < W) ? bits[(int64_t)i * W + w] : 0ULL;
+    const int qc = vi ? count[i] : 0;
+    if (t < kPairRows) npart[t] = 0;
+    for (int j0 = 0; j0 < M; j0 += kPairTile) {
+        __syncthreads();
+        for (int x = t; x < kPairTile * MAXW; x += 256) {
+            const int jj = x / MAXW, w = x % MAXW;
+            const int j = j0 + jj;
+            tile[x] = (j < M && w < W) ? bits[(int64_t)j * W + w] : 0ULL;
+        }
+        for (int jj = t; jj < kPairTile; jj += 256) tcount[jj] = j0 + jj < M ? count[j0 + jj] : 0;
+        __syncthreads();
+        if (!vi) continue;
+        for (int jj = part; jj < kPairTile; jj += 256 / kPairRows) {
+            const int j = j0 + jj;
+            if (j >= M || j == i) continue;
+            const int qj = tcount[jj];
+            const int mn = qj < qc ? qj : qc, mx = qj < qc ? qc : qj;
+            if (jaccard_distance(mn, mx) > thr) continue;
+            int inter = 0, uni = 0;
+#pragma unroll
+            for (int w = 0; w < MAXW; ++w) {
+                const uint64_t y = tile[jj * MAXW + w];
+                inter += __popcll(q[w] & y);
+                uni += __popcll(q[w] | y);
+            }
+            if (jaccard_distance(inter, uni) <= thr) {
+                const int k = atomicAdd(&npart[li], 1);
+                if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
+            }
+        }
+    }
+    __syncthreads();
+    if (t < kPairRows && vi) pn[i] = npart[t] > kPartnerCap ? -1 : npart[t];
+}
+
+// Pairs through the per-block row lists: one workgroup per row i counts
+// |q_i & q_j| for the rows j it meets in an LDS hash table.  Only rows whose
+// popcount bound allows a join are inserted; a row whose table would pass
+// half full, and empty rows (their partners are the other empty rows, which
+// share no block), get pn = -1.
+__global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64_t* __restrict__ rb_start,
+                                                             const int32_t* __restrict__ rb,
+                                                             const int64_t* __restrict__ bl_start,
+                                                             const int32_t* __restrict__ bl_rows,
+                                                             const int32_t* __restrict__ count,
+                                                             float thr, int32_t* pn, int32_t* partners)
+{
+    __shared__ int32_t hkey[kHashSlots];
+    __shared__ int32_t hval[kHashSlots];
+    __shared__ int s_n, s_over, s_np;
+    const int t = threadIdx.x;
+    for (int i = blockIdx.x; i < M; i += gridDim.x) {
+        const int qi = count[i];
+        if (qi == 0) {
+            if (t == 0) pn[i] = -1;
+            continue;
+        }
+        for (int h = t; h < kHashSlots; h += 1024) {
+            hkey[h] = -1;
+            hval[h] = 0;
+        }
+        if (t == 0) {
+            s_n = 0;
+            s_over = 0;
+            s_np = 0;
+        }
+        __syncthreads();
+        const int64_t rs = rb_start[i];
+        for (int k = 0; k < qi; ++k) {
+            const int32_t b = rb[rs + k];
+            for (int64_t e = bl_start[b] + t; e < bl_start[b + 1]; e += 1024) {
+                const int32_t j = bl_rows[e];
+                if (j == i || s_over) continue;
+                const int qj = count[j];
+                const int mn = qj < qi ? qj : qi, mx = qj < qi ? qi : qj;
+                if (jaccard_distance(mn, mx) > thr) continue;
+                uint32_t h = ((uint32_t)j * 2654435761u) & (kHashSlots - 1);
+                for (int probe = 0; probe < kHashSlots; ++probe) {
+                    const int32_t old = atomicCAS(&hkey[h], -1, j);
+                    if (old == -1 || old == j) {
+                        if (old == -1 && atomicAdd(&s_n, 1) >= kHashSlots / 2) s_over = 1;
+                        atomicAdd(&hval[h], 1);
+                        break;
+                    }
+                    h = (h + 1) & (kHashSlots - 1);
+                }
+            }
+        }
+        __syncthreads();
+        if (!s_over) {
+            for (int h = t; h < kHashSlots; h += 1024) {
+                const int32_t j = hkey[h];
+                if (j < 0) continue;
+                const int inter = hval[h];
+                if (jaccard_distance(inter, qi + count[j] - inter) <= thr) {
+                    const int k = atomicAdd(&s_np, 1);
+                    if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
+                }
+            }
+        }
+        __syncthreads();
+        if (t == 0) pn[i] = (s_over || s_np > kPartnerCap) ? -1 : s_np;
+        __syncthreads();
+    }
+}
+
 struct ClusterArgs {
     int64_t M, W, Kb;
     float thresh;
@@ -249,6 +396,8 @@ struct ClusterArgs {
     int32_t* cand_a;          // candidate lists (compacted each round)
     int32_t* cand_b;
     int32_t* plist;           // blocks of the pattern
+    const int32_t* pn;        // partner counts (-1: unknown), or null
+    const int32_t* partners;  // M x kPartnerCap partner rows
     int* engine_used;
 };
 
@@ -296,16 +445,38 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     int n_un = M;  // every thread holds the same loop state
     int out = 0;
 
+    // Highest position of an unclustered partner of `seed` (-1: none), or
+    // -2 when the seed's partner list is unknown.  Two barriers.
+    auto first_partner = [&](int seed) -> int {
+        const int np = a.pn ? a.pn[seed] : -1;
+        if (np < 0) return -2;
+        int key = -1;
+        if (t < np) {
+            const int pr = a.pos[a.partners[(int64_t)seed * kPartnerCap + t]];
+            if (pr >= 0) key = pr;
+        }
+        return block_max(key, red);
+    };
+
     if (engine == kEngineScan) {
         while (n_un > 0) {
             const int seed = a.un[n_un - 1];
             --n_un;
-            if (t == 0) perm[out] = (I)seed;
+            if (t == 0) {
+                perm[out] = (I)seed;
+                a.pos[seed] = -1;
+            }
             ++out;
+            // positions above the first partner cannot join: start there
+            const int fp = first_partner(seed);
+            if (fp == -1) {
+                phase_sync();
+                continue;  // no unclustered partner: a cluster of one
+            }
             for (int w = t; w < W; w += kClThreads) p64[w] = a.bits[(int64_t)seed * W + w];
             int pc = a.count[seed];
-            int hi = n_un - 1;  // highest position not yet visited
-            __syncthreads();
+            int hi = fp >= 0 ? fp : n_un - 1;  // highest position not yet visited
+            phase_sync();
             while (hi >= 0) {
                 const int at = hi - t;
                 int key = -1;
@@ -339,7 +510,10 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
                 pc += (int)block_sum64(add, red64);
                 if (t == 0) {
                     perm[out] = (I)c;
-                    a.un[best] = a.un[n_un - 1];
+                    const int moved = a.un[n_un - 1];
+                    a.un[best] = moved;
+                    a.pos[moved] = best;
+                    a.pos[c] = -1;
                 }
                 ++out;
                 --n_un;
@@ -429,6 +603,9 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
             continue;
         }
 
+        const int fp = first_partner(seed);
+        if (fp == -1) continue;  // no unclustered partner: a cluster of one
+
         // pattern := blocks of the seed
         {
             const int64_t rs = a.rb_start[seed];
@@ -440,7 +617,9 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
             }
         }
         int pc = a.count[seed];
-        int limit = n_un;  // positions below limit are not yet visited
+        // positions below limit are not yet visited; those above the first
+        // partner cannot join and are skipped
+        int limit = fp >= 0 ? fp + 1 : n_un;
         int32_t* cur = a.cand_a;
         int32_t* nxt = a.cand_b;
         phase_sync();
@@ -582,6 +761,37 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     Scratch plist((size_t)nb * sizeof(int32_t), s);
     XSPMM_HIP_CHECK(hipMemsetAsync(cnt.get(), 0, (size_t)M * sizeof(int32_t), s));
 
+    // partner lists (XSPMM_CLUSTER_PARTNERS=off leaves every seed on the full path)
+    Scratch pn((size_t)M * sizeof(int32_t), s);
+    Scratch partners((size_t)M * kPartnerCap * sizeof(int32_t), s);
+    bool use_partners = true;
+    if (const char* e = std::getenv("XSPMM_CLUSTER_PARTNERS"))
+        use_partners = std::strcmp(e, "off") != 0;
+    if (use_partners) {
+        const int Mi = (int)M, Wi = (int)W;
+        if (W <= 32 && (double)M * (double)M * (double)W <= 6.4e10) {
+            const dim3 g((unsigned)((M + kPairRows - 1) / kPairRows));
+            if (W <= 8)
+                hipLaunchKernelGGL(partners_bitmap_kernel<8>, g, dim3(256), 0, s, bits.as<uint64_t>(),
+                                   count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
+                                   partners.as<int32_t>());
+            else if (W <= 16)
+                hipLaunchKernelGGL(partners_bitmap_kernel<16>, g, dim3(256), 0, s, bits.as<uint64_t>(),
+                                   count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
+                                   partners.as<int32_t>());
+            else
+                hipLaunchKernelGGL(partners_bitmap_kernel<32>, g, dim3(256), 0, s, bits.as<uint64_t>(),
+                                   count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
+                                   partners.as<int32_t>());
+        } else {
+            hipLaunchKernelGGL(partners_index_kernel, dim3((unsigned)std::min<int64_t>(M, 1024)),
+                               dim3(1024), 0, s, Mi, rb_start.as<int64_t>(), rb.as<int32_t>(),
+                               bl_start.as<int64_t>(), bl_rows.as<int32_t>(), count.as<int32_t>(),
+                               dist_thresh, pn.as<int32_t>(), partners.as<int32_t>());
+        }
+        XSPMM_LAUNCH_CHECK();
+    }
+
     int engine = kEngineAuto;
     if (const char* e = std::getenv("XSPMM_CLUSTER_ENGINE")) {
         if (std::strcmp(e, "scan") == 0) engine = kEngineScan;
@@ -591,7 +801,8 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
                      rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
                      bl_rows.as<int32_t>(), un.as<int32_t>(), pos.as<int32_t>(),
                      cnt.as<int32_t>(), logb.as<int32_t>(), ca.as<int32_t>(), cb.as<int32_t>(),
-                     plist.as<int32_t>(), bad + 1};
+                     plist.as<int32_t>(), use_partners ? pn.as<int32_t>() : nullptr,
+                     partners.as<int32_t>(), bad + 1};
     hipLaunchKernelGGL(cluster_kernel<I>, dim3(1), dim3(kClThreads), 0, s, args, perm);
     XSPMM_LAUNCH_CHECK();
     if (engine_used) {
