@@ -445,6 +445,39 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     int n_un = M;  // every thread holds the same loop state
     int out = 0;
 
+    // Clusters of one, up to 1024 at a time.  The next seeds are un[n_un-1],
+    // un[n_un-2], ... for as long as each stays alone, and the partner lists
+    // decide that up front: the seed at position `at` is alone iff it has a
+    // list and none of its partners is unclustered below `at` (partners above
+    // `at` are the seeds before it, clustered by its turn).  The longest run
+    // of such seeds is committed at once.
+    auto singleton_runs = [&]() {
+        if (!a.pn) return;
+        while (n_un > 0) {
+            const int at = n_un - 1 - t;
+            int s = -1;
+            bool alone = false;
+            if (at >= 0) {
+                s = a.un[at];
+                const int np = a.pn[s];
+                alone = np >= 0;
+                for (int e = 0; alone && e < np; ++e) {
+                    const int pr = a.pos[a.partners[(int64_t)s * kPartnerCap + e]];
+                    if (pr >= 0 && pr < at) alone = false;
+                }
+            }
+            const int run = -block_max(alone ? -kClThreads : -t, red);  // first seed not alone
+            if (t < run) {
+                perm[out + t] = (I)s;
+                a.pos[s] = -1;
+            }
+            out += run;
+            n_un -= run;
+            phase_sync();
+            if (run < kClThreads) return;
+        }
+    };
+
     // Highest position of an unclustered partner of `seed` (-1: none), or
     // -2 when the seed's partner list is unknown.  Two barriers.
     auto first_partner = [&](int seed) -> int {
@@ -460,6 +493,8 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
 
     if (engine == kEngineScan) {
         while (n_un > 0) {
+            singleton_runs();
+            if (n_un == 0) break;
             const int seed = a.un[n_un - 1];
             --n_un;
             if (t == 0) {
@@ -562,6 +597,8 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     };
 
     while (n_un > 0) {
+        singleton_runs();
+        if (n_un == 0) break;
         const int seed = a.un[n_un - 1];
         --n_un;
         if (t == 0) {
