@@ -247,7 +247,8 @@ __global__ void reversed_perm_kernel(I* perm, int64_t M)
 // without one stays alone.  Lists hold up to kPartnerCap rows; pn[i] = -1
 // marks a row whose list was not computed or overflowed (it then takes the
 // full path).  Partnership is symmetric and fixed, so the lists are computed
-// for all rows at once, in parallel.
+// for all rows at once, in parallel.  pn[i] > kPartnerCap also means
+// "overflowed": such a row takes the full path too.
 
 constexpr int kPartnerCap = 32;
 constexpr int kPairRows = 64;    // bitmap method: rows i per workgroup
@@ -255,7 +256,9 @@ constexpr int kPairTile = 128;   // rows j per LDS tile
 constexpr int kHashSlots = 16384;
 
 // All pairs by bitmap popcounts (row bitmaps of at most MAXW words).
-// 256 threads: 64 rows i, four threads per row splitting each tile.
+// 256 threads: 64 rows i, four threads per row splitting each tile; the
+// rows j are split over gridDim.y workgroups.  pn[i] (zeroed first) ends as
+// the number of partners of row i; the first kPartnerCap are listed.
 template <int MAXW>
 __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __restrict__ bits,
                                                               const int32_t* __restrict__ count,
@@ -264,7 +267,6 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
 {
     __shared__ uint64_t tile[kPairTile * MAXW];
     __shared__ int32_t tcount[kPairTile];
-    __shared__ int32_t npart[kPairRows];
     const int t = threadIdx.x;
     const int li = t & (kPairRows - 1);
     const int part = t / kPairRows;
@@ -274,8 +276,11 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
 #pragma unroll
     for (int w = 0; w < MAXW; ++w) q[w] = (vi && w < W) ? bits[(int64_t)i * W + w] : 0ULL;
     const int qc = vi ? count[i] : 0;
-    if (t < kPairRows) npart[t] = 0;
-    for (int j0 = 0; j0 < M; j0 += kPairTile) {
+    const int tiles = (M + kPairTile - 1) / kPairTile;
+    const int per = (tiles + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int jbeg = (int)blockIdx.y * per * kPairTile;
+    const int jend = min(M, jbeg + per * kPairTile);
+    for (int j0 = jbeg; j0 < jend; j0 += kPairTile) {
         __syncthreads();
         for (int x = t; x < kPairTile * MAXW; x += 256) {
             const int jj = x / MAXW, w = x % MAXW;
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
         if (!vi) continue;
         for (int jj = part; jj < kPairTile; jj += 256 / kPairRows) {
             const int j = j0 + jj;
-            if (j >= M || j == i) continue;
+            if (j >= jend || j == i) continue;
             const int qj = tcount[jj];
             const int mn = qj < qc ? qj : qc, mx = qj < qc ? qc : qj;
             if (jaccard_distance(mn, mx) > thr) continue;
@@ -299,13 +304,11 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
                 uni += __popcll(q[w] | y);
             }
             if (jaccard_distance(inter, uni) <= thr) {
-                const int k = atomicAdd(&npart[li], 1);
+                const int k = atomicAdd(&pn[i], 1);
                 if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
             }
         }
     }
-    __syncthreads();
-    if (t < kPairRows && vi) pn[i] = npart[t] > kPartnerCap ? -1 : npart[t];
 }
 
 // Pairs through the per-block row lists: one workgroup per row i counts
@@ -322,6 +325,9 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
 {
     __shared__ int32_t hkey[kHashSlots];
     __shared__ int32_t hval[kHashSlots];
+    __shared__ int32_t s_blk[1024];
+    __shared__ int64_t s_pre[1024];
+    __shared__ int64_t red64[kClWaves];
     __shared__ int s_n, s_over, s_np;
     const int t = threadIdx.x;
     for (int i = blockIdx.x; i < M; i += gridDim.x) {
@@ -341,10 +347,27 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
         }
         __syncthreads();
         const int64_t rs = rb_start[i];
-        for (int k = 0; k < qi; ++k) {
-            const int32_t b = rb[rs + k];
-            for (int64_t e = bl_start[b] + t; e < bl_start[b + 1]; e += 1024) {
-                const int32_t j = bl_rows[e];
+        for (int c0 = 0; c0 < qi; c0 += 1024) {
+            // the row's list entries, 1024 blocks at a time, as one flat range
+            const int nb = qi - c0 < 1024 ? qi - c0 : 1024;
+            int64_t len = 0;
+            if (t < nb) {
+                const int32_t b = rb[rs + c0 + t];
+                s_blk[t] = b;
+                len = bl_start[b + 1] - bl_start[b];
+            }
+            int64_t total;
+            const int64_t ex = block_exscan64(len, &total, red64);
+            if (t < nb) s_pre[t] = ex;
+            __syncthreads();
+            for (int64_t e = t; e < total; e += 1024) {
+                int lo = 0, hi = nb - 1;  // last block with s_pre <= e
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (s_pre[mid] <= e) lo = mid;
+                    else hi = mid - 1;
+                }
+                const int32_t j = bl_rows[bl_start[s_blk[lo]] + (e - s_pre[lo])];
                 if (j == i || s_over) continue;
                 const int qj = count[j];
                 const int mn = qj < qi ? qj : qi, mx = qj < qi ? qi : qj;
@@ -360,8 +383,8 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
                     h = (h + 1) & (kHashSlots - 1);
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
         if (!s_over) {
             for (int h = t; h < kHashSlots; h += 1024) {
                 const int32_t j = hkey[h];
@@ -460,7 +483,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
             if (at >= 0) {
                 s = a.un[at];
                 const int np = a.pn[s];
-                alone = np >= 0;
+                alone = np >= 0 && np <= kPartnerCap;
                 for (int e = 0; alone && e < np; ++e) {
                     const int pr = a.pos[a.partners[(int64_t)s * kPartnerCap + e]];
                     if (pr >= 0 && pr < at) alone = false;
@@ -482,7 +505,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     // -2 when the seed's partner list is unknown.  Two barriers.
     auto first_partner = [&](int seed) -> int {
         const int np = a.pn ? a.pn[seed] : -1;
-        if (np < 0) return -2;
+        if (np < 0 || np > kPartnerCap) return -2;
         int key = -1;
         if (t < np) {
             const int pr = a.pos[a.partners[(int64_t)seed * kPartnerCap + t]];
@@ -807,7 +830,11 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     if (use_partners) {
         const int Mi = (int)M, Wi = (int)W;
         if (W <= 32 && (double)M * (double)M * (double)W <= 6.4e10) {
-            const dim3 g((unsigned)((M + kPairRows - 1) / kPairRows));
+            XSPMM_HIP_CHECK(hipMemsetAsync(pn.get(), 0, (size_t)M * sizeof(int32_t), s));
+            // about 2048 workgroups: the rows j are split over grid.y
+            const int64_t gx = (M + kPairRows - 1) / kPairRows;
+            const int64_t tiles = (M + kPairTile - 1) / kPairTile;
+            const dim3 g((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(tiles, 2048 / gx)));
             if (W <= 8)
                 hipLaunchKernelGGL(partners_bitmap_kernel<8>, g, dim3(256), 0, s, bits.as<uint64_t>(),
                                    count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
