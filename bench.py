@@ -256,10 +256,18 @@ def main():
                      "alg_bytes_per_call": alg_bytes,
                      "padded_flops_per_call": 2.0 * nnzb * 256 * N})
 
-    stages = None
+    stages = stages_gpu = None
     if not args.no_pipeline:
         _, stages = X.spmm_pipeline(A, B, optimize_pattern=p.cluster)
         torch.cuda.synchronize()
+        if p.cluster:
+            # the same pipeline with the clustering stage on the GPU engine
+            os.environ["XSPMM_CLUSTER_DEVICE"] = "gpu"
+            try:
+                _, stages_gpu = X.spmm_pipeline(A, B, optimize_pattern=True)
+                torch.cuda.synchronize()
+            finally:
+                del os.environ["XSPMM_CLUSTER_DEVICE"]
 
     cpu = None
     if not args.no_cpu:
@@ -294,6 +302,7 @@ def main():
         "spot_check_rel_frob": spot,
         "prep": prep,
         "pipeline_stages_ms": stages,
+        "pipeline_stages_ms_gpu_clustering": stages_gpu,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -122,7 +122,8 @@ int xspmm_jaccard_clustering(int itype, int64_t M, int64_t K, int64_t nnz, const
 
 /*
  * Tier-2 pipeline on device CSR arrays rp/ci/vals, device B and C.
- * hw_block_size must be 16.  With optimize_pattern != 0: cluster ->
+ * hw_block_size must be 16.  With optimize_pattern != 0: cluster (host
+ * greedy; the GPU engine when the environment sets XSPMM_CLUSTER_DEVICE=gpu) ->
  * permute -> convert -> SpMM -> unpermute; else convert -> SpMM.  timings
  * (nullable, host) receives the six SpMMTimings fields in declaration order:
  * clustering, permutation, conversion, spmm, unpermutation, total (ms);

@@ -206,3 +206,37 @@ def test_gpu_clustering_power_law_graph_matches_host_engine(torch):
     got, used = gpu_perm(torch, p.M, p.K, p.rp, p.ci)
     note(f"gnn engine={used}")
     np.testing.assert_array_equal(widen(got), widen(want))
+
+
+def many_joins_csr(rng, M, K, n_patterns=40):
+    base = [rng.choice(K, size=int(rng.integers(5, 40)), replace=False) for _ in range(n_patterns)]
+    rows = []
+    for _ in range(M):
+        b = base[int(rng.integers(0, len(base)))]
+        keep = b[rng.random(len(b)) < 0.9]
+        rows.append(np.concatenate([keep, rng.integers(0, K, size=int(rng.integers(0, 3)))]))
+    rp = np.zeros(M + 1, np.int64)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    return rp, np.concatenate(rows).astype(np.int64)
+
+
+@pytest.mark.parametrize("itype", [np.int32, np.int64])
+@pytest.mark.parametrize("vdtype", [np.float16, np.float32])
+def test_pipeline_gpu_clustering_equals_host_clustering(torch, itype, vdtype, monkeypatch):
+    # XSPMM_CLUSTER_DEVICE=gpu only moves the clustering stage: C is identical
+    rng = np.random.default_rng(41)
+    M, K, N = 4000, 3000, 64
+    rp, ci = many_joins_csr(rng, M, K)
+    vals = rng.uniform(-1, 1, size=len(ci)).astype(vdtype)
+    A = X.CSRMatrix.from_host(M, K, rp.astype(itype), ci.astype(itype), vals)
+    B = torch.as_tensor(rng.uniform(-1, 1, size=(K, N)).astype(vdtype)).cuda()
+    monkeypatch.delenv("XSPMM_CLUSTER_DEVICE", raising=False)
+    C_host, _ = X.spmm_pipeline(A, B, optimize_pattern=True)
+    monkeypatch.setenv("XSPMM_CLUSTER_DEVICE", "gpu")
+    C_gpu, st = X.spmm_pipeline(A, B, optimize_pattern=True)
+    torch.cuda.synchronize()
+    assert torch.equal(C_host, C_gpu)
+    assert st["clustering_ms"] >= 0.0
+    perm_host = oracle.jaccard(M, K, rp, ci)
+    assert not np.array_equal(perm_host, np.arange(M - 1, -1, -1))  # the clustering joins rows
+

@@ -174,8 +174,8 @@ void spmm(const BCSRMatrix<InputType, IndexType>& A, const InputType* B, OutputT
 }
 
 // ---------------------------------------------------------------------------
-// Clustering: on the GPU for a HipExecutor (same permutation as the
-// reference's host greedy), on the host for a CpuExecutor
+// Clustering: the host greedy for every executor, as in the reference; a
+// HipExecutor can run the GPU engine instead (XSPMM_CLUSTER_DEVICE=gpu)
 // ---------------------------------------------------------------------------
 template <typename ValueType, typename IndexType>
 void compute_1d_jaccard_clustering(std::shared_ptr<const Executor> exec,
@@ -185,8 +185,8 @@ void compute_1d_jaccard_clustering(std::shared_ptr<const Executor> exec,
     const int64_t M = A.get_num_rows();
     if (M == 0) return;
     if (const HipExecutor* h = as_hip(exec)) {
-        // perm_out lives on the executor's device; the GPU engine gives the
-        // host greedy's permutation
+        // perm_out lives on the executor's device: host greedy on copies,
+        // or the GPU engine with XSPMM_CLUSTER_DEVICE=gpu (same permutation)
         use_device(h);
         DeviceCsr<ValueType, IndexType> v;
         device_view(A, v);

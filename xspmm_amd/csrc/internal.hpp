@@ -115,9 +115,10 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
 // blocks, row bitmaps within 16 GiB).
 bool clustering_device_supported(int64_t M, int64_t K, int64_t block_width);
 
-// Clustering of device CSR arrays into the device array d_perm: the GPU
-// engine, or the host greedy on copies when XSPMM_CLUSTER_DEVICE=host or the
-// shape is beyond the GPU engine.  Synchronizes `s`.
+// Clustering of device CSR arrays into the device array d_perm: the host
+// greedy on copies (the reference's placement), or the GPU engine when
+// XSPMM_CLUSTER_DEVICE=gpu and the shape is within its limits.  Both give the
+// same permutation.  Synchronizes `s`.
 template <typename I>
 void jaccard_clustering_dispatch(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                                  float dist_thresh, int64_t block_width, I* d_perm, hipStream_t s);

@@ -6,10 +6,10 @@
 //                   permute rows -> CSR->BCSR -> SpMM into C_temp ->
 //                   un-permute C_temp into C;
 //   clustering off: CSR->BCSR -> SpMM into C.
-// Every stage runs on the GPU: clustering too (the same permutation as the
-// reference's host greedy), unless XSPMM_CLUSTER_DEVICE=host or the shape is
-// beyond the GPU engine's limits, where the host greedy runs on copies of
-// row_ptr/col_ind.  Each timed stage is
+// Every stage except clustering runs on the GPU.  Clustering runs the host
+// greedy on copies of row_ptr/col_ind, as the reference does; with
+// XSPMM_CLUSTER_DEVICE=gpu it runs the GPU engine instead (the same
+// permutation), within that engine's shape limits.  Each timed stage is
 // bracketed by HIP events on the pipeline stream and waited for, so host work
 // inside a bracket counts too (the reference's HipTimer does the same).
 // Differences from the reference, with identical results: C / C_temp are not
@@ -69,8 +69,8 @@ void jaccard_clustering_dispatch(int64_t M, int64_t K, int64_t nnz, const I* rp,
     if (M == 0) return;
     if (block_width <= 0) throw std::invalid_argument("clustering: block_width must be positive.");
     const char* where = std::getenv("XSPMM_CLUSTER_DEVICE");
-    const bool host = where && std::strcmp(where, "host") == 0;
-    if (!host && clustering_device_supported(M, K, block_width)) {
+    const bool gpu = where && std::strcmp(where, "gpu") == 0;
+    if (gpu && clustering_device_supported(M, K, block_width)) {
         jaccard_clustering_device<I>(M, K, nnz, rp, ci, dist_thresh, block_width, d_perm, s, nullptr);
         return;
     }
