@@ -138,6 +138,43 @@ int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
                         float* C, int64_t N, int64_t hw_block_size, int optimize_pattern,
                         double* timings, void* stream);
 
+/*
+ * Prepared Tier-2 product ("plan"): the pipeline's clustering, permutation
+ * and CSR->BCSR stages run once at creation, on device CSR arrays rp/ci/vals
+ * (hw_block_size must be 16; clustering as in xspmm_spmm_pipeline); the plan
+ * keeps the permutation, the BCSR matrix and the SpMM dispatch order on the
+ * device and does not reference rp/ci/vals afterwards.  timings (nullable,
+ * host) receives the clustering, permutation, conversion and total fields
+ * of SpMMTimings (declaration order, six doubles); the spmm and
+ * unpermutation fields are left unchanged.  Synchronizes `stream`.
+ * No counterpart in the reference, whose pipeline repeats every stage per
+ * call (src/hip/unstructured_mtx_mul.hip:31-100); for callers that multiply
+ * the same matrix many times.
+ */
+typedef struct xspmm_plan_s* xspmm_plan_t;
+int xspmm_plan_create(int vtype, int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
+                      const void* ci, const void* vals, int64_t hw_block_size,
+                      int optimize_pattern, double* timings, void* stream, xspmm_plan_t* plan_out);
+
+/*
+ * C[M x N] (fp32, device) = A * B[K x N] (device, the plan's value type) with
+ * the plan's A, in the original row order: identical to xspmm_spmm_pipeline's
+ * C.  Asynchronous on `stream`.  On the fp16 path with N % 8 == 0 it is one
+ * kernel launch with the un-permutation fused into the store; otherwise it
+ * uses a device workspace kept by the plan (grown, with a synchronization,
+ * when N exceeds every earlier N).  Calls on one plan must not overlap.
+ */
+int xspmm_plan_execute(xspmm_plan_t plan, const void* B, float* C, int64_t N, void* stream);
+
+/* Block count, block-row count, whether the rows were clustered and the
+ * device permutation perm[new] = old (NULL when not clustered).  Any output
+ * pointer may be NULL. */
+int xspmm_plan_info(xspmm_plan_t plan, int64_t* num_blocks, int64_t* num_block_rows,
+                    int* clustered, const void** perm);
+
+/* Frees the plan's device memory (NULL is accepted). */
+int xspmm_plan_destroy(xspmm_plan_t plan);
+
 #ifdef __cplusplus
 }
 #endif

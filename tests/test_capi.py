@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     assert len(syms) >= 9
     for s in syms:
         assert hasattr(L, s), s
-    assert L.xspmm_abi_version() == 2
+    assert L.xspmm_abi_version() == 3
     assert L.xspmm_last_error() == b""
 
 
@@ -85,6 +85,24 @@ def test_device_clustering_argument_errors_without_gpu():
     assert f(9, 1, 16, 0, None, None, 0.5, 16, None, None, None) == X.ERR_INVALID
     # M = 0: nothing to cluster, no device work
     assert f(X.I64, 0, 16, 0, None, None, 0.5, 16, None, None, None) == X.OK
+
+
+def test_plan_argument_errors_without_gpu():
+    L = X.load()
+    h = C.c_void_p()
+    create = L.xspmm_plan_create
+    assert create(X.F16, X.I32, 4, 4, 0, None, None, None, 16, 1, None, None, None) == X.ERR_INVALID
+    assert b"plan_out" in L.xspmm_last_error()
+    assert create(X.F16, X.I32, 4, 4, 0, None, None, None, 8, 1, None, None,
+                  C.byref(h)) == X.ERR_INVALID
+    assert b"hw_block_size" in L.xspmm_last_error() and h.value is None
+    assert create(X.F16, X.I32, -4, 4, 0, None, None, None, 16, 1, None, None,
+                  C.byref(h)) == X.ERR_INVALID
+    assert create(5, X.I32, 4, 4, 0, None, None, None, 16, 1, None, None,
+                  C.byref(h)) == X.ERR_INVALID
+    assert L.xspmm_plan_execute(None, None, None, 8, None) == X.ERR_INVALID
+    assert L.xspmm_plan_info(None, None, None, None, None) == X.ERR_INVALID
+    assert L.xspmm_plan_destroy(None) == X.OK
 
 
 JAC = golden_cases("jaccard")

@@ -76,6 +76,16 @@ def load():
     L.xspmm_jaccard_clustering.restype = i32
     L.xspmm_jaccard_clustering.argtypes = [i32, i64, i64, i64, p, p, C.c_float, i64, p,
                                            C.POINTER(C.c_int), p]
+    L.xspmm_plan_create.restype = i32
+    L.xspmm_plan_create.argtypes = [i32, i32, i64, i64, i64, p, p, p, i64, i32,
+                                    C.POINTER(C.c_double), p, C.POINTER(C.c_void_p)]
+    L.xspmm_plan_execute.restype = i32
+    L.xspmm_plan_execute.argtypes = [p, p, p, i64, p]
+    L.xspmm_plan_info.restype = i32
+    L.xspmm_plan_info.argtypes = [p, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                  C.POINTER(C.c_int), C.POINTER(C.c_void_p)]
+    L.xspmm_plan_destroy.restype = i32
+    L.xspmm_plan_destroy.argtypes = [p]
     L.xspmm_spmm_pipeline.restype = i32
     L.xspmm_spmm_pipeline.argtypes = [i32, i32, i64, i64, i64, p, p, p, p, p, i64, i64, i32,
                                       C.POINTER(C.c_double), p]
@@ -313,3 +323,57 @@ def spmm_pipeline(A: CSRMatrix, B, C_out=None, N: int | None = None, hw_block_si
                                  C.cast(t, C.POINTER(C.c_double)) if t is not None else None,
                                  _stream()))
     return C_out, (dict(zip(TIMING_FIELDS, list(t))) if t is not None else None)
+
+
+class SpMMPlan:
+    """Prepared Tier-2 product (C ABI xspmm_plan_*): the pipeline's clustering,
+    permutation and CSR->BCSR stages run once here; execute() multiplies with
+    the Tier-1 SpMM alone (un-permutation fused into the fp16 kernel's store)
+    and returns the same C as spmm_pipeline(A, B, ...).  `timings` holds the
+    preparation stage times.  No counterpart in the reference."""
+
+    def __init__(self, A: CSRMatrix, hw_block_size: int = 16, optimize_pattern: bool = True):
+        L = load()
+        self._L = L
+        self._h = None
+        self.num_rows, self.num_cols = A.num_rows, A.num_cols
+        self.value_dtype = A.values.dtype
+        self.device = A.row_ptr.device
+        t = (C.c_double * 6)()
+        h = C.c_void_p()
+        _check(L.xspmm_plan_create(vcode(A.values.dtype), icode(A.row_ptr.dtype), A.num_rows,
+                                   A.num_cols, A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind),
+                                   _ptr(A.values), hw_block_size, 1 if optimize_pattern else 0,
+                                   C.cast(t, C.POINTER(C.c_double)), _stream(), C.byref(h)))
+        self._h = h
+        self.timings = {k: v for k, v in zip(TIMING_FIELDS, list(t))
+                        if k in ("clustering_ms", "permutation_ms", "conversion_ms",
+                                 "total_pipeline_ms")}
+        nb, nbr, cl = C.c_int64(), C.c_int64(), C.c_int()
+        _check(L.xspmm_plan_info(h, C.byref(nb), C.byref(nbr), C.byref(cl), None))
+        self.num_blocks, self.num_block_rows, self.clustered = nb.value, nbr.value, bool(cl.value)
+
+    def execute(self, B, C_out=None, N: int | None = None):
+        torch = _torch()
+        if self._h is None:
+            raise RuntimeError("SpMMPlan is closed")
+        if B.dtype != self.value_dtype:
+            raise TypeError("B must have the plan's value dtype")
+        if N is None:
+            N = int(B.shape[1])
+        if C_out is None:
+            C_out = torch.empty((self.num_rows, N), dtype=torch.float32, device=self.device)
+        _check(self._L.xspmm_plan_execute(self._h, _ptr(B), _ptr(C_out), N, _stream()))
+        return C_out
+
+    def close(self):
+        if self._h is not None:
+            self._L.xspmm_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+

@@ -19,6 +19,7 @@
 #include "internal.hpp"
 #include "xspmm/clustering.hpp"
 #include "xspmm/matrix/conversion.hpp"
+#include "xspmm/plan.hpp"
 #include "xspmm/xspmm.hpp"
 
 namespace xspmm {
@@ -341,6 +342,80 @@ void spmm(std::shared_ptr<const Executor> exec, const CSRMatrix<InputType, Index
 }
 
 // ---------------------------------------------------------------------------
+// Prepared Tier-2 product
+// ---------------------------------------------------------------------------
+template <typename ValueType, typename IndexType>
+SpMMPlan<ValueType, IndexType>::SpMMPlan(std::shared_ptr<const Executor> exec,
+                                         const CSRMatrix<ValueType, IndexType>& A,
+                                         IndexType hw_block_size, bool optimize_pattern,
+                                         SpMMTimings* timings)
+    : exec_(std::move(exec))
+{
+    const HipExecutor* h = as_hip(exec_);
+    if (!h) throw std::runtime_error("xSpMM: CPU pipeline fallback is not yet implemented.");
+    use_device(h);
+    DeviceCsr<ValueType, IndexType> src;
+    device_view(A, src);
+    impl_ = detail::make_plan<dev_t<ValueType>, IndexType>(
+        A.get_num_rows(), A.get_num_cols(), A.get_nnz(), src.d_rp, src.d_ci, dev(src.d_vals),
+        hw_block_size, optimize_pattern, timings ? reinterpret_cast<double*>(timings) : nullptr,
+        kStream);
+}
+
+template <typename ValueType, typename IndexType>
+SpMMPlan<ValueType, IndexType>::~SpMMPlan()
+{
+    if (impl_) {
+        if (const HipExecutor* h = as_hip(exec_)) (void)hipSetDevice(h->get_device_id());
+        delete impl_;
+    }
+}
+
+template <typename ValueType, typename IndexType>
+SpMMPlan<ValueType, IndexType>::SpMMPlan(SpMMPlan&& o) noexcept : exec_(std::move(o.exec_)), impl_(o.impl_)
+{
+    o.impl_ = nullptr;
+}
+
+template <typename ValueType, typename IndexType>
+SpMMPlan<ValueType, IndexType>& SpMMPlan<ValueType, IndexType>::operator=(SpMMPlan&& o) noexcept
+{
+    if (this != &o) {
+        delete impl_;
+        exec_ = std::move(o.exec_);
+        impl_ = o.impl_;
+        o.impl_ = nullptr;
+    }
+    return *this;
+}
+
+template <typename ValueType, typename IndexType>
+void SpMMPlan<ValueType, IndexType>::execute(const ValueType* B, float* C, IndexType N) const
+{
+    if (!impl_) throw std::runtime_error("xSpMM: empty (moved-from) plan.");
+    use_device(as_hip(exec_));
+    impl_->execute(dev(B), C, (int64_t)N, kStream);
+}
+
+template <typename ValueType, typename IndexType>
+IndexType SpMMPlan<ValueType, IndexType>::get_num_blocks() const
+{
+    return impl_ ? (IndexType)impl_->num_blocks() : 0;
+}
+
+template <typename ValueType, typename IndexType>
+bool SpMMPlan<ValueType, IndexType>::is_clustered() const
+{
+    return impl_ && impl_->clustered();
+}
+
+template <typename ValueType, typename IndexType>
+const IndexType* SpMMPlan<ValueType, IndexType>::get_permutation() const
+{
+    return impl_ ? static_cast<const IndexType*>(impl_->permutation()) : nullptr;
+}
+
+// ---------------------------------------------------------------------------
 // Explicit instantiations
 // ---------------------------------------------------------------------------
 #define XSPMM_INSTANTIATE(T, I)                                                                       \
@@ -352,7 +427,8 @@ void spmm(std::shared_ptr<const Executor> exec, const CSRMatrix<InputType, Index
     template CSRMatrix<T, I> apply_permutation<T, I>(std::shared_ptr<const Executor>,               \
                                                      const CSRMatrix<T, I>&, const I*);              \
     template BCSRMatrix<T, I> csr_to_bcsr<T, I>(std::shared_ptr<const Executor>,                    \
-                                                const CSRMatrix<T, I>&, I, I);
+                                                const CSRMatrix<T, I>&, I, I);                       \
+    template class SpMMPlan<T, I>;
 XSPMM_INSTANTIATE(float, int32_t)
 XSPMM_INSTANTIATE(float, int64_t)
 XSPMM_INSTANTIATE(__half, int32_t)

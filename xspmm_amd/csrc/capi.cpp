@@ -11,6 +11,11 @@
 
 using namespace xspmm::detail;
 
+// The opaque plan handle of the C ABI.
+struct xspmm_plan_s {
+    PlanBase* impl;
+};
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -73,7 +78,7 @@ extern "C" {
 
 const char* xspmm_last_error(void) { return g_last_error.c_str(); }
 
-int xspmm_abi_version(void) { return 2; }
+int xspmm_abi_version(void) { return 3; }
 
 int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
                     int64_t nnzb, const void* brp, const void* bci, const void* bvals,
@@ -195,6 +200,58 @@ int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
                                 static_cast<const T*>(vals), static_cast<const T*>(B), C, N,
                                 hw_block_size, optimize_pattern != 0, timings, as_stream(stream));
         });
+    });
+}
+
+int xspmm_plan_create(int vtype, int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
+                      const void* ci, const void* vals, int64_t hw_block_size,
+                      int optimize_pattern, double* timings, void* stream, xspmm_plan_t* plan_out)
+{
+    return guarded([&] {
+        require(plan_out != nullptr, "xspmm_plan_create: plan_out is null.");
+        *plan_out = nullptr;
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            require(M >= 0 && K >= 0 && nnz >= 0, "CSR dimensions must be non-negative.");
+            require(hw_block_size == 16,
+                    "xSpMM: the MFMA tile kernel requires hw_block_size == 16.");
+            PlanBase* impl = make_plan<T, I>(M, K, nnz, static_cast<const I*>(rp),
+                                             static_cast<const I*>(ci), static_cast<const T*>(vals),
+                                             hw_block_size, optimize_pattern != 0, timings,
+                                             as_stream(stream));
+            *plan_out = new xspmm_plan_s{impl};
+        });
+    });
+}
+
+int xspmm_plan_execute(xspmm_plan_t plan, const void* B, float* C, int64_t N, void* stream)
+{
+    return guarded([&] {
+        require(plan != nullptr, "xspmm_plan_execute: null plan.");
+        require(N >= 0, "xSpMM: negative N.");
+        plan->impl->execute(B, C, N, as_stream(stream));
+    });
+}
+
+int xspmm_plan_info(xspmm_plan_t plan, int64_t* num_blocks, int64_t* num_block_rows,
+                    int* clustered, const void** perm)
+{
+    return guarded([&] {
+        require(plan != nullptr, "xspmm_plan_info: null plan.");
+        if (num_blocks) *num_blocks = plan->impl->num_blocks();
+        if (num_block_rows) *num_block_rows = plan->impl->num_block_rows();
+        if (clustered) *clustered = plan->impl->clustered() ? 1 : 0;
+        if (perm) *perm = plan->impl->permutation();
+    });
+}
+
+int xspmm_plan_destroy(xspmm_plan_t plan)
+{
+    return guarded([&] {
+        if (!plan) return;
+        delete plan->impl;
+        delete plan;
     });
 }
 

@@ -19,6 +19,7 @@
 #include <xspmm/clustering.hpp>
 #include <xspmm/core/executor.hpp>
 #include <xspmm/matrix/conversion.hpp>
+#include <xspmm/plan.hpp>
 #include <xspmm/xspmm.hpp>
 
 namespace {
@@ -294,6 +295,58 @@ void check_errors(std::shared_ptr<const xspmm::Executor> gpu)
            std::to_string(ok1) + std::to_string(ok2) + std::to_string(ok3) + std::to_string(ok4));
 }
 
+// Prepared product: a plan's C equals the pipeline's C bit for bit, for
+// several N, after the source matrix is gone and after a move.
+template <typename T, typename I>
+void check_plan(std::shared_ptr<const xspmm::Executor> ex, bool cluster, const char* tname)
+{
+    const I M = 1000, N = 72;
+    auto h = checkers<I>(M, M, 4, 11);
+    std::vector<T> hv;
+    std::vector<T> hB((size_t)M * N);
+    std::mt19937 rng(3);
+    std::uniform_real_distribution<float> u(-1.0f, 1.0f);
+    for (auto& b : hB) b = T(u(rng));
+    T* d_B = nullptr;
+    float *d_C1 = nullptr, *d_C2 = nullptr;
+    ex->allocate(reinterpret_cast<void**>(&d_B), sizeof(T) * hB.size());
+    ex->allocate(reinterpret_cast<void**>(&d_C1), sizeof(float) * (size_t)M * N);
+    ex->allocate(reinterpret_cast<void**>(&d_C2), sizeof(float) * (size_t)M * N);
+    ex->copy_from_host(d_B, hB.data(), sizeof(T) * hB.size());
+    bool ok = true;
+    std::string detail;
+    xspmm::SpMMTimings t;
+    std::unique_ptr<xspmm::SpMMPlan<T, I>> plan;
+    {
+        auto A = upload<T, I>(ex, h, hv);
+        plan = std::make_unique<xspmm::SpMMPlan<T, I>>(ex, A, (I)16, cluster, &t);
+    }  // A freed: the plan keeps its own copies
+    xspmm::SpMMPlan<T, I> moved(std::move(*plan));
+    for (I n : {N, (I)8, (I)13, N}) {
+        std::vector<float> c1((size_t)M * n), c2((size_t)M * n);
+        {
+            auto A2 = upload<T, I>(ex, h, hv);
+            xspmm::spmm(ex, A2, d_B, d_C1, n, (I)16, cluster, nullptr);
+        }
+        moved.execute(d_B, d_C2, n);
+        ex->synchronize();
+        ex->copy_to_host(c1.data(), d_C1, sizeof(float) * c1.size());
+        ex->copy_to_host(c2.data(), d_C2, sizeof(float) * c2.size());
+        if (std::memcmp(c1.data(), c2.data(), sizeof(float) * c1.size()) != 0) {
+            ok = false;
+            detail += " mismatch at N=" + std::to_string((long long)n);
+        }
+    }
+    ok = ok && moved.get_num_blocks() > 0 && moved.is_clustered() == cluster &&
+         (moved.get_permutation() != nullptr) == cluster && t.total_pipeline_ms > 0 &&
+         (!cluster || t.clustering_ms > 0);
+    report(std::string("prepared plan ") + (cluster ? "clustered " : "plain ") + tname, ok,
+           detail + " prep_ms=" + std::to_string(t.total_pipeline_ms));
+    ex->free(d_B);
+    ex->free(d_C1);
+    ex->free(d_C2);
+}
+
 }  // namespace
 
 int main()
@@ -311,6 +364,9 @@ int main()
         check_cpu_gpu_conversion<int32_t>(ex);
         check_cpu_gpu_conversion<int64_t>(ex);
         check_errors(ex);
+        check_plan<__half, int32_t>(ex, true, "f16/i32");
+        check_plan<__half, int64_t>(ex, false, "f16/i64");
+        check_plan<float, int32_t>(ex, true, "f32/i32");
     } catch (const std::exception& e) {
         std::printf("[FAIL] exception: %s\n", e.what());
         return 2;

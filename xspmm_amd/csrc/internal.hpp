@@ -58,6 +58,42 @@ private:
     hipStream_t s_ = nullptr;
 };
 
+// Elapsed time of a stage bracketed by HIP events on stream s; stop() waits
+// for the stage and writes milliseconds.  A disabled timer does nothing.
+class StageTimer {
+public:
+    StageTimer(bool on, hipStream_t s) : on_(on), s_(s) {
+        if (on_) {
+            XSPMM_HIP_CHECK(hipEventCreate(&a_));
+            XSPMM_HIP_CHECK(hipEventCreate(&b_));
+        }
+    }
+    ~StageTimer() {
+        if (on_) {
+            (void)hipEventDestroy(a_);
+            (void)hipEventDestroy(b_);
+        }
+    }
+    StageTimer(const StageTimer&) = delete;
+    StageTimer& operator=(const StageTimer&) = delete;
+    void start() {
+        if (on_) XSPMM_HIP_CHECK(hipEventRecord(a_, s_));
+    }
+    void stop(double* out) {
+        if (!on_) return;
+        XSPMM_HIP_CHECK(hipEventRecord(b_, s_));
+        XSPMM_HIP_CHECK(hipEventSynchronize(b_));
+        float ms = 0.f;
+        XSPMM_HIP_CHECK(hipEventElapsedTime(&ms, a_, b_));
+        *out = (double)ms;
+    }
+
+private:
+    bool on_;
+    hipStream_t s_;
+    hipEvent_t a_ = nullptr, b_ = nullptr;
+};
+
 // Keeps freed stream-ordered memory in the device pool instead of returning
 // it to the driver at every synchronization (called once per device).
 void init_device_pool(int device);
@@ -73,8 +109,25 @@ template <typename T, typename I>
 void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
                const I* bci, const T* bvals, const T* B, float* C, int64_t N, hipStream_t s);
 
+// Tier-1 with a precomputed dispatch order (null: built here when useful, see
+// spmm_order_wanted) and an optional output row map: product row r is stored
+// in C row row_map[r] (row_map a permutation of [0, M)).  Returns false and
+// launches nothing when row_map is given but the selected kernel stores rows
+// in place; the caller then un-permutes a temporary.
+template <typename T, typename I>
+bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+                  const I* bci, const T* bvals, const T* B, float* C, int64_t N,
+                  const int32_t* order, const I* row_map, hipStream_t s);
+// Longest-block-row-first dispatch order of the fp16 batch kernel: whether
+// the grid is long enough to use one, and the kernel that writes it (Mb ids).
+bool spmm_order_wanted(int64_t Mb);
+template <typename I>
+void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s);
+
 // Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb).
-// Returns false (and launches nothing) when the shape is not covered.
+// Returns false (and launches nothing) when the shape is not covered;
+// spmm_dense_f16_covers tells in advance.
+bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N);
 bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
                          const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
                          hipStream_t s);
@@ -122,6 +175,25 @@ bool clustering_device_supported(int64_t M, int64_t K, int64_t block_width);
 template <typename I>
 void jaccard_clustering_dispatch(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                                  float dist_thresh, int64_t block_width, I* d_perm, hipStream_t s);
+
+// Prepared Tier-2 product: clustering, permutation and conversion done once
+// (plan.cpp); execute() runs the Tier-1 SpMM with the un-permutation fused
+// or through a kept workspace.  Value type erased for the C ABI.
+class PlanBase {
+public:
+    virtual ~PlanBase() = default;
+    virtual void execute(const void* B, float* C, int64_t N, hipStream_t s) = 0;
+    virtual int64_t num_blocks() const = 0;
+    virtual int64_t num_block_rows() const = 0;
+    virtual bool clustered() const = 0;
+    virtual const void* permutation() const = 0;  // device perm[M], or null
+};
+// Builds a plan on stream s (synchronizes it).  timings: null, or six doubles
+// laid out like SpMMTimings; the clustering, permutation, conversion and total
+// fields receive the preparation times.
+template <typename T, typename I>
+PlanBase* make_plan(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const T* vals,
+                    int64_t hw_block_size, bool optimize_pattern, double* timings, hipStream_t s);
 
 // Tier-2 pipeline on raw device pointers.  `timings` may be null; it points
 // at six doubles laid out like SpMMTimings.

@@ -25,41 +25,6 @@
 namespace xspmm {
 namespace detail {
 
-namespace {
-
-class StageTimer {
-public:
-    StageTimer(bool on, hipStream_t s) : on_(on), s_(s) {
-        if (on_) {
-            XSPMM_HIP_CHECK(hipEventCreate(&a_));
-            XSPMM_HIP_CHECK(hipEventCreate(&b_));
-        }
-    }
-    ~StageTimer() {
-        if (on_) {
-            (void)hipEventDestroy(a_);
-            (void)hipEventDestroy(b_);
-        }
-    }
-    void start() {
-        if (on_) XSPMM_HIP_CHECK(hipEventRecord(a_, s_));
-    }
-    void stop(double* out) {
-        if (!on_) return;
-        XSPMM_HIP_CHECK(hipEventRecord(b_, s_));
-        XSPMM_HIP_CHECK(hipEventSynchronize(b_));
-        float ms = 0.f;
-        XSPMM_HIP_CHECK(hipEventElapsedTime(&ms, a_, b_));
-        *out = (double)ms;
-    }
-
-private:
-    bool on_;
-    hipStream_t s_;
-    hipEvent_t a_ = nullptr, b_ = nullptr;
-};
-
-}  // namespace
 
 template <typename I>
 void jaccard_clustering_dispatch(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,

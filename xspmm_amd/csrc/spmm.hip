@@ -549,7 +549,8 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
                                                              const uint16_t* __restrict__ B,
                                                              float* __restrict__ C, int64_t M,
                                                              int64_t K, int64_t N, int64_t Kb,
-                                                             const int32_t* __restrict__ order)
+                                                             const int32_t* __restrict__ order,
+                                                             const I* __restrict__ row_map)
 {
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
@@ -798,7 +799,10 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
             const int o = row * 128 + c0 + e;
             out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
         }
-        float* dst = C + grow * N + n0 + c0;
+        // product row grow lands in C row row_map[grow] (the un-permutation
+        // of the clustered pipeline, fused into the store) or in row grow
+        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+        float* dst = C + crow * N + n0 + c0;
         if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
             *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
             *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
@@ -960,12 +964,31 @@ void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int
 
 }  // namespace
 
+bool spmm_order_wanted(int64_t Mb) { return Mb > kOrderMinRows && Mb <= 0x7fffffffLL; }
+
+template <typename I>
+void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s)
+{
+    hipLaunchKernelGGL((order_rows_kernel<I>), dim3(1), dim3(kOrderThreads), 0, s, brp, Mb, order);
+    XSPMM_LAUNCH_CHECK();
+}
+template void spmm_dispatch_order<int32_t>(const int32_t*, int64_t, int32_t*, hipStream_t);
+template void spmm_dispatch_order<int64_t>(const int64_t*, int64_t, int32_t*, hipStream_t);
+
 template <typename T, typename I>
 void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
                const I* bci, const T* bvals, const T* B, float* C, int64_t N, hipStream_t s)
 {
+    (void)bcsr_spmm_ex<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr, s);
+}
+
+template <typename T, typename I>
+bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+                  const I* bci, const T* bvals, const T* B, float* C, int64_t N,
+                  const int32_t* order_in, const I* row_map, hipStream_t s)
+{
     check_shape(M, K, Mb, Kb, nnzb, N);
-    if (M == 0 || N == 0 || Mb == 0) return;
+    if (M == 0 || N == 0 || Mb == 0) return true;
     const int64_t ntiles64 = (N + 15) / 16;
     if (ntiles64 > (1 << 24)) throw std::invalid_argument("xSpMM: N too large.");
     const int ntiles = (int)ntiles64;
@@ -979,10 +1002,12 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
         // batch and gather paths: byte offsets into B, and a wave's A range,
         // fit 32 bits; B row indices fit 24 bits
         const Fp16Kernel choice = fp16_kernel_choice();
-        // every block present: GEMM-tiled kernel (matrix-core bound)
-        if (choice == Fp16Kernel::kAuto &&
-            bcsr_spmm_dense_f16(M, K, Mb, Kb, nnzb, v, b, C, N, s))
-            return;
+        // every block present: GEMM-tiled kernel (matrix-core bound); it
+        // stores rows in place, so a row-mapped call is declined
+        if (choice == Fp16Kernel::kAuto && spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N)) {
+            if (row_map) return false;
+            return bcsr_spmm_dense_f16(M, K, Mb, Kb, nnzb, v, b, C, N, s);
+        }
         const bool offsets32 = K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
                                Kb < (int64_t(1) << 20);
         const int64_t chunks = (N + 127) / 128;
@@ -993,29 +1018,28 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
             // more block-rows than resident workgroups (4 per CU on 256 CUs,
             // times two): dispatch the longest rows first
             Scratch order_buf;
-            const int32_t* order = nullptr;
-            if (Mb > kOrderMinRows && Mb <= 0x7fffffffLL) {
+            const int32_t* order = order_in;
+            if (!order && spmm_order_wanted(Mb)) {
                 order_buf = Scratch((size_t)Mb * sizeof(int32_t), s);
-                hipLaunchKernelGGL((order_rows_kernel<I>), dim3(1), dim3(kOrderThreads), 0, s, brp,
-                                   Mb, order_buf.as<int32_t>());
-                XSPMM_LAUNCH_CHECK();
+                spmm_dispatch_order<I>(brp, Mb, order_buf.as<int32_t>(), s);
                 order = order_buf.as<int32_t>();
             }
             if (N <= 16)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order);
+                                   v, b, C, M, K, N, Kb, order, row_map);
             else if (N <= 32)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order);
+                                   v, b, C, M, K, N, Kb, order, row_map);
             else if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order);
+                                   v, b, C, M, K, N, Kb, order, row_map);
             else
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order);
+                                   v, b, C, M, K, N, Kb, order, row_map);
             XSPMM_LAUNCH_CHECK();
-            return;
+            return true;
         }
+        if (row_map) return false;  // the other fp16 kernels store rows in place
         if (choice == Fp16Kernel::kGather && N % 2 == 0 && offsets32) {
             if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_gather_kernel<I, 4, kGatherRows>), ggrid, dim3(256), 0, s, brp, bci,
@@ -1024,7 +1048,7 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
                 hipLaunchKernelGGL((spmm_f16_gather_kernel<I, 8, kGatherRows>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb);
             XSPMM_LAUNCH_CHECK();
-            return;
+            return true;
         }
         const int64_t Np = ntiles64 * 16;
         Scratch bt((size_t)(Kb > 0 ? Kb : 1) * (size_t)Np * 16 * sizeof(uint16_t), s);
@@ -1051,6 +1075,7 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
         }
         XSPMM_LAUNCH_CHECK();
     } else {
+        if (row_map) return false;  // the fp32 kernel stores rows in place
         const float* v = reinterpret_cast<const float*>(bvals);
         const float* b = reinterpret_cast<const float*>(B);
         switch (geo.ntw) {
@@ -1069,7 +1094,18 @@ void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const
         }
         XSPMM_LAUNCH_CHECK();
     }
+    return true;
 }
+
+#define XSPMM_SPMM_EX(T, I)                                                                  \
+    template bool bcsr_spmm_ex<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*,  \
+                                     const I*, const T*, const T*, float*, int64_t,          \
+                                     const int32_t*, const I*, hipStream_t);
+XSPMM_SPMM_EX(uint16_t, int32_t)
+XSPMM_SPMM_EX(uint16_t, int64_t)
+XSPMM_SPMM_EX(float, int32_t)
+XSPMM_SPMM_EX(float, int64_t)
+#undef XSPMM_SPMM_EX
 
 template void bcsr_spmm<uint16_t, int32_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
                                            const int32_t*, const int32_t*, const uint16_t*,

@@ -318,18 +318,32 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
 
 }  // namespace
 
+namespace {
+// workgroups of the dense grid: row groups padded to a multiple of the XCD
+// count (padding groups exit) times column groups
+int64_t dense_groups(int64_t Mb, int64_t N)
+{
+    const int64_t ncg = (N + kDN - 1) / kDN;
+    const int64_t nrg = (Mb + kDR - 1) / kDR;
+    return ((nrg + kXcds - 1) / kXcds) * kXcds * ncg;
+}
+}  // namespace
+
+bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N)
+{
+    (void)M;
+    if (nnzb != Mb * Kb || Mb <= 0 || Kb <= 0 || N <= 0) return false;
+    if (N % 8 != 0) return false;
+    if (Mb * Kb * 512 >= (int64_t(1) << 31) || K * N * 2 >= (int64_t(1) << 31)) return false;
+    return dense_groups(Mb, N) <= 0x7fffffffLL;
+}
+
 bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
                          const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
                          hipStream_t s)
 {
-    if (nnzb != Mb * Kb || Mb <= 0 || Kb <= 0 || N <= 0) return false;
-    if (N % 8 != 0) return false;
-    if (Mb * Kb * 512 >= (int64_t(1) << 31) || K * N * 2 >= (int64_t(1) << 31)) return false;
-    const int64_t ncg = (N + kDN - 1) / kDN;
-    const int64_t nrg = (Mb + kDR - 1) / kDR;
-    // row groups padded to a multiple of the XCD count; padding groups exit
-    const int64_t groups = ((nrg + kXcds - 1) / kXcds) * kXcds * ncg;
-    if (groups > 0x7fffffffLL) return false;
+    if (!spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N)) return false;
+    const int64_t groups = dense_groups(Mb, N);
     hipLaunchKernelGGL(spmm_f16_dense_kernel, dim3((unsigned)groups), dim3(kDThreads), 0, s, bvals, B, C,
                        M, K, N, Mb, Kb);
     XSPMM_LAUNCH_CHECK();
