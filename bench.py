@@ -269,6 +269,31 @@ def main():
             finally:
                 del os.environ["XSPMM_CLUSTER_DEVICE"]
 
+    # prepared product (plan): per-call time of execute(), which is the
+    # Tier-1 SpMM with the un-permutation fused and the dispatch order
+    # precomputed, against the pipeline's per-call SpMM + un-permutation
+    plan_info = None
+    if p.cluster and not args.no_pipeline:
+        plan = X.SpMMPlan(A)
+        Cp = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        for _ in range(args.warmup):
+            plan.execute(B, Cp)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            plan.execute(B, Cp)
+        b.record()
+        torch.cuda.synchronize()
+        Cq, _ = X.spmm_pipeline(A, B, optimize_pattern=True)
+        torch.cuda.synchronize()
+        plan_info = {"execute_ms": a.elapsed_time(b) / args.steps,
+                     "prepare_ms": plan.timings["total_pipeline_ms"],
+                     "equals_pipeline": bool(torch.equal(Cp, Cq))}
+        if stages:
+            plan_info["pipeline_spmm_plus_unpermute_ms"] = stages["spmm_ms"] + stages["unpermutation_ms"]
+        plan.close()
+
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -303,6 +328,7 @@ def main():
         "prep": prep,
         "pipeline_stages_ms": stages,
         "pipeline_stages_ms_gpu_clustering": stages_gpu,
+        "plan": plan_info,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
