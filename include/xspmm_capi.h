@@ -36,6 +36,7 @@ extern "C" {
 #define XSPMM_ERR_INVALID 1     /* bad argument (std::invalid_argument in C++) */
 #define XSPMM_ERR_HIP 2         /* HIP runtime error (std::runtime_error "HIP Error: ...") */
 #define XSPMM_ERR_UNSUPPORTED 3 /* valid request this build does not support */
+#define XSPMM_ERR_IO 4          /* file cannot be opened or parsed (MatrixMarket reader) */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* xspmm_last_error(void);
@@ -174,6 +175,26 @@ int xspmm_plan_info(xspmm_plan_t plan, int64_t* num_blocks, int64_t* num_block_r
 
 /* Frees the plan's device memory (NULL is accepted). */
 int xspmm_plan_destroy(xspmm_plan_t plan);
+
+/*
+ * MatrixMarket coordinate file -> host CSR, the same matrix as the
+ * reference's reader (utils/matrix_io.hpp:27-98, matrix_utils::io::read_mtx):
+ * comment/empty lines skipped, 1-based entries outside the matrix dropped,
+ * missing or unreadable values read as 1.0, no symmetric expansion, entries
+ * sorted by (row, column) with duplicates kept in file order.
+ * xspmm_mtx_read parses the file once into a handle (XSPMM_ERR_IO with the
+ * reference's message when it cannot be opened or has no readable dimension
+ * line); xspmm_mtx_info gives rows, cols and the number of entries kept;
+ * xspmm_mtx_export writes HOST arrays row_ptr[rows+1], col_ind[nnz] (index
+ * type code) and values[nnz] (value type code; fp16 rounded to nearest even
+ * from the float read); xspmm_mtx_free releases the handle (NULL accepted).
+ */
+typedef struct xspmm_mtx_s* xspmm_mtx_t;
+int xspmm_mtx_read(const char* path, xspmm_mtx_t* out);
+int xspmm_mtx_info(xspmm_mtx_t m, int64_t* rows, int64_t* cols, int64_t* nnz);
+int xspmm_mtx_export(xspmm_mtx_t m, int itype, int vtype, void* row_ptr, void* col_ind,
+                     void* values);
+int xspmm_mtx_free(xspmm_mtx_t m);
 
 #ifdef __cplusplus
 }

@@ -241,3 +241,150 @@ def ref_apply_perm(M, K, rp, ci, vals, perm, index_dtype=np.int64):
     getattr(R, "ref_apply_perm_" + name)(M, K, nnz, _ptr(rp), _ptr(ci), _ptr(v), _ptr(perm),
                                          _ptr(nrp), _ptr(nci), _ptr(nv))
     return nrp, nci[:nnz], nv[:nnz]
+
+
+# ---------------------------------------------------------------------------
+# MatrixMarket reader: restatement of the reference's utils/matrix_io.hpp:27-98
+# (matrix_utils::io::read_mtx<float>), plain Python.  The reference extracts
+# tokens with std::istringstream; the helpers below restate libstdc++'s
+# extraction rules for int and float (skip whitespace, the numeric grammar,
+# strtof on the accepted characters, failure on overflow) and use libc's
+# strtof for the rounding, as libstdc++ does.
+# ---------------------------------------------------------------------------
+
+_WS = b" \t\n\v\f\r"
+_libc = None
+
+
+def _strtof(tok: bytes):
+    """libc strtof on tok; None unless the whole token converts to a finite float."""
+    global _libc
+    if _libc is None:
+        _libc = C.CDLL(None)
+        _libc.strtof.restype = C.c_float
+        _libc.strtof.argtypes = [C.c_char_p, C.POINTER(C.c_char_p)]
+    buf = C.create_string_buffer(tok)
+    end = C.c_char_p()
+    v = _libc.strtof(buf, C.byref(end))
+    consumed = C.cast(end, C.c_void_p).value - C.cast(buf, C.c_void_p).value
+    if len(tok) == 0 or consumed != len(tok) or v in (float("inf"), float("-inf")):
+        return None
+    return np.float32(v)
+
+
+def _skip_ws(s: bytes, i: int) -> int:
+    while i < len(s) and s[i] in _WS:
+        i += 1
+    return i
+
+
+def _extract_int(s: bytes, i: int):
+    """`iss >> int`: optional sign, decimal digits, must fit int32."""
+    i = _skip_ws(s, i)
+    j = i
+    if j < len(s) and s[j] in b"+-":
+        j += 1
+    k = j
+    while k < len(s) and 48 <= s[k] <= 57:
+        k += 1
+    if k == j:
+        return None, k
+    v = int(s[i:k])
+    if not (-2**31 <= v < 2**31):
+        return None, k
+    return v, k
+
+
+def _extract_float(s: bytes, i: int):
+    """`iss >> float`: sign, digits, one '.', an exponent after a digit."""
+    i = _skip_ws(s, i)
+    j = i
+    if j < len(s) and s[j] in b"+-":
+        j += 1
+    mant = dot = sci = False
+    while j < len(s):
+        c = s[j]
+        if 48 <= c <= 57:
+            mant = True
+        elif c == 46 and not dot and not sci:
+            dot = True
+        elif c in b"eE" and not sci and mant:
+            sci = True
+            if j + 1 < len(s) and s[j + 1] in b"+-":
+                j += 1
+        else:
+            break
+        j += 1
+    return _strtof(s[i:j]), j
+
+
+def read_mtx(path):
+    """(M, K, rp int32, ci int32, vals float32) as the reference reads `path`:
+    lines that are empty or start with '%' are skipped; the first other line
+    gives rows, cols, nnz; each entry line gives 1-based row and column and a
+    value (1.0 when absent or unreadable); entries outside the matrix and
+    unreadable lines are dropped; entries are sorted by (row, column), equal
+    keys in file order (the reference's std::sort leaves them in file order for
+    the small duplicate cases tested); duplicates are kept."""
+    data = open(path, "rb").read()
+    lines = data.split(b"\n")
+    if lines and lines[-1] == b"":
+        lines.pop()
+    rows = cols = 0
+    k = 0
+    while k < len(lines):
+        line = lines[k]
+        k += 1
+        if not line or line[:1] == b"%":
+            continue
+        r, i = _extract_int(line, 0)
+        c, i = _extract_int(line, i) if r is not None else (None, i)
+        n, i = _extract_int(line, i) if c is not None else (None, i)
+        if n is None:
+            raise RuntimeError("Failed to parse MTX dimensions.")
+        rows, cols = r, c
+        break
+    el = []
+    for line in lines[k:]:
+        if not line or line[:1] == b"%":
+            continue
+        r, i = _extract_int(line, 0)
+        if r is None:
+            continue
+        c, i = _extract_int(line, i)
+        if c is None:
+            continue
+        v, _ = _extract_float(line, i)
+        if v is None:
+            v = np.float32(1.0)
+        if r < 1 or r > rows or c < 1 or c > cols:
+            continue
+        el.append((r - 1, c - 1, v))
+    el.sort(key=lambda e: (e[0], e[1]))
+    rp = np.zeros(max(rows, 0) + 1, np.int32)
+    for e in el:
+        rp[e[0] + 1] += 1
+    rp = np.cumsum(rp).astype(np.int32)
+    ci = np.array([e[1] for e in el], np.int32)
+    vals = np.array([e[2] for e in el], np.float32)
+    return rows, cols, rp, ci, vals
+
+
+def ref_read_mtx(path):
+    """The reference's own reader (oracle/_ref): (M, K, rp, ci, vals), or
+    raises RuntimeError with its message."""
+    R = ref()
+    R.ref_read_mtx.restype = C.c_int64
+    M, K = C.c_int32(), C.c_int32()
+    err = C.create_string_buffer(256)
+    p = os.fsencode(path)
+    nnz = R.ref_read_mtx(p, C.byref(M), C.byref(K), None, None, None, C.c_int64(-1), err, 256)
+    if nnz < 0:
+        raise RuntimeError(err.value.decode())
+    rp = np.zeros(max(M.value, 0) + 1, np.int32)
+    ci = np.zeros(max(nnz, 1), np.int32)
+    vals = np.zeros(max(nnz, 1), np.float32)
+    R.ref_read_mtx(p, C.byref(M), C.byref(K), _ptr(rp), _ptr(ci), _ptr(vals), C.c_int64(nnz),
+                   err, 256)
+    return M.value, K.value, rp, ci[:nnz], vals[:nnz]
+

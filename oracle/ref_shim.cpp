@@ -7,6 +7,9 @@
 // oracle/_ref/libxspmm_ref.so.  tests/golden/make_golden.py calls it through
 // ctypes to write golden vectors that pin the C restatement in oracle.c.
 //
+// The MatrixMarket reader is the reference's header utils/matrix_io.hpp
+// (matrix_utils::io::read_mtx<float>, :27-98), included where it lies.
+//
 // Everything runs on the reference's CpuExecutor (src/core/executor.cpp:44-72),
 // so "device" pointers are host memory.  The reference instantiates float
 // values only (src/core/conversion.cpp:106-108, src/xspmm.cpp:110-114), so
@@ -18,6 +21,7 @@
 #include "xspmm/clustering.hpp"
 #include "xspmm/core/executor.hpp"
 #include "xspmm/matrix/conversion.hpp"
+#include "matrix_io.hpp"
 
 namespace {
 
@@ -117,6 +121,32 @@ void ref_apply_perm_i64(int64_t M, int64_t K, int64_t nnz, const int64_t* rp, co
                         float* nvals)
 {
     apply_perm<int64_t>(M, K, nnz, rp, ci, vals, perm, nrp, nci, nvals);
+}
+
+// Reads `path` with the reference's reader.  Returns nnz (the number of
+// entries kept) and fills the outputs when nnz <= cap, or -1 with the
+// exception message in err.
+int64_t ref_read_mtx(const char* path, int32_t* M, int32_t* K, int32_t* rp, int32_t* ci,
+                     float* vals, int64_t cap, char* err, int32_t errlen)
+{
+    try {
+        auto h = matrix_utils::io::read_mtx<float>(path);
+        *M = h.num_rows;
+        *K = h.num_cols;
+        const int64_t nnz = (int64_t)h.values.size();
+        if (nnz <= cap) {
+            std::memcpy(rp, h.row_ptr.data(), sizeof(int32_t) * h.row_ptr.size());
+            if (nnz > 0) {
+                std::memcpy(ci, h.col_ind.data(), sizeof(int32_t) * (size_t)nnz);
+                std::memcpy(vals, h.values.data(), sizeof(float) * (size_t)nnz);
+            }
+        }
+        return nnz;
+    } catch (const std::exception& e) {
+        std::strncpy(err, e.what(), (size_t)errlen - 1);
+        err[errlen - 1] = '\0';
+        return -1;
+    }
 }
 
 }  // extern "C"

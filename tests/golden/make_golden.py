@@ -82,7 +82,68 @@ PERM_CASES = [
 ]
 
 
+# MatrixMarket inputs (text, written under mtx/): the reader's edge cases.
+def _mtx_cases(rng):
+    big = ["%%MatrixMarket matrix coordinate real general", "% random, unsorted, no duplicates",
+           "1000 800 5000"]
+    cells = rng.choice(1000 * 800, size=5000, replace=False)
+    for x in cells:
+        big.append(f"{x // 800 + 1} {x % 800 + 1} {rng.uniform(-2, 2):.6g}")
+    return {
+        "basic": "%%MatrixMarket matrix coordinate real general\n% comment\n"
+                 "4 5 6\n3 2 1.5\n1 1 -2\n4 5 7e-1\n1 5 3\n2 3 0.25\n3 1 8\n",
+        "pattern": "%%MatrixMarket matrix coordinate pattern general\n3 3 4\n1 2\n3 3\n2 1\n1 1\n",
+        "symmetric": "%%MatrixMarket matrix coordinate real symmetric\n4 4 5\n1 1 2\n2 1 -1\n"
+                     "3 2 -1\n4 3 -1\n4 4 2\n",
+        "integer_complex": "%%MatrixMarket matrix coordinate integer general\n3 4 4\n1 4 7\n"
+                           "2 2 -3\n3 1 1 9\n3 3 2.5 -1.5\n",
+        # CRLF, blank lines, indented comments, bad tokens, out-of-range
+        # entries, awkward numbers (overflow -> the reader's 1.0 default,
+        # underflow, partial exponents, signs, trailing text, inf/nan)
+        "messy": "%%MatrixMarket matrix coordinate real general\r\n%c\r\n 6 7 99\r\n\r\n"
+                 "1 1 1e50\r\n1 2 1e-50\r\n1 3 1e\r\n1 4 -.5\r\n1 5 +3\r\n1 6 .\r\n"
+                 "1 7 -\r\n2 1 2.5x\r\n2 2 0x1p3\r\n2 3 inf\r\n2 4 nan\r\n2 5\t\t4.75\r\n"
+                 "  % not a comment\r\nabc def\r\n1.5 2 3\r\n0 1 5\r\n7 1 5\r\n3 0 5\r\n"
+                 "3 8 5\r\n-1 2 5\r\n99999999999 1 5\r\n3 3 1e38\r\n3 4 3.4028236e38\r\n"
+                 "4 4 1.17549435e-38\r\n4 5 1e-45\r\n5 5 0.1\r\n5 6 1E+2\r\n6 7 1e+\r\n\r\n",
+        # a CRLF blank line is "\r", not empty: read as the dimension line
+        "crlf_blank_before_dims": "%%MatrixMarket matrix coordinate real general\r\n\r\n2 2 1\r\n1 1 1\r\n",
+        "duplicates": "%%MatrixMarket matrix coordinate real general\n3 3 6\n2 2 1\n1 3 4\n"
+                      "2 2 5\n1 3 6\n3 1 7\n2 2 9\n",
+        "no_entries": "%%MatrixMarket matrix coordinate real general\n5 3 0\n",
+        "only_comments": "%%MatrixMarket matrix coordinate real general\n% nothing else\n",
+        "bad_dims": "%%MatrixMarket matrix coordinate real general\nrows cols nnz\n1 1 1\n",
+        "no_final_newline": "%%MatrixMarket matrix coordinate real general\n2 2 2\n2 2 4\n1 1 3",
+        "random_1000x800": "\n".join(big) + "\n",
+    }
+
+
+def write_mtx_cases(rng):
+    d = os.path.join(HERE, "mtx")
+    os.makedirs(d, exist_ok=True)
+    n = 0
+    for name, text in _mtx_cases(rng).items():
+        path = os.path.join(d, name + ".mtx")
+        with open(path, "wb") as f:
+            f.write(text.encode())
+        try:
+            M, K, rp, ci, vals = oracle.ref_read_mtx(path)
+            np.savez_compressed(os.path.join(HERE, f"mtx_{name}.npz"), kind="mtx",
+                                source=f"mtx/{name}.mtx", M=M, K=K, rp=rp, ci=ci, vals=vals,
+                                error="")
+        except RuntimeError as e:
+            np.savez_compressed(os.path.join(HERE, f"mtx_{name}.npz"), kind="mtx",
+                                source=f"mtx/{name}.mtx", error=str(e))
+        n += 1
+    return n
+
+
 def main():
+    if "--only" in sys.argv and sys.argv[sys.argv.index("--only") + 1] == "mtx":
+        if not oracle.ref_available():
+            oracle.build()
+        print(f"wrote {write_mtx_cases(np.random.default_rng(77))} MatrixMarket cases")
+        return
     if not oracle.ref_available():
         oracle.build()
     if not oracle.ref_available():
@@ -117,6 +178,7 @@ def main():
                                 M=M, K=K, rp=rp.astype(it), ci=ci.astype(it), vals=vals,
                                 perm=perm.astype(it), nrp=nrp, nci=nci, nvals=nv)
             n += 1
+    n += write_mtx_cases(np.random.default_rng(77))
     print(f"wrote {n} golden cases to {HERE}")
 
 

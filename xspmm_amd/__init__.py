@@ -26,7 +26,7 @@ LIB_PATH = os.environ.get("XSPMM_LIBRARY") or os.path.join(HERE, "libxspmm.so")
 
 F32, F16 = 0, 1
 I32, I64 = 0, 1
-OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3
+OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_IO = 0, 1, 2, 3, 4
 
 TIMING_FIELDS = ("clustering_ms", "permutation_ms", "conversion_ms", "spmm_ms",
                  "unpermutation_ms", "total_pipeline_ms")
@@ -86,6 +86,15 @@ def load():
                                   C.POINTER(C.c_int), C.POINTER(C.c_void_p)]
     L.xspmm_plan_destroy.restype = i32
     L.xspmm_plan_destroy.argtypes = [p]
+    L.xspmm_mtx_read.restype = i32
+    L.xspmm_mtx_read.argtypes = [C.c_char_p, C.POINTER(C.c_void_p)]
+    L.xspmm_mtx_info.restype = i32
+    L.xspmm_mtx_info.argtypes = [p, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                 C.POINTER(C.c_int64)]
+    L.xspmm_mtx_export.restype = i32
+    L.xspmm_mtx_export.argtypes = [p, i32, i32, p, p, p]
+    L.xspmm_mtx_free.restype = i32
+    L.xspmm_mtx_free.argtypes = [p]
     L.xspmm_spmm_pipeline.restype = i32
     L.xspmm_spmm_pipeline.argtypes = [i32, i32, i64, i64, i64, p, p, p, p, p, i64, i64, i32,
                                       C.POINTER(C.c_double), p]
@@ -274,6 +283,29 @@ def jaccard_clustering(A: CSRMatrix, dist_thresh=0.5, block_width=16, return_eng
     if return_engine:
         return perm, CLUSTER_ENGINES.get(used.value, "none")
     return perm
+
+
+def read_mtx(path, index_dtype=np.int32, value_dtype=np.float32):
+    """MatrixMarket coordinate file -> (M, K, row_ptr, col_ind, values) as
+    host numpy arrays, the matrix the reference's reader gives
+    (utils/matrix_io.hpp:27-98).  Raises XspmmError (code ERR_IO) with the
+    reference's message when the file cannot be opened or parsed."""
+    L = load()
+    h = C.c_void_p()
+    _check(L.xspmm_mtx_read(os.fsencode(os.fspath(path)), C.byref(h)))
+    try:
+        M, K, n = C.c_int64(), C.c_int64(), C.c_int64()
+        _check(L.xspmm_mtx_info(h, C.byref(M), C.byref(K), C.byref(n)))
+        nnz = n.value
+        rp = np.zeros(max(M.value, 0) + 1, index_dtype)
+        ci = np.zeros(max(nnz, 1), index_dtype)
+        vals = np.zeros(max(nnz, 1), value_dtype)
+        _check(L.xspmm_mtx_export(h, icode(rp.dtype), vcode(vals.dtype),
+                                  rp.ctypes.data_as(C.c_void_p), ci.ctypes.data_as(C.c_void_p),
+                                  vals.ctypes.data_as(C.c_void_p)))
+    finally:
+        L.xspmm_mtx_free(h)
+    return M.value, K.value, rp, ci[:nnz], vals[:nnz]
 
 
 def apply_permutation(A: CSRMatrix, perm) -> CSRMatrix:

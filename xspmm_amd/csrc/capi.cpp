@@ -2,6 +2,8 @@
 // Each maps type codes onto the internal launchers and turns exceptions into
 // error codes (std::invalid_argument -> XSPMM_ERR_INVALID, "HIP Error" ->
 // XSPMM_ERR_HIP, any other failure -> XSPMM_ERR_UNSUPPORTED).
+#include <hip/hip_fp16.h>
+
 #include <cstring>
 #include <string>
 #include <utility>
@@ -11,9 +13,12 @@
 
 using namespace xspmm::detail;
 
-// The opaque plan handle of the C ABI.
+// The opaque handles of the C ABI.
 struct xspmm_plan_s {
     PlanBase* impl;
+};
+struct xspmm_mtx_s {
+    MtxData data;
 };
 
 namespace {
@@ -30,6 +35,9 @@ int guarded(F&& f)
     } catch (const std::invalid_argument& e) {
         g_last_error = e.what();
         return XSPMM_ERR_INVALID;
+    } catch (const MtxError& e) {
+        g_last_error = e.what();
+        return XSPMM_ERR_IO;
     } catch (const std::exception& e) {
         g_last_error = e.what();
         return std::strncmp(e.what(), "HIP Error", 9) == 0 ? XSPMM_ERR_HIP : XSPMM_ERR_UNSUPPORTED;
@@ -253,6 +261,60 @@ int xspmm_plan_destroy(xspmm_plan_t plan)
         delete plan->impl;
         delete plan;
     });
+}
+
+int xspmm_mtx_read(const char* path, xspmm_mtx_t* out)
+{
+    return guarded([&] {
+        require(out != nullptr && path != nullptr, "xspmm_mtx_read: null argument.");
+        *out = nullptr;
+        auto* m = new xspmm_mtx_s{read_matrix_market(path)};
+        *out = m;
+    });
+}
+
+int xspmm_mtx_info(xspmm_mtx_t m, int64_t* rows, int64_t* cols, int64_t* nnz)
+{
+    return guarded([&] {
+        require(m != nullptr, "xspmm_mtx_info: null handle.");
+        if (rows) *rows = m->data.rows;
+        if (cols) *cols = m->data.cols;
+        if (nnz) *nnz = (int64_t)m->data.values.size();
+    });
+}
+
+int xspmm_mtx_export(xspmm_mtx_t m, int itype, int vtype, void* row_ptr, void* col_ind,
+                     void* values)
+{
+    return guarded([&] {
+        require(m != nullptr, "xspmm_mtx_export: null handle.");
+        const MtxData& d = m->data;
+        const size_t nnz = d.values.size();
+        require(row_ptr != nullptr && (nnz == 0 || (col_ind != nullptr && values != nullptr)),
+                "xspmm_mtx_export: null output array.");
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            I* rp = static_cast<I*>(row_ptr);
+            I* ci = static_cast<I*>(col_ind);
+            for (size_t i = 0; i < d.row_ptr.size(); ++i) rp[i] = (I)d.row_ptr[i];
+            for (size_t k = 0; k < nnz; ++k) ci[k] = (I)d.col_ind[k];
+            T* v = static_cast<T*>(values);
+            for (size_t k = 0; k < nnz; ++k) {
+                if constexpr (sizeof(T) == 2) {
+                    const __half h = __float2half(d.values[k]);  // round to nearest even
+                    std::memcpy(&v[k], &h, 2);
+                } else {
+                    v[k] = d.values[k];
+                }
+            }
+        });
+    });
+}
+
+int xspmm_mtx_free(xspmm_mtx_t m)
+{
+    return guarded([&] { delete m; });
 }
 
 }  // extern "C"

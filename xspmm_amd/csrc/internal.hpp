@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "xspmm/core/executor.hpp"
 
@@ -194,6 +195,20 @@ public:
 template <typename T, typename I>
 PlanBase* make_plan(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const T* vals,
                     int64_t hw_block_size, bool optimize_pattern, double* timings, hipStream_t s);
+
+// MatrixMarket coordinate file read as the reference's reader does
+// (mtx.cpp): CSR with int indices, float values.
+struct MtxError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct MtxData {
+    int rows = 0, cols = 0;
+    std::vector<int> row_ptr, col_ind;
+    std::vector<float> values;
+    std::vector<int> r, c;  // entries before sorting (emptied afterwards)
+    std::vector<float> v;
+};
+MtxData read_matrix_market(const std::string& path);
 
 // Tier-2 pipeline on raw device pointers.  `timings` may be null; it points
 // at six doubles laid out like SpMMTimings.
