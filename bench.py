@@ -139,6 +139,43 @@ def calibrate_copy():
                       "launches": 3}), flush=True)
 
 
+def vendor_columns(Ap, Bm, B, C, ms, iters):
+    """The same product by rocSPARSE (CSR, BSR) and rocBLAS (dense A, when it
+    fits in 512 MB), each with its time and its relative Frobenius difference
+    from this library's C (same inputs, fp32 accumulation)."""
+    import torch
+    from xspmm_amd import vendor as V
+
+    def rel(Cv):
+        return float(torch.linalg.norm(Cv - C) / max(float(torch.linalg.norm(C)), 1e-30))
+
+    out = {"xspmm_ms": ms}
+    iters = max(5, min(iters, 50))
+    try:
+        if Ap.row_ptr.dtype == torch.int32:
+            Cv, t = V.csr_spmm(Ap, B, iters=iters)
+            out.update(rocsparse_csr_ms=t, rocsparse_csr_rel_diff=rel(Cv), speedup_vs_csr=t / ms)
+            Kp = Bm.num_block_cols * 16
+            Bp = B if Kp == B.shape[0] else torch.cat(
+                [B, torch.zeros((Kp - B.shape[0], B.shape[1]), dtype=B.dtype, device=B.device)])
+            Cv, t = V.bsr_spmm(Bm, Bp, iters=iters)
+            out.update(rocsparse_bsr_ms=t, rocsparse_bsr_rel_diff=rel(Cv), speedup_vs_bsr=t / ms)
+            del Cv
+        M, K = Ap.num_rows, Ap.num_cols
+        if M * K * B.element_size() <= (512 << 20):
+            D = torch.zeros((M, K), dtype=B.dtype, device=B.device)
+            lens = Ap.row_ptr[1:] - Ap.row_ptr[:-1]
+            rows = torch.repeat_interleave(torch.arange(M, device=B.device), lens.long())
+            D[rows, Ap.col_ind.long()] = Ap.values
+            Cv, t = V.dense_gemm(D, B, iters=iters)
+            out.update(rocblas_dense_ms=t, rocblas_dense_rel_diff=rel(Cv), speedup_vs_dense=t / ms)
+            del D, Cv
+        torch.cuda.synchronize()
+    except Exception as e:  # the comparison is context; report why it is missing
+        out["error"] = str(e)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,6 +185,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pipeline", action="store_true")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the rocSPARSE / rocBLAS comparison columns")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the known-size copy used to scale byte counters")
     args = ap.parse_args()
@@ -294,6 +333,10 @@ def main():
             plan_info["pipeline_spmm_plus_unpermute_ms"] = stages["spmm_ms"] + stages["unpermutation_ms"]
         plan.close()
 
+    vendor = None
+    if not args.no_vendor:
+        vendor = vendor_columns(Ap, Bm, B, C, ms, args.steps)
+
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -329,6 +372,7 @@ def main():
         "pipeline_stages_ms": stages,
         "pipeline_stages_ms_gpu_clustering": stages_gpu,
         "plan": plan_info,
+        "vendor": vendor,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
