@@ -161,9 +161,10 @@ int xspmm_plan_create(int vtype, int itype, int64_t M, int64_t K, int64_t nnz, c
  * C[M x N] (fp32, device) = A * B[K x N] (device, the plan's value type) with
  * the plan's A, in the original row order: identical to xspmm_spmm_pipeline's
  * C.  Asynchronous on `stream`.  On the fp16 path with N % 8 == 0 it is one
- * kernel launch with the un-permutation fused into the store; otherwise it
- * uses a device workspace kept by the plan (grown, with a synchronization,
- * when N exceeds every earlier N).  Calls on one plan must not overlap.
+ * kernel launch with the un-permutation fused into the store, which streams
+ * the plan's packed column batches when it has them; otherwise it uses a
+ * device workspace kept by the plan (grown, with a synchronization, when N
+ * exceeds every earlier N).  Calls on one plan must not overlap.
  */
 int xspmm_plan_execute(xspmm_plan_t plan, const void* B, float* C, int64_t N, void* stream);
 
@@ -172,6 +173,12 @@ int xspmm_plan_execute(xspmm_plan_t plan, const void* B, float* C, int64_t N, vo
  * pointer may be NULL. */
 int xspmm_plan_info(xspmm_plan_t plan, int64_t* num_blocks, int64_t* num_block_rows,
                     int* clustered, const void** perm);
+
+/* Number of packed column batches the plan multiplies from (fp16 plans of
+ * sparse blocks keep the SpMM kernel's batches -- A' operands and B-row
+ * indices -- instead of streaming the BCSR blocks), or -1 when the plan
+ * multiplies the BCSR matrix itself. */
+int xspmm_plan_packed_batches(xspmm_plan_t plan, int64_t* batches);
 
 /* Frees the plan's device memory (NULL is accepted). */
 int xspmm_plan_destroy(xspmm_plan_t plan);

@@ -101,6 +101,35 @@ def test_plan_on_a_full_block_grid(torch, cluster):
         assert torch.equal(C_pipe, C_plan), N
 
 
+@pytest.mark.parametrize("cluster", [True, False])
+@pytest.mark.parametrize("itype", [np.int32, np.int64])
+def test_packed_plan_equals_unpacked_plan_and_pipeline(torch, itype, cluster, monkeypatch):
+    # fp16 plans of sparse blocks keep the SpMM kernel's column batches; C is
+    # the same as multiplying the BCSR matrix (and as the pipeline's)
+    rng = np.random.default_rng(21)
+    M, K = 5001, 4000
+    rp, ci = many_joins(rng, M, K, n_patterns=200)
+    vals = rng.uniform(-1, 1, size=len(ci)).astype(np.float16)
+    vals[rng.random(len(vals)) < 0.05] = 0  # explicit zeros keep their columns' blocks
+    A = X.CSRMatrix.from_host(M, K, rp.astype(itype), ci.astype(itype), vals)
+    packed = X.SpMMPlan(A, optimize_pattern=cluster)
+    monkeypatch.setenv("XSPMM_PLAN_PACK", "off")
+    plain = X.SpMMPlan(A, optimize_pattern=cluster)
+    monkeypatch.delenv("XSPMM_PLAN_PACK")
+    note(f"packed batches {packed.packed_batches}, blocks {packed.num_blocks}")
+    assert packed.packed_batches > 0 and plain.packed_batches == -1
+    for N in (8, 64, 128, 200, 24, 12):
+        B = torch.as_tensor(rng.uniform(-1, 1, size=(K, N)).astype(np.float16)).cuda()
+        C1 = packed.execute(B)
+        C2 = plain.execute(B)
+        C3, _ = X.spmm_pipeline(A, B, optimize_pattern=cluster)
+        torch.cuda.synchronize()
+        assert torch.equal(C1, C2), N
+        assert torch.equal(C1, C3), N
+    packed.close()
+    plain.close()
+
+
 def test_plan_outlives_its_source_matrix(torch):
     rng = np.random.default_rng(8)
     M, K, N = 2000, 1800, 64

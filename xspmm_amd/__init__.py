@@ -84,6 +84,8 @@ def load():
     L.xspmm_plan_info.restype = i32
     L.xspmm_plan_info.argtypes = [p, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
                                   C.POINTER(C.c_int), C.POINTER(C.c_void_p)]
+    L.xspmm_plan_packed_batches.restype = i32
+    L.xspmm_plan_packed_batches.argtypes = [p, C.POINTER(C.c_int64)]
     L.xspmm_plan_destroy.restype = i32
     L.xspmm_plan_destroy.argtypes = [p]
     L.xspmm_mtx_read.restype = i32
@@ -384,6 +386,9 @@ class SpMMPlan:
         nb, nbr, cl = C.c_int64(), C.c_int64(), C.c_int()
         _check(L.xspmm_plan_info(h, C.byref(nb), C.byref(nbr), C.byref(cl), None))
         self.num_blocks, self.num_block_rows, self.clustered = nb.value, nbr.value, bool(cl.value)
+        pb = C.c_int64()
+        _check(L.xspmm_plan_packed_batches(h, C.byref(pb)))
+        self.packed_batches = pb.value  # -1: multiplies the BCSR matrix itself
 
     def execute(self, B, C_out=None, N: int | None = None):
         torch = _torch()

@@ -254,6 +254,14 @@ int xspmm_plan_info(xspmm_plan_t plan, int64_t* num_blocks, int64_t* num_block_r
     });
 }
 
+int xspmm_plan_packed_batches(xspmm_plan_t plan, int64_t* batches)
+{
+    return guarded([&] {
+        require(plan != nullptr && batches != nullptr, "xspmm_plan_packed_batches: null argument.");
+        *batches = plan->impl->num_packed_batches();
+    });
+}
+
 int xspmm_plan_destroy(xspmm_plan_t plan)
 {
     return guarded([&] {

@@ -125,6 +125,31 @@ bool spmm_order_wanted(int64_t Mb);
 template <typename I>
 void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s);
 
+// Packed column batches (fp16): the batches the Tier-1 batch kernel forms
+// for each (block-row, wave) -- their A' operands (1 KB each) and B-row
+// indices (32 per batch) -- stored once so that later products stream them
+// instead of the BCSR blocks.  count writes Mb * 4 batch counts (wave-major
+// per row); fill writes the batches at the exclusive-scan offsets of those
+// counts (Mb * 4 + 1 entries) into a (batches x 1 KB) and rows (batches x 32).
+// spmm_f16_packed multiplies them (same C as bcsr_spmm_ex on the BCSR matrix,
+// with the same order / row_map meaning); it returns false when N is not
+// covered (N % 8 != 0 or too large).
+bool spmm_f16_pack_supported(int64_t K, int64_t Mb, int64_t Kb);
+// offsets[0..n] = exclusive scan of counts[0..n-1]; returns offsets[n]
+// (synchronizes s).
+int64_t spmm_f16_pack_offsets(const int32_t* counts, int64_t n, int64_t* offsets, hipStream_t s);
+template <typename I>
+void spmm_f16_pack_count(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                         const uint16_t* bvals, int32_t* counts, hipStream_t s);
+template <typename I>
+void spmm_f16_pack_fill(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                        const uint16_t* bvals, const int64_t* offsets, void* a, uint32_t* rows,
+                        hipStream_t s);
+template <typename I>
+bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, const void* a,
+                     const uint32_t* rows, const uint16_t* B, float* C, int64_t N,
+                     const int32_t* order, const I* row_map, hipStream_t s);
+
 // Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb).
 // Returns false (and launches nothing) when the shape is not covered;
 // spmm_dense_f16_covers tells in advance.
@@ -186,6 +211,7 @@ public:
     virtual void execute(const void* B, float* C, int64_t N, hipStream_t s) = 0;
     virtual int64_t num_blocks() const = 0;
     virtual int64_t num_block_rows() const = 0;
+    virtual int64_t num_packed_batches() const = 0;  // -1 when not packed
     virtual bool clustered() const = 0;
     virtual const void* permutation() const = 0;  // device perm[M], or null
 };

@@ -16,6 +16,7 @@
 // same order, only the row a result is stored to differs.  execute() does not
 // allocate once the workspace is large enough (never, on the fused path).
 // Calls on one plan must not overlap (they share the workspace).
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -37,6 +38,16 @@ public:
     }
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+        if (this != &o) {
+            if (p_) (void)hipFree(p_);
+            p_ = o.p_;
+            n_ = o.n_;
+            o.p_ = nullptr;
+            o.n_ = 0;
+        }
+        return *this;
+    }
     void reset(size_t bytes) {
         if (p_) XSPMM_HIP_CHECK(hipFree(p_));
         p_ = nullptr;
@@ -103,9 +114,35 @@ public:
             order_.reset((size_t)Mb_ * sizeof(int32_t));
             spmm_dispatch_order<I>(brp_.as<I>(), Mb_, order_.as<int32_t>(), s);
         }
+        if constexpr (sizeof(T) == 2) pack(s);
         if (tm) step.stop(&tm[2]);
         if (tm) total.stop(&tm[5]);
         XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    }
+
+    // Packed column batches: the batch kernel's batches, formed once.  Kept
+    // when they take at most 3/4 of the BCSR values' bytes (sparse blocks);
+    // a fully populated grid keeps the GEMM-tiled kernel instead.
+    void pack(hipStream_t s)
+    {
+        if (nnzb_ == 0 || nnzb_ == Mb_ * Kb_ || !spmm_f16_pack_supported(K_, Mb_, Kb_)) return;
+        if (const char* e = std::getenv("XSPMM_PLAN_PACK"))
+            if (std::strcmp(e, "off") == 0) return;
+        const uint16_t* v = reinterpret_cast<const uint16_t*>(bvals_.as<T>());
+        Scratch counts((size_t)Mb_ * 4 * sizeof(int32_t), s);
+        spmm_f16_pack_count<I>(M_, K_, Mb_, Kb_, brp_.as<I>(), bci_.as<I>(), v,
+                               counts.as<int32_t>(), s);
+        DeviceBuffer offsets((size_t)(Mb_ * 4 + 1) * sizeof(int64_t));
+        const int64_t nb = spmm_f16_pack_offsets(counts.as<int32_t>(), Mb_ * 4,
+                                                 offsets.as<int64_t>(), s);
+        if ((double)nb * (1024.0 + 128.0) > 0.75 * (double)nnzb_ * 512.0) return;
+        pa_.reset((size_t)(nb > 0 ? nb : 1) * 1024);
+        prow_.reset((size_t)(nb > 0 ? nb : 1) * 128);
+        spmm_f16_pack_fill<I>(M_, K_, Mb_, Kb_, brp_.as<I>(), bci_.as<I>(), v,
+                              offsets.as<int64_t>(), pa_.as<void>(), prow_.as<uint32_t>(), s);
+        poff_ = std::move(offsets);
+        nbatches_ = nb;
+        packed_ = true;
     }
 
     void execute(const void* Bv, float* C, int64_t N, hipStream_t s) override
@@ -114,6 +151,13 @@ public:
         if (M_ == 0 || N == 0) return;
         const T* B = static_cast<const T*>(Bv);
         const int32_t* order = order_.size() ? order_.as<int32_t>() : nullptr;
+        if constexpr (sizeof(T) == 2) {
+            if (packed_ && spmm_f16_packed<I>(M_, K_, Mb_, poff_.as<int64_t>(), pa_.as<void>(),
+                                              prow_.as<uint32_t>(),
+                                              reinterpret_cast<const uint16_t*>(B), C, N, order,
+                                              clustered_ ? perm_.as<I>() : nullptr, s))
+                return;
+        }
         if (!clustered_) {
             bcsr_spmm_ex<T, I>(M_, K_, Mb_, Kb_, nnzb_, brp_.as<I>(), bci_.as<I>(), bvals_.as<T>(),
                                B, C, N, order, nullptr, s);
@@ -133,14 +177,16 @@ public:
     }
 
     int64_t num_blocks() const override { return nnzb_; }
+    int64_t num_packed_batches() const override { return packed_ ? nbatches_ : -1; }
     int64_t num_block_rows() const override { return Mb_; }
     bool clustered() const override { return clustered_; }
     const void* permutation() const override { return clustered_ ? perm_.as<void>() : nullptr; }
 
 private:
-    int64_t M_ = 0, K_ = 0, Mb_ = 0, Kb_ = 0, nnzb_ = 0;
-    bool clustered_ = false;
+    int64_t M_ = 0, K_ = 0, Mb_ = 0, Kb_ = 0, nnzb_ = 0, nbatches_ = 0;
+    bool clustered_ = false, packed_ = false;
     DeviceBuffer perm_, brp_, bci_, bvals_, order_, ws_;
+    DeviceBuffer poff_, pa_, prow_;  // packed column batches
 };
 
 }  // namespace

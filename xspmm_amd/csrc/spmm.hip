@@ -27,6 +27,7 @@
 #include <string>
 
 #include "internal.hpp"
+#include "scan.hpp"
 
 namespace xspmm {
 namespace detail {
@@ -542,7 +543,60 @@ __device__ __forceinline__ uint32_t block_col_scalar(int64_t c)
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
+// What the batch kernel does with each batch it forms: multiply it (the
+// Tier-1 SpMM), only count it, or store it for spmm_f16_packed_kernel -- the
+// wave's A' operand (64 lanes x 16 bytes) and its 32 B-row indices
+// (0xffffffff for unused slots), in the order the wave forms them.
+enum class BatchMode { kMultiply, kCount, kPack };
+
+struct BatchPack {
+    int32_t* counts;          // kCount: batches of (block-row, wave), 4 per row
+    const int64_t* offsets;   // kPack: first batch of (block-row, wave)
+    u32x4_t* a;               // kPack: A' operands
+    uint32_t* rows;           // kPack: B-row indices
+};
+
+// Sum the four waves' partial 16 x (16 NT) tiles through LDS (in wave order)
+// and store C rows: product row r of the block-row goes to C row row_map[r]
+// when row_map is given (the un-permutation fused), else to row r.
 template <typename I, int NT>
+__device__ __forceinline__ void batch_tile_store(const float4_t (&acc)[NT], unsigned char* smem,
+                                                 int wave, int g, int li, int64_t br, int64_t n0,
+                                                 int64_t M, int64_t N, float* __restrict__ C,
+                                                 const I* __restrict__ row_map)
+{
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);  // 4 x [16][128] fp32 = 32 KB
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave * 2048 + (4 * g + r) * 128 + 16 * j + li] = acc[j][r];
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int row = t >> 4;
+    const int c0 = (t & 15) * 8;
+    const int64_t grow = br * 16 + row;
+    if (grow < M && c0 < NT * 16) {
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int o = row * 128 + c0 + e;
+            out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
+        }
+        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+        float* dst = C + crow * N + n0 + c0;
+        if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
+            *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (n0 + c0 + e < N) dst[e] = out[e];
+        }
+    }
+}
+
+template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply>
 __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_kernel(const I* __restrict__ brp,
                                                              const I* __restrict__ bci,
                                                              const uint16_t* __restrict__ vals,
@@ -550,7 +604,8 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
                                                              float* __restrict__ C, int64_t M,
                                                              int64_t K, int64_t N, int64_t Kb,
                                                              const int32_t* __restrict__ order,
-                                                             const I* __restrict__ row_map)
+                                                             const I* __restrict__ row_map,
+                                                             BatchPack pk)
 {
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
@@ -641,7 +696,22 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
     };
     // Close the open batch of `cnt` slots: multiply the previous one, then
     // read this one's A' operand and issue its row loads.
+    int64_t nbatch = 0;  // batches formed so far (count and pack modes)
+    int64_t pbase = 0;   // first output batch of this wave (pack mode)
+    if constexpr (MODE == BatchMode::kPack) pbase = pk.offsets[br * 4 + wave];
     auto start = [&](uint32_t cnt) {
+        if constexpr (MODE != BatchMode::kMultiply) {
+            if constexpr (MODE == BatchMode::kPack) {
+                const int64_t bi = pbase + nbatch;
+                pk.a[bi * 64 + lane] = *reinterpret_cast<const u32x4_t*>(W + ap_row + 16u * (uint32_t)g);
+                if (lane < 32) {
+                    const uint32_t r = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * (uint32_t)lane);
+                    pk.rows[bi * 32 + lane] = (uint32_t)lane < cnt ? r : 0xffffffffu;
+                }
+            }
+            ++nbatch;
+            return;
+        }
         if (started) finish();
         aop = __builtin_bit_cast(half8_t,
                                  *reinterpret_cast<const u32x4_t*>(W + ap_row + 16u * (uint32_t)g));
@@ -777,41 +847,112 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
             }
         }
         if (pending > 0u) start(pending);
-        if (started) finish();
+        if constexpr (MODE == BatchMode::kMultiply) {
+            if (started) finish();
+        }
     }
+    if constexpr (MODE == BatchMode::kCount) {
+        if (lane == 0) pk.counts[br * 4 + wave] = (int32_t)nbatch;
+        return;
+    } else if constexpr (MODE == BatchMode::kPack) {
+        return;
+    } else {
+        batch_tile_store<I, NT>(acc, smem, wave, g, li, br, n0, M, N, C, row_map);
+    }
+}
 
-    // Sum the four waves' partial tiles through LDS and store C.
-    __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);  // 4 x [16][128] fp32 = 32 KB
+// ---------------------------------------------------------------------------
+// Multiply packed column batches (written by the batch kernel in pack mode).
+// Wave w of the workgroup of block-row br multiplies the batches
+// [offsets[4 br + w], offsets[4 br + w + 1]) in order: the stored A' operand,
+// the B rows of the stored slot indices (unused slots read zeros), and the
+// batch kernel's own multiply step and store -- the same MFMA operands in the
+// same order, so C equals the batch kernel's C.  The next batch's operand and
+// indices load while the current batch multiplies, and its B rows load right
+// after.  grid = (block-rows, ceil(N / 128)); N % 8 == 0, K * N * 2 <= 2^31.
+// ---------------------------------------------------------------------------
+template <typename I, int NT>
+__global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_kernel(
+    const int64_t* __restrict__ offsets, const u32x4_t* __restrict__ pa,
+    const uint32_t* __restrict__ prow, const uint16_t* __restrict__ B, float* __restrict__ C,
+    int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ order, const I* __restrict__ row_map)
+{
+    static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
+    constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
+    constexpr int RPL = 64 / CPR;  // B rows per load instruction
+    __shared__ __align__(16) unsigned char smem[4 * kBatchWaveLds];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    unsigned char* const W = smem + wave * kBatchWaveLds;
+    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * 128;
+    const int li = lane & 15;
+    const int g = lane >> 4;
+
+    const uint32_t b_bytes = (uint32_t)(K * N * 2);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
+    const uint32_t k32 = (uint32_t)K;
+    const uint32_t rowbytes = (uint32_t)(2 * N);
+    const uint32_t ld_c = (uint32_t)(lane % CPR);
+    const uint32_t ld_r = (uint32_t)(lane / CPR);
+    const uint32_t ld_off = (uint32_t)(2 * n0) + 16u * ld_c;
+    const uint32_t tr_e0 = (uint32_t)(8 * g + (li >> 2));
+    const uint32_t tr_base = tr_e0 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
+    const uint32_t tr_swz16 = bt_swz(tr_e0) << 4;
+
+    float4_t acc[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t b0 = offsets[br * 4 + wave];
+    const int64_t b1 = offsets[br * 4 + wave + 1];
+    if (b0 < b1) {
+        auto load_rows = [&](int64_t bi, uint32_t (&row)[NT]) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave * 2048 + (4 * g + r) * 128 + 16 * j + li] = acc[j][r];
-    __syncthreads();
-    const int t = threadIdx.x;
-    const int row = t >> 4;
-    const int c0 = (t & 15) * 8;
-    const int64_t grow = br * 16 + row;
-    if (grow < M && c0 < NT * 16) {
-        float out[8];
+            for (int t = 0; t < NT; ++t) row[t] = prow[bi * 32 + t * RPL + ld_r];
+        };
+        auto load_b = [&](const uint32_t (&row)[NT], u32x4_t (&bv)[NT]) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int o = row * 128 + c0 + e;
-            out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
-        }
-        // product row grow lands in C row row_map[grow] (the un-permutation
-        // of the clustered pipeline, fused into the store) or in row grow
-        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
-        float* dst = C + crow * N + n0 + c0;
-        if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
-            *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
-            *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
-        } else {
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t off = row[t] < k32 ? __umul24(row[t], rowbytes) + ld_off : b_bytes + ld_off;
+                bv[t] = __builtin_bit_cast(u32x4_t,
+                                           __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+            }
+        };
+        u32x4_t a_cur = pa[b0 * 64 + lane];
+        uint32_t row[NT];
+        load_rows(b0, row);
+        u32x4_t bv[NT];
+        load_b(row, bv);
+        for (int64_t bi = b0; bi < b1; ++bi) {
+            const bool more = bi + 1 < b1;
+            u32x4_t a_nxt = a_cur;
+            if (more) {
+                a_nxt = pa[(bi + 1) * 64 + lane];
+                load_rows(bi + 1, row);
+            }
+            // the batch kernel's multiply step
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (n0 + c0 + e < N) dst[e] = out[e];
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+                *reinterpret_cast<u32x4_t*>(W + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[t];
+            }
+            const half8_t aop = __builtin_bit_cast(half8_t, a_cur);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const uint32_t a = tr_base + ((uint32_t)(32 * j) ^ tr_swz16);
+                const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a));
+                const short4_t hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a + 4 * kBtRow));
+                const half8_t bop = __builtin_bit_cast(
+                    half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
+            }
+            if (more) load_b(row, bv);
+            a_cur = a_nxt;
         }
     }
+    batch_tile_store<I, NT>(acc, smem, wave, g, li, br, n0, M, N, C, row_map);
 }
 
 // ---------------------------------------------------------------------------
@@ -966,6 +1107,83 @@ void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int
 
 bool spmm_order_wanted(int64_t Mb) { return Mb > kOrderMinRows && Mb <= 0x7fffffffLL; }
 
+bool spmm_f16_pack_supported(int64_t K, int64_t Mb, int64_t Kb)
+{
+    return Mb > 0 && Mb <= 0x7fffffffLL && Kb < (int64_t(1) << 20) && K < (int64_t(1) << 24);
+}
+
+template <typename I>
+void spmm_f16_pack_count(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                         const uint16_t* bvals, int32_t* counts, hipStream_t s)
+{
+    BatchPack pk{counts, nullptr, nullptr, nullptr};
+    hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kCount>), dim3((unsigned)Mb, 1),
+                       dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
+                       nullptr, nullptr, pk);
+    XSPMM_LAUNCH_CHECK();
+}
+
+template <typename I>
+void spmm_f16_pack_fill(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                        const uint16_t* bvals, const int64_t* offsets, void* a, uint32_t* rows,
+                        hipStream_t s)
+{
+    BatchPack pk{nullptr, offsets, static_cast<u32x4_t*>(a), rows};
+    hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kPack>), dim3((unsigned)Mb, 1),
+                       dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
+                       nullptr, nullptr, pk);
+    XSPMM_LAUNCH_CHECK();
+}
+
+template <typename I>
+bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, const void* a,
+                     const uint32_t* rows, const uint16_t* B, float* C, int64_t N,
+                     const int32_t* order, const I* row_map, hipStream_t s)
+{
+    if (M == 0 || N == 0 || Mb == 0) return true;
+    if (N % 8 != 0 || K * N * 2 > (int64_t(1) << 31) || N >= (int64_t(1) << 22)) return false;
+    const int64_t chunks = (N + 127) / 128;
+    if (chunks > 65535) return false;
+    const dim3 grid((unsigned)Mb, (unsigned)chunks);
+    const u32x4_t* pa = static_cast<const u32x4_t*>(a);
+    if (N <= 16)
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 1>), grid, dim3(256), 0, s, offsets, pa, rows,
+                           B, C, M, K, N, order, row_map);
+    else if (N <= 32)
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 2>), grid, dim3(256), 0, s, offsets, pa, rows,
+                           B, C, M, K, N, order, row_map);
+    else if (N <= 64)
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 4>), grid, dim3(256), 0, s, offsets, pa, rows,
+                           B, C, M, K, N, order, row_map);
+    else
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 8>), grid, dim3(256), 0, s, offsets, pa, rows,
+                           B, C, M, K, N, order, row_map);
+    XSPMM_LAUNCH_CHECK();
+    return true;
+}
+
+int64_t spmm_f16_pack_offsets(const int32_t* counts, int64_t n, int64_t* offsets, hipStream_t s)
+{
+    device_exclusive_scan(ArrayValue<int32_t>{counts}, n, offsets, s);
+    int64_t total = 0;
+    XSPMM_HIP_CHECK(hipMemcpyAsync(&total, offsets + n, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    return total;
+}
+
+#define XSPMM_PACK(I)                                                                             \
+    template void spmm_f16_pack_count<I>(int64_t, int64_t, int64_t, int64_t, const I*, const I*,   \
+                                         const uint16_t*, int32_t*, hipStream_t);                 \
+    template void spmm_f16_pack_fill<I>(int64_t, int64_t, int64_t, int64_t, const I*, const I*,    \
+                                        const uint16_t*, const int64_t*, void*, uint32_t*,        \
+                                        hipStream_t);                                              \
+    template bool spmm_f16_packed<I>(int64_t, int64_t, int64_t, const int64_t*, const void*,       \
+                                     const uint32_t*, const uint16_t*, float*, int64_t,            \
+                                     const int32_t*, const I*, hipStream_t);
+XSPMM_PACK(int32_t)
+XSPMM_PACK(int64_t)
+#undef XSPMM_PACK
+
 template <typename I>
 void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s)
 {
@@ -1026,16 +1244,16 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
             }
             if (N <= 16)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order, row_map);
+                                   v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 32)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order, row_map);
+                                   v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order, row_map);
+                                   v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
-                                   v, b, C, M, K, N, Kb, order, row_map);
+                                   v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             XSPMM_LAUNCH_CHECK();
             return true;
         }
