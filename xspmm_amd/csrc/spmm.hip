@@ -867,9 +867,9 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
 // [offsets[4 br + w], offsets[4 br + w + 1]) in order: the stored A' operand,
 // the B rows of the stored slot indices (unused slots read zeros), and the
 // batch kernel's own multiply step and store -- the same MFMA operands in the
-// same order, so C equals the batch kernel's C.  The next batch's operand and
-// indices load while the current batch multiplies, and its B rows load right
-// after.  grid = (block-rows, ceil(N / 128)); N % 8 == 0, K * N * 2 <= 2^31.
+// same order, so C equals the batch kernel's C.  While a batch multiplies,
+// the next batch's B rows are in flight and the indices of the one after
+// are loading.  LDS holds only the B tile of each wave (8 KB).  grid = (block-rows, ceil(N / 128)); N % 8 == 0, K * N * 2 <= 2^31.
 // ---------------------------------------------------------------------------
 template <typename I, int NT>
 __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_kernel(
@@ -880,10 +880,10 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_ke
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
     constexpr int RPL = 64 / CPR;  // B rows per load instruction
-    __shared__ __align__(16) unsigned char smem[4 * kBatchWaveLds];
+    __shared__ __align__(16) unsigned char smem[4 * kBtBytes];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    unsigned char* const W = smem + wave * kBatchWaveLds;
+    unsigned char* const W = smem + wave * kBtBytes;
     const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
     const int64_t n0 = (int64_t)blockIdx.y * 128;
     const int li = lane & 15;
@@ -905,39 +905,42 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_ke
     for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     const int64_t b0 = offsets[br * 4 + wave];
-    const int64_t b1 = offsets[br * 4 + wave + 1];
-    if (b0 < b1) {
-        auto load_rows = [&](int64_t bi, uint32_t (&row)[NT]) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) row[t] = prow[bi * 32 + t * RPL + ld_r];
-        };
-        auto load_b = [&](const uint32_t (&row)[NT], u32x4_t (&bv)[NT]) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const uint32_t off = row[t] < k32 ? __umul24(row[t], rowbytes) + ld_off : b_bytes + ld_off;
-                bv[t] = __builtin_bit_cast(u32x4_t,
-                                           __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
-            }
-        };
-        u32x4_t a_cur = pa[b0 * 64 + lane];
-        uint32_t row[NT];
-        load_rows(b0, row);
+    const int nb = (int)(offsets[br * 4 + wave + 1] - b0);
+    if (nb > 0) {
+        const u32x4_t* pa_w = pa + b0 * 64 + lane;
+        const uint32_t* pr_w = prow + b0 * 32 + ld_r;
         u32x4_t bv[NT];
-        load_b(row, bv);
-        for (int64_t bi = b0; bi < b1; ++bi) {
-            const bool more = bi + 1 < b1;
-            u32x4_t a_nxt = a_cur;
-            if (more) {
-                a_nxt = pa[(bi + 1) * 64 + lane];
-                load_rows(bi + 1, row);
-            }
-            // the batch kernel's multiply step
+        uint32_t row[NT];
+        u32x4_t a_cur = pa_w[0];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t r = pr_w[t * RPL];
+            const uint32_t off = r < k32 ? __umul24(r, rowbytes) + ld_off : b_bytes + ld_off;
+            bv[t] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+        }
+        {
+            const int nx = nb > 1 ? 1 : 0;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) row[t] = pr_w[nx * 32 + t * RPL];
+        }
+        for (int bi = 0; bi < nb; ++bi) {
+            const bool more = bi + 1 < nb;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const uint32_t e = (uint32_t)(t * RPL) + ld_r;
                 *reinterpret_cast<u32x4_t*>(W + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[t];
             }
             const half8_t aop = __builtin_bit_cast(half8_t, a_cur);
+            if (more) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint32_t off = row[t] < k32 ? __umul24(row[t], rowbytes) + ld_off : b_bytes + ld_off;
+                    bv[t] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+                }
+            }
+            const int n2 = bi + 2 < nb ? bi + 2 : (more ? bi + 1 : bi);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) row[t] = pr_w[n2 * 32 + t * RPL];
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 const uint32_t a = tr_base + ((uint32_t)(32 * j) ^ tr_swz16);
@@ -948,8 +951,7 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_ke
                     half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
             }
-            if (more) load_b(row, bv);
-            a_cur = a_nxt;
+            a_cur = pa_w[(more ? bi + 1 : bi) * 64];
         }
     }
     batch_tile_store<I, NT>(acc, smem, wave, g, li, br, n0, M, N, C, row_map);
