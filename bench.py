@@ -326,9 +326,18 @@ def main():
         torch.cuda.synchronize()
         Cq, _ = X.spmm_pipeline(A, B, optimize_pattern=True)
         torch.cuda.synchronize()
-        plan_info = {"execute_ms": a.elapsed_time(b) / args.steps,
+        ex_ms = a.elapsed_time(b) / args.steps
+        plan_info = {"execute_ms": ex_ms,
                      "prepare_ms": plan.timings["total_pipeline_ms"],
-                     "equals_pipeline": bool(torch.equal(Cp, Cq))}
+                     "equals_pipeline": bool(torch.equal(Cp, Cq)),
+                     "packed_batches": plan.packed_batches,
+                     "effective_tflops": 2.0 * nnz * N / (ex_ms * 1e-3) / 1e12}
+        if plan.packed_batches > 0:
+            # streamed per call: packed A' (1 KB) + indices (128 B) per batch,
+            # 4 offsets per block-row, B once, C once, the permutation once
+            pb = (plan.packed_batches * 1152 + (4 * Mb + 1) * 8 + K * N * p.vals.dtype.itemsize
+                  + M * N * 4 + M * p.rp.dtype.itemsize)
+            plan_info.update(bytes_per_call=pb, achieved_gbs=pb / (ex_ms * 1e-3) / 1e9)
         if stages:
             plan_info["pipeline_spmm_plus_unpermute_ms"] = stages["spmm_ms"] + stages["unpermutation_ms"]
         plan.close()
@@ -336,6 +345,8 @@ def main():
     vendor = None
     if not args.no_vendor:
         vendor = vendor_columns(Ap, Bm, B, C, ms, args.steps)
+        if plan_info and "rocsparse_csr_ms" in vendor:
+            plan_info["speedup_vs_rocsparse_csr"] = vendor["rocsparse_csr_ms"] / plan_info["execute_ms"]
 
     cpu = None
     if not args.no_cpu:
