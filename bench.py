@@ -61,25 +61,39 @@ def cpu_baseline(p, N, nnz, seconds):
     over the whole matrix until `seconds` have elapsed; median per call."""
     import oracle
 
+    t0 = time.perf_counter()
     brp, bci, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    conv_ms = (time.perf_counter() - t0) * 1e3
     threads = host_threads()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        oracle.bcsr_spmm_f32(p.M, p.K, N, brp, bci, bv, p.B, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    t = statistics.median(times)
+
+    def run(nthreads, budget, cap):
+        times = []
+        t_end = time.perf_counter() + budget
+        while time.perf_counter() < t_end or not times:
+            t0 = time.perf_counter()
+            oracle.bcsr_spmm_f32(p.M, p.K, N, brp, bci, bv, p.B, nthreads=nthreads)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= cap:
+                break
+        return statistics.median(times), len(times)
+
+    t, n = run(threads, seconds, 200)
+    # one thread, as the reference's CpuExecutor would run, when a call fits
+    # the budget (estimated from the all-thread time)
+    single = None
+    if t * threads <= seconds:
+        t1, n1 = run(1, seconds / 3, 20)
+        single = {"value": 2.0 * nnz * N / t1 / 1e12, "ms_per_call": t1 * 1e3, "runs": n1}
     return {
         "value": 2.0 * nnz * N / t / 1e12,
         "unit": "TFLOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"whole matrix ({len(bci)} blocks), {len(times)} runs, median "
+        "sample": f"whole matrix ({len(bci)} blocks), {n} runs, median "
                   f"{t * 1e3:.1f} ms/call; BCSR tile product with fp32 accumulation "
                   f"(oracle/oracle.c xo_bcsr_spmm_f32)",
+        "single_thread": single,
+        "csr_to_bcsr_ms": conv_ms,
     }
 
 
@@ -183,6 +197,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="templates", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cluster", choices=("config", "on", "off"), default="config",
+                    help="override the workload's clustering setting")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pipeline", action="store_true")
     ap.add_argument("--no-vendor", action="store_true",
@@ -212,6 +228,8 @@ def main():
 
     print(f"[bench] generating {args.config}", file=sys.stderr, flush=True)
     p = synth.CONFIGS[args.config]()
+    if args.cluster != "config":
+        p.cluster = args.cluster == "on"
     M, K, N, nnz = p.M, p.K, p.N, p.nnz
     A = X.CSRMatrix.from_host(M, K, p.rp, p.ci, p.vals)
     B = torch.as_tensor(p.B).cuda()
