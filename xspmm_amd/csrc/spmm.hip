@@ -1002,21 +1002,29 @@ __global__ __launch_bounds__(kOrderThreads) void order_rows_kernel(const I* __re
 
 // ---------------------------------------------------------------------------
 // fp32 x fp32 -> fp32 tile kernel.
+//
+// A workgroup of kF32Waves waves owns one block-row and NTW 16-column tiles
+// (up to 64 columns).  The waves split the row's blocks (wave w: blocks
+// w, w + kF32Waves, ...), two blocks per step with all their loads issued
+// before the MFMAs (v_mfma_f32_16x16x4_f32, four per block and tile), and
+// their partial tiles are summed through LDS in wave order.  Splitting the
+// row keeps short rows' dependent load chains short: a small matrix has few
+// block-rows, and one wave per row would leave the chip idle.
 // ---------------------------------------------------------------------------
+constexpr int kF32Waves = 8;
+
 template <typename I, int NTW>
-__global__ __launch_bounds__(256) void spmm_f32_kernel(const I* __restrict__ brp,
-                                                       const I* __restrict__ bci,
-                                                       const float* __restrict__ vals,
-                                                       const float* __restrict__ B,
-                                                       float* __restrict__ C, int64_t M,
-                                                       int64_t K, int64_t N, int ntiles)
+__global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __restrict__ brp,
+                                                                  const I* __restrict__ bci,
+                                                                  const float* __restrict__ vals,
+                                                                  const float* __restrict__ B,
+                                                                  float* __restrict__ C, int64_t M,
+                                                                  int64_t K, int64_t N, int ntiles)
 {
+    __shared__ float red[kF32Waves][16][NTW * 16];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int waves = blockDim.x / kWave;
-    const int tile0 = (blockIdx.y * waves + wave) * NTW;
-    if (tile0 >= ntiles) return;
-
+    const int tile0 = blockIdx.y * NTW;
     const int64_t br = blockIdx.x;
     const int64_t rs = brp[br];
     const int64_t re = brp[br + 1];
@@ -1027,34 +1035,57 @@ __global__ __launch_bounds__(256) void spmm_f32_kernel(const I* __restrict__ brp
 #pragma unroll
     for (int j = 0; j < NTW; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t blk = rs; blk < re; ++blk) {
-        const float4_t a = *reinterpret_cast<const float4_t*>(vals + blk * 256 + li * 16 + g * 4);
-        const int64_t col = (int64_t)bci[blk];
+    auto b_panel = [&](int64_t col, float (&bv)[NTW][4]) {
         const int64_t kbase = (col >= 0 ? col : K) * 16 + g * 4;  // invalid columns read nothing
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
             const int64_t n = (int64_t)(tile0 + j) * 16 + li;
-            float bv[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int64_t k = kbase + s;
-                bv[s] = (k >= 0 && k < K && n < N) ? B[k * N + n] : 0.f;
+                bv[j][s] = (k >= 0 && k < K && n < N) ? B[k * N + n] : 0.f;
             }
+        }
+    };
+    auto multiply = [&](const float4_t& a, const float (&bv)[NTW][4]) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bv[s], acc[j], 0, 0, 0);
-        }
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bv[j][s], acc[j], 0, 0, 0);
+    };
+
+    int64_t blk = rs + wave;
+    for (; blk + kF32Waves < re; blk += 2 * kF32Waves) {
+        const float4_t a0 = *reinterpret_cast<const float4_t*>(vals + blk * 256 + li * 16 + g * 4);
+        const float4_t a1 =
+            *reinterpret_cast<const float4_t*>(vals + (blk + kF32Waves) * 256 + li * 16 + g * 4);
+        float b0[NTW][4], b1[NTW][4];
+        b_panel((int64_t)bci[blk], b0);
+        b_panel((int64_t)bci[blk + kF32Waves], b1);
+        multiply(a0, b0);
+        multiply(a1, b1);
+    }
+    if (blk < re) {
+        const float4_t a0 = *reinterpret_cast<const float4_t*>(vals + blk * 256 + li * 16 + g * 4);
+        float b0[NTW][4];
+        b_panel((int64_t)bci[blk], b0);
+        multiply(a0, b0);
     }
 
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-        const int64_t col = (int64_t)(tile0 + j) * 16 + li;
-        if (tile0 + j >= ntiles || col >= N) continue;
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t row = br * 16 + g * 4 + r;
-            if (row < M) C[row * N + col] = acc[j][r];
-        }
+        for (int r = 0; r < 4; ++r) red[wave][4 * g + r][16 * j + li] = acc[j][r];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 16 * NTW * 16; o += 64 * kF32Waves) {
+        const int row = o / (NTW * 16), c = o % (NTW * 16);
+        float sum = red[0][row][c];
+#pragma unroll
+        for (int w = 1; w < kF32Waves; ++w) sum += red[w][row][c];
+        const int64_t grow = br * 16 + row;
+        const int64_t col = (int64_t)tile0 * 16 + c;
+        if (grow < M && col < N && tile0 + c / 16 < ntiles) C[grow * N + col] = sum;
     }
 }
 
@@ -1298,17 +1329,22 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
         if (row_map) return false;  // the fp32 kernel stores rows in place
         const float* v = reinterpret_cast<const float*>(bvals);
         const float* b = reinterpret_cast<const float*>(B);
-        switch (geo.ntw) {
+        const int ntw = ntiles >= 4 ? 4 : (ntiles >= 2 ? 2 : 1);
+        const int64_t gy = (ntiles + ntw - 1) / ntw;
+        if (gy > 65535) throw std::invalid_argument("xSpMM: N too large.");
+        const dim3 fgrid((unsigned)Mb, (unsigned)gy);
+        const dim3 fblock(64 * kF32Waves);
+        switch (ntw) {
         case 4:
-            hipLaunchKernelGGL((spmm_f32_kernel<I, 4>), grid, block, 0, s, brp, bci, v, b, C, M,
+            hipLaunchKernelGGL((spmm_f32_kernel<I, 4>), fgrid, fblock, 0, s, brp, bci, v, b, C, M,
                                K, N, ntiles);
             break;
         case 2:
-            hipLaunchKernelGGL((spmm_f32_kernel<I, 2>), grid, block, 0, s, brp, bci, v, b, C, M,
+            hipLaunchKernelGGL((spmm_f32_kernel<I, 2>), fgrid, fblock, 0, s, brp, bci, v, b, C, M,
                                K, N, ntiles);
             break;
         default:
-            hipLaunchKernelGGL((spmm_f32_kernel<I, 1>), grid, block, 0, s, brp, bci, v, b, C, M,
+            hipLaunchKernelGGL((spmm_f32_kernel<I, 1>), fgrid, fblock, 0, s, brp, bci, v, b, C, M,
                                K, N, ntiles);
             break;
         }
