@@ -150,13 +150,15 @@ bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, c
                      const uint32_t* rows, const uint16_t* B, float* C, int64_t N,
                      const int32_t* order, const I* row_map, hipStream_t s);
 
-// Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb).
-// Returns false (and launches nothing) when the shape is not covered;
-// spmm_dense_f16_covers tells in advance.
+// Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb);
+// row_map (null: rows in place) as for bcsr_spmm_ex.  Returns false (and
+// launches nothing) when the shape is not covered; spmm_dense_f16_covers
+// tells in advance.
 bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N);
+template <typename RM>
 bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
                          const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
-                         hipStream_t s);
+                         hipStream_t s, const RM* row_map);
 
 // CSR -> BCSR.  count writes brp[Mb+1] and returns nnzb (synchronizes `s`);
 // it throws std::invalid_argument on an out-of-range column index.

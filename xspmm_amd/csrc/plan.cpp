@@ -9,9 +9,10 @@
 //   * fp16, N % 8 == 0, on the batch kernel: its store writes product row r
 //     straight into C row perm[r] -- the un-permutation of the pipeline fused
 //     into the SpMM, one launch, no temporary;
-//   * otherwise (fp32, other N, or a fully populated block grid, which takes
-//     the GEMM-tiled kernel as in the pipeline) the product goes to a
-//     workspace kept by the plan (it only grows) and is un-permuted into C.
+//   * a fully populated block grid takes the GEMM-tiled kernel, as in the
+//     pipeline, with the same fused store;
+//   * otherwise (fp32, other N) the product goes to a workspace kept by the
+//     plan (it only grows) and is un-permuted into C.
 // C equals the pipeline's C bit for bit: the same kernels accumulate in the
 // same order, only the row a result is stored to differs.  execute() does not
 // allocate once the workspace is large enough (never, on the fused path).

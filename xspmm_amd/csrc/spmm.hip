@@ -1253,12 +1253,9 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
         // batch and gather paths: byte offsets into B, and a wave's A range,
         // fit 32 bits; B row indices fit 24 bits
         const Fp16Kernel choice = fp16_kernel_choice();
-        // every block present: GEMM-tiled kernel (matrix-core bound); it
-        // stores rows in place, so a row-mapped call is declined
-        if (choice == Fp16Kernel::kAuto && spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N)) {
-            if (row_map) return false;
-            return bcsr_spmm_dense_f16(M, K, Mb, Kb, nnzb, v, b, C, N, s);
-        }
+        // every block present: GEMM-tiled kernel (matrix-core bound)
+        if (choice == Fp16Kernel::kAuto && spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N))
+            return bcsr_spmm_dense_f16<I>(M, K, Mb, Kb, nnzb, v, b, C, N, s, row_map);
         const bool offsets32 = K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
                                Kb < (int64_t(1) << 20);
         const int64_t chunks = (N + 127) / 128;

@@ -116,12 +116,17 @@ __device__ __forceinline__ uint32_t panel_swz(uint32_t e)
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
 }
 
+// RM: index type of the optional output row map (C row row_map[r] receives
+// product row r -- the clustered pipeline's un-permutation fused into the
+// store; null stores rows in place).
+template <typename RM>
 __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const uint16_t* __restrict__ vals,
                                                                  const uint16_t* __restrict__ B,
                                                                  float* __restrict__ C,
                                                                  int64_t M, int64_t K,
                                                                  int64_t N, int64_t Mb,
-                                                                 int64_t Kb)
+                                                                 int64_t Kb,
+                                                                 const RM* __restrict__ row_map)
 {
     constexpr int NS = XSPMM_DENSE_STAGES;
     static_assert(NS == 2 || NS == 3, "2 or 3 LDS stages");
@@ -281,6 +286,7 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
                     T[(16 * wr + 4 * g + q) * TS + 16 * kDTiles * wc + 16 * j + li] = acc[r][j][q];
             __syncthreads();
             const int64_t row = 16 * (br0 + 8 * (row_l / 16) + r) + (row_l % 16);
+            const int64_t crow = (row_map && row < M) ? (int64_t)row_map[row] : row;
 #pragma unroll
             for (int p = 0; p < kDN / (4 * TPR); ++p) {
                 const int c = col_l + 4 * TPR * p;
@@ -288,9 +294,9 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
                 const int64_t col = n0 + c;
                 if (row < M && col < N) {
                     if (col + 4 <= N && (N & 3) == 0)
-                        __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(C + row * N + col));
+                        __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(C + crow * N + col));
                     else
-                        for (int e = 0; e < 4 && col + e < N; ++e) C[row * N + col + e] = v[e];
+                        for (int e = 0; e < 4 && col + e < N; ++e) C[crow * N + col + e] = v[e];
                 }
             }
             __syncthreads();
@@ -306,10 +312,11 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     if (row0 + q < M) {
+                        const int64_t crow = row_map ? (int64_t)row_map[row0 + q] : row0 + q;
                         if constexpr (XSPMM_DENSE_EPI == 1)
-                            __builtin_nontemporal_store(acc[r][j][q], C + (row0 + q) * N + col);
+                            __builtin_nontemporal_store(acc[r][j][q], C + crow * N + col);
                         else
-                            C[(row0 + q) * N + col] = acc[r][j][q];
+                            C[crow * N + col] = acc[r][j][q];
                     }
             }
         }
@@ -338,17 +345,25 @@ bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t
     return dense_groups(Mb, N) <= 0x7fffffffLL;
 }
 
+template <typename RM>
 bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
                          const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
-                         hipStream_t s)
+                         hipStream_t s, const RM* row_map)
 {
     if (!spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N)) return false;
     const int64_t groups = dense_groups(Mb, N);
-    hipLaunchKernelGGL(spmm_f16_dense_kernel, dim3((unsigned)groups), dim3(kDThreads), 0, s, bvals, B, C,
-                       M, K, N, Mb, Kb);
+    hipLaunchKernelGGL(spmm_f16_dense_kernel<RM>, dim3((unsigned)groups), dim3(kDThreads), 0, s,
+                       bvals, B, C, M, K, N, Mb, Kb, row_map);
     XSPMM_LAUNCH_CHECK();
     return true;
 }
+
+template bool bcsr_spmm_dense_f16<int32_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
+                                           const uint16_t*, const uint16_t*, float*, int64_t,
+                                           hipStream_t, const int32_t*);
+template bool bcsr_spmm_dense_f16<int64_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
+                                           const uint16_t*, const uint16_t*, float*, int64_t,
+                                           hipStream_t, const int64_t*);
 
 }  // namespace detail
 }  // namespace xspmm
