@@ -508,6 +508,9 @@ constexpr int kApStride = 80;
 constexpr int kApOff = kBtBytes;
 constexpr int kSlotOff = kApOff + 16 * kApStride;
 constexpr int kBatchWaveLds = kSlotOff + 32 * 4;
+// each wave's region starts 16-byte aligned (128-bit LDS accesses)
+static_assert(kBatchWaveLds % 16 == 0 && kApOff % 16 == 0 && kSlotOff % 16 == 0,
+              "batch kernel LDS layout must keep 16-byte alignment");
 #ifndef XSPMM_BATCH_DEPTH
 #define XSPMM_BATCH_DEPTH 5
 #endif
