@@ -865,6 +865,293 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
 }
 
 // ---------------------------------------------------------------------------
+// fp16 column-batch kernel with the compaction on the matrix cores.
+//
+// Same batches as above (the non-zero block columns of a wave's pairs stacked
+// into K = 32 slots, then multiplied with their gathered B rows), but the
+// pair's columns are moved into their slots by an MFMA instead of per-column
+// LDS writes.  With the pair in registers as the B operand (lane (r, g): row
+// r, pair columns 8g .. 8g+7) and a one-hot selection S^T (16 slots x 32 pair
+// columns) as the A operand,
+//     D_h += S_h^T * pair^T
+// is the transposed A' of slots 16h .. 16h+15: lane (r, g) of D_h holds
+// A'[r][16h + 4g .. 16h + 4g + 3].  Each D entry receives one product
+// x * 1.0 and zeros, so the compaction is exact (a -0.0 entry becomes +0.0,
+// which changes no sum of products).  S^T lives in LDS (16 rows x 32 halves,
+// all zero between pairs): column lane (i < 8, g) of a set pair column
+// 8g + i writes 1.0 at [slot][8g + i] before the read and 0 after it, and its
+// B row index into the slot list.
+//
+// A' then carries, in MFMA K position k of lane group g (k = 8g .. 8g+7),
+// slot kslot(k) = 16 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3): the B tile row
+// of K position k holds the B row of slot kslot(k).  Pack mode stores A' and
+// the B rows in that K order, so spmm_f16_packed_kernel (tile row = K
+// position) multiplies the same operands in the same order.
+//
+// The per-pair column mask is formed as in the kernel above, placed in byte
+// g of each lane and OR-ed over the wave by DPP (row rotations, then the two
+// row broadcasts), so lane 63 holds the 32-bit pair mask.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ constexpr uint32_t kslot(uint32_t k)
+{
+    return 16u * ((k >> 2) & 1u) + 4u * (k >> 3) + (k & 3u);
+}
+
+template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply>
+__global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
+    const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
+    const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
+    int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map, BatchPack pk)
+{
+    static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
+    constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
+    constexpr int RPL = 64 / CPR;  // B rows per load instruction
+    constexpr uint32_t kSel = kApOff;  // S^T: 16 rows x kApStride bytes
+    // discard word for slot-list writes of lanes without a column: pad bytes
+    // 72..75 of S^T row 0 (reads cover bytes 0..63 of each row)
+    constexpr uint32_t kSlotPad = kSel + 72;
+    __shared__ __align__(16) unsigned char smem[4 * kBatchWaveLds];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    unsigned char* const W = smem + wave * kBatchWaveLds;
+
+    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * 128;
+    const int64_t rs = brp[br];
+    const int64_t re = brp[br + 1];
+    const int64_t npairs = (re - rs + 1) >> 1;
+
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int sel = lane >> 5;
+    const int kh = g & 1;
+
+    const uint32_t nblk = (uint32_t)(re - rs);
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + rs * 256, nblk * 512u);
+    const uint32_t b_bytes = (uint32_t)(K * N * 2);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
+    const uint32_t a_voff = (uint32_t)(sel * 512 + li * 32 + kh * 16);
+    const uint32_t kb32 = (uint32_t)Kb;
+    const uint32_t k32 = (uint32_t)K;
+    const uint32_t rowbytes = (uint32_t)(2 * N);
+
+    // --- per-lane constants --------------------------------------------------
+    // column lanes: lane (i < 8, g) stands for pair column 8g + i (bit 8g + i
+    // of the pair mask); the other lanes never match a bit
+    const uint32_t bitk = li < 8 ? 1u << (8 * g + li) : 0u;
+    const uint32_t lowk = bitk - 1u;
+    // its S^T entry: row (slot & 15), half 8g + i; lanes without a column
+    // write to pad bytes 64.. of S^T row li, which no read covers
+    const uint32_t st_k = kSel + 2u * (uint32_t)(8 * g + li);
+    const uint32_t st_pad = kSel + (uint32_t)(li * kApStride + 64 + 2 * g);
+    // its B row: 16 * (block column of block sel) + 8 kh + i
+    const uint32_t row_k = (uint32_t)(8 * kh + li);
+    // selection lanes: S^T row li, halves 8g .. 8g+7
+    const uint32_t st_rd = kSel + (uint32_t)(li * kApStride + 16 * g);
+    const uint32_t gshift = (uint32_t)(8 * g);
+    // B row loads: load t moves tile row t * RPL + lane / CPR, chunk lane % CPR
+    const uint32_t ld_c = (uint32_t)(lane % CPR);
+    const uint32_t ld_r = (uint32_t)(lane / CPR);
+    const uint32_t ld_off = (uint32_t)(2 * n0) + 16u * ld_c;
+    const uint32_t tr_e0 = (uint32_t)(8 * g + (li >> 2));
+    const uint32_t tr_base = tr_e0 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
+    const uint32_t tr_a0 = tr_base ^ (bt_swz(tr_e0) << 4);
+    // slot of tile row t * RPL + ld_r is kslot(t * RPL) + ks_r (RPL is 4 or a
+    // multiple of 8)
+    const int ks_r = (int)kslot(ld_r);
+    uint32_t one;
+    asm("s_mov_b32 %0, 0x10001" : "=s"(one));
+
+    // S^T starts all zero and every pair leaves it so
+    for (int i = lane; i < 16 * kApStride / 4; i += kWave)
+        reinterpret_cast<uint32_t*>(W + kSel)[i] = 0u;
+
+    float4_t acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float4_t d0 = float4_t{0.f, 0.f, 0.f, 0.f};  // A' slots 0..15 (transposed)
+    float4_t d1 = float4_t{0.f, 0.f, 0.f, 0.f};  // A' slots 16..31
+
+    u32x4_t bv[NT];
+    half8_t aop{};
+    bool started = false;
+    uint32_t pending = 0;
+
+    auto finish = [&]() {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+            *reinterpret_cast<u32x4_t*>(W + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[t];
+        }
+        // read address of tile j: tr_a0 ^ 32 j (the swizzle XORs bits 5..7,
+        // which tr_base leaves clear); recomputed here rather than kept live
+        uint32_t a0 = tr_a0;
+        asm volatile("" : "+v"(a0));
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t a = a0 ^ (uint32_t)(32 * j);
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a));
+            const short4_t hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a + 4 * kBtRow));
+            const half8_t bop = __builtin_bit_cast(
+                half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
+        }
+    };
+    int64_t nbatch = 0;
+    int64_t pbase = 0;
+    if constexpr (MODE == BatchMode::kPack) pbase = pk.offsets[br * 4 + wave];
+    // Close the open batch of `cnt` slots: A' from the D registers (exact
+    // fp16 values), then multiply the previous batch and issue this one's
+    // B row loads in K order.
+    auto start = [&](uint32_t cnt) {
+        if constexpr (MODE == BatchMode::kCount) {
+            ++nbatch;
+            return;
+        }
+        const half8_t a = half8_t{(_Float16)d0[0], (_Float16)d0[1], (_Float16)d0[2], (_Float16)d0[3],
+                                  (_Float16)d1[0], (_Float16)d1[1], (_Float16)d1[2], (_Float16)d1[3]};
+        d0 = float4_t{0.f, 0.f, 0.f, 0.f};
+        d1 = float4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (MODE == BatchMode::kPack) {
+            const int64_t bi = pbase + nbatch;
+            pk.a[bi * 64 + lane] = __builtin_bit_cast(u32x4_t, a);
+            if (lane < 32) {
+                const uint32_t s = kslot((uint32_t)lane);
+                const uint32_t r = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * s);
+                pk.rows[bi * 32 + lane] = s < cnt ? r : 0xffffffffu;
+            }
+            ++nbatch;
+            return;
+        }
+        if (started) finish();
+        aop = a;
+        uint32_t row[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            row[t] = *reinterpret_cast<const uint32_t*>(
+                W + kSlotOff + 4u * ((uint32_t)ks_r + kslot((uint32_t)(t * RPL))));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const bool use = (ks_r < (int)cnt - (int)kslot((uint32_t)(t * RPL))) & (row[t] < k32);
+            const uint32_t at = __umul24(row[t], rowbytes) + ld_off;
+            const uint32_t off = use ? at : b_bytes + ld_off;
+            bv[t] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+        }
+        started = true;
+    };
+
+    auto stage_a = [&](int64_t q, BatchA& P) {
+        const uint32_t pq = (uint32_t)q;
+        P.a = __builtin_bit_cast(
+            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, kNonTemporal));
+        const int64_t i0 = rs + ((int64_t)(2 * pq) < (int64_t)nblk ? (int64_t)(2 * pq) : (int64_t)nblk - 1);
+        const int64_t i1 = rs + ((int64_t)(2 * pq + 1) < (int64_t)nblk ? (int64_t)(2 * pq + 1) : (int64_t)nblk - 1);
+        P.c0 = block_col_scalar(bci[i0]);
+        P.c1 = block_col_scalar(bci[i1]);
+    };
+
+    // One compaction MFMA into D_h: column lanes in `mine` (slots 16h ..
+    // 16h+15) set their S^T entry before the read and clear it after; the
+    // other lanes write to the pad bytes of their S^T row, which no read sees.
+    const uint16_t h_one = 0x3c00u;  // fp16 1.0
+    auto round = [&](float4_t& d, bool mine, uint32_t st, const half8_t& pa) {
+        const uint32_t at = mine ? st : st_pad;
+        *reinterpret_cast<uint16_t*>(W + at) = h_one;
+        const half8_t x =
+            __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4_t*>(W + st_rd));
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, pa, d, 0, 0, 0);
+        *reinterpret_cast<uint16_t*>(W + at) = (uint16_t)0u;
+    };
+
+    auto process = [&](const BatchA& P) {
+        const uint32_t c0 = P.c0;
+        const uint32_t c1 = P.c1;
+        const u32x4_t w = __builtin_bit_cast(u32x4_t, P.a);
+        uint32_t nz[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t x = w[d];
+            nz[d] = __builtin_bit_cast(
+                uint32_t, __builtin_elementwise_min(__builtin_bit_cast(ushort2_t, x),
+                                                    __builtin_bit_cast(ushort2_t, one)));
+        }
+        uint32_t v = nz[0] | (nz[1] << 2) | (nz[2] << 4) | (nz[3] << 6);
+        v = ((v | (v >> 15)) & 0xffu) << gshift;
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+        const uint32_t valid = (c0 < kb32 ? 0x0000ffffu : 0u) | (c1 < kb32 ? 0xffff0000u : 0u);
+        const uint32_t pm = (uint32_t)__builtin_amdgcn_readlane((int)v, 63) & valid;
+        if (pm == 0u) return;
+        const uint32_t cnt = (uint32_t)__builtin_popcount(pm);
+        if (pending + cnt > 32u) {
+            start(pending);
+            pending = 0;
+        }
+        if constexpr (MODE != BatchMode::kCount) {
+            const bool set = (pm & bitk) != 0u;
+            const uint32_t rank = (uint32_t)__builtin_popcount(pm & (bitk - 1u)) + pending;
+            const uint32_t cb = 16u * (sel ? c1 : c0) + row_k;
+            *reinterpret_cast<uint32_t*>(W + (set ? kSlotOff + 4u * rank : kSlotPad)) = cb;
+            const uint32_t st = (rank & 15u) * (uint32_t)kApStride + st_k;
+            const half8_t pa = P.a;
+            const bool lo = rank < 16u;
+            if (pending < 16u) round(d0, set & lo, st, pa);
+            if (pending + cnt > 16u) round(d1, set & !lo, st, pa);
+        }
+        pending += cnt;
+    };
+
+    if (wave < npairs) {
+        BatchA P0, P1, P2, P3, P4, P5;
+        constexpr int S = 4;
+        constexpr int A = S * kBatchDepth;
+        const int64_t q0 = wave;
+        stage_a(q0, P0);
+        stage_a(q0 + S, P1);
+        stage_a(q0 + 2 * S, P2);
+        stage_a(q0 + 3 * S, P3);
+        if constexpr (kBatchDepth > 4) stage_a(q0 + 4 * S, P4);
+        if constexpr (kBatchDepth > 5) stage_a(q0 + 5 * S, P5);
+        for (int64_t q = q0; q < npairs; q += A) {
+            process(P0);
+            stage_a(q + A, P0);
+            process(P1);
+            stage_a(q + A + S, P1);
+            process(P2);
+            stage_a(q + A + 2 * S, P2);
+            process(P3);
+            stage_a(q + A + 3 * S, P3);
+            if constexpr (kBatchDepth > 4) {
+                process(P4);
+                stage_a(q + A + 4 * S, P4);
+            }
+            if constexpr (kBatchDepth > 5) {
+                process(P5);
+                stage_a(q + A + 5 * S, P5);
+            }
+        }
+        if (pending > 0u) start(pending);
+        if constexpr (MODE == BatchMode::kMultiply) {
+            if (started) finish();
+        }
+    }
+    if constexpr (MODE == BatchMode::kCount) {
+        if (lane == 0) pk.counts[br * 4 + wave] = (int32_t)nbatch;
+        return;
+    } else if constexpr (MODE == BatchMode::kPack) {
+        return;
+    } else {
+        batch_tile_store<I, NT>(acc, smem, wave, g, li, br, n0, M, N, C, row_map);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Multiply packed column batches (written by the batch kernel in pack mode).
 // Wave w of the workgroup of block-row br multiplies the batches
 // [offsets[4 br + w], offsets[4 br + w + 1]) in order: the stored A' operand,
@@ -1093,6 +1380,18 @@ __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __res
 }
 
 // Launch geometry: waves per workgroup and 16-column tiles per wave.
+// Column-batch kernel used by the Tier-1 launcher and by the prepared products'
+// count and pack passes (they must be the same kernel: packed batches carry
+// its operand order).
+#ifndef XSPMM_BATCH_COMPACT
+#define XSPMM_BATCH_COMPACT 1
+#endif
+#if XSPMM_BATCH_COMPACT
+#define XSPMM_BATCH_KERNEL spmm_f16_cbatch_kernel
+#else
+#define XSPMM_BATCH_KERNEL spmm_f16_batch_kernel
+#endif
+
 struct Geometry {
     int ntw;
     int waves;
@@ -1153,7 +1452,7 @@ void spmm_f16_pack_count(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* 
                          const uint16_t* bvals, int32_t* counts, hipStream_t s)
 {
     BatchPack pk{counts, nullptr, nullptr, nullptr};
-    hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kCount>), dim3((unsigned)Mb, 1),
+    hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 1, BatchMode::kCount>), dim3((unsigned)Mb, 1),
                        dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
                        nullptr, nullptr, pk);
     XSPMM_LAUNCH_CHECK();
@@ -1165,7 +1464,7 @@ void spmm_f16_pack_fill(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
                         hipStream_t s)
 {
     BatchPack pk{nullptr, offsets, static_cast<u32x4_t*>(a), rows};
-    hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kPack>), dim3((unsigned)Mb, 1),
+    hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 1, BatchMode::kPack>), dim3((unsigned)Mb, 1),
                        dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
                        nullptr, nullptr, pk);
     XSPMM_LAUNCH_CHECK();
@@ -1276,16 +1575,16 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
                 order = order_buf.as<int32_t>();
             }
             if (N <= 16)
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 32)
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 64)
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             XSPMM_LAUNCH_CHECK();
             return true;
