@@ -892,6 +892,18 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_ker
 // g of each lane and OR-ed over the wave by DPP (row rotations, then the two
 // row broadcasts), so lane 63 holds the 32-bit pair mask.
 // ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) unsigned char lds_u8_t;
+// byte address in LDS of a pointer into a __shared__ array, and back
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return (uint32_t)(uintptr_t)(const lds_u8_t*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(3))) T* lds_ptr(uint32_t a)
+{
+    return (__attribute__((address_space(3))) T*)(uintptr_t)a;
+}
+
 __device__ __forceinline__ constexpr uint32_t kslot(uint32_t k)
 {
     return 16u * ((k >> 2) & 1u) + 4u * (k >> 3) + (k & 3u);
@@ -904,6 +916,7 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
     int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map, BatchPack pk)
 {
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
+    static_assert(4 * kBatchDepth <= kWave, "one index window per ring pass");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
     constexpr int RPL = 64 / CPR;  // B rows per load instruction
     constexpr uint32_t kSel = kApOff;  // S^T: 16 rows x kApStride bytes
@@ -926,29 +939,49 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
     const int sel = lane >> 5;
     const int kh = g & 1;
 
+    // A of this row and its block columns: reads past either return zeros
     const uint32_t nblk = (uint32_t)(re - rs);
     const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + rs * 256, nblk * 512u);
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(bci + rs, nblk * (uint32_t)sizeof(I));
     const uint32_t b_bytes = (uint32_t)(K * N * 2);
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
     const uint32_t a_voff = (uint32_t)(sel * 512 + li * 32 + kh * 16);
     const uint32_t kb32 = (uint32_t)Kb;
     const uint32_t k32 = (uint32_t)K;
     const uint32_t rowbytes = (uint32_t)(2 * N);
+    // index window of one ring pass (pairs q, q + 4, ..., q + 4 (depth - 1)
+    // of this wave): lane l holds dword l of their block columns in order,
+    // so pair j's columns sit in lanes 2j, 2j + 1 (int64: 4j .. 4j + 3)
+    const uint32_t cw_off = sizeof(I) == 4
+                                ? 32u * (uint32_t)(lane >> 1) + 4u * (uint32_t)(lane & 1)
+                                : 64u * (uint32_t)(lane >> 2) + 8u * (uint32_t)((lane >> 1) & 1) +
+                                      4u * (uint32_t)(lane & 1);
 
     // --- per-lane constants --------------------------------------------------
-    // column lanes: lane (i < 8, g) stands for pair column 8g + i (bit 8g + i
-    // of the pair mask); the other lanes never match a bit
-    const uint32_t bitk = li < 8 ? 1u << (8 * g + li) : 0u;
-    const uint32_t lowk = bitk - 1u;
-    // its S^T entry: row (slot & 15), half 8g + i; lanes without a column
+    // Pair mask layout: lane (r, g)'s non-zero halves 2d go to bit 4g + d and
+    // halves 2d + 1 to bit 16 + 4g + d, so the four groups never overlap.
+    // Column lane (i < 8, g) stands for bit 16 (i >> 2) + 4g + (i & 3), i.e.
+    // half e = 2 (i & 3) + (i >> 2) of group g (pair column 8g + e); the other
+    // lanes never match a bit.
+    const int ce = 2 * (li & 3) + ((li >> 2) & 1);
+    const uint32_t bitk = li < 8 ? 1u << (16 * ((li >> 2) & 1) + 4 * g + (li & 3)) : 0u;
+    // its S^T entry: row (slot & 15), half 8g + e; lanes without a column
     // write to pad bytes 64.. of S^T row li, which no read covers
-    const uint32_t st_k = kSel + 2u * (uint32_t)(8 * g + li);
-    const uint32_t st_pad = kSel + (uint32_t)(li * kApStride + 64 + 2 * g);
-    // its B row: 16 * (block column of block sel) + 8 kh + i
-    const uint32_t row_k = (uint32_t)(8 * kh + li);
+    // (LDS byte addresses, kept in VGPRs so that each access costs one
+    // address instruction)
+    uint32_t st_k = lds_addr(W + kSel + 2 * (8 * g + ce));
+    uint32_t st_pad = lds_addr(W + kSel + li * kApStride + 64 + 2 * g);
+    uint32_t slot_w = lds_addr(W + kSlotOff);
+    uint32_t slot_pad = lds_addr(W + kSlotPad);
+    // ds_bpermute address of this lane's block column in the index window
+    // (pair j adds 8 j, int64: 16 j)
+    const uint32_t csel_addr = 4u * (uint32_t)sel * (uint32_t)(sizeof(I) / 4);
+    // its B row: 16 * (block column of block sel) + 8 kh + e
+    const uint32_t row_k = (uint32_t)(8 * kh + ce);
     // selection lanes: S^T row li, halves 8g .. 8g+7
-    const uint32_t st_rd = kSel + (uint32_t)(li * kApStride + 16 * g);
-    const uint32_t gshift = (uint32_t)(8 * g);
+    uint32_t st_rd = lds_addr(W + kSel + li * kApStride + 16 * g);
+    asm volatile("" : "+v"(st_k), "+v"(st_pad), "+v"(slot_w), "+v"(slot_pad), "+v"(st_rd));
+    const uint32_t gshift = (uint32_t)(4 * g);
     // B row loads: load t moves tile row t * RPL + lane / CPR, chunk lane % CPR
     const uint32_t ld_c = (uint32_t)(lane % CPR);
     const uint32_t ld_r = (uint32_t)(lane / CPR);
@@ -1042,14 +1075,13 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
         started = true;
     };
 
-    auto stage_a = [&](int64_t q, BatchA& P) {
-        const uint32_t pq = (uint32_t)q;
-        P.a = __builtin_bit_cast(
-            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, kNonTemporal));
-        const int64_t i0 = rs + ((int64_t)(2 * pq) < (int64_t)nblk ? (int64_t)(2 * pq) : (int64_t)nblk - 1);
-        const int64_t i1 = rs + ((int64_t)(2 * pq + 1) < (int64_t)nblk ? (int64_t)(2 * pq + 1) : (int64_t)nblk - 1);
-        P.c0 = block_col_scalar(bci[i0]);
-        P.c1 = block_col_scalar(bci[i1]);
+    auto stage_a = [&](int64_t q, half8_t& P) {
+        P = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                            a_rsrc, (int)(a_voff + (uint32_t)q * 1024u), 0, kNonTemporal));
+    };
+    auto load_cols = [&](int64_t q) -> uint32_t {
+        return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+            c_rsrc, (int)(cw_off + (uint32_t)q * (uint32_t)(2 * sizeof(I))), 0, 0);
     };
 
     // One compaction MFMA into D_h: column lanes in `mine` (slots 16h ..
@@ -1058,17 +1090,32 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
     const uint16_t h_one = 0x3c00u;  // fp16 1.0
     auto round = [&](float4_t& d, bool mine, uint32_t st, const half8_t& pa) {
         const uint32_t at = mine ? st : st_pad;
-        *reinterpret_cast<uint16_t*>(W + at) = h_one;
-        const half8_t x =
-            __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4_t*>(W + st_rd));
+        *lds_ptr<uint16_t>(at) = h_one;
+        const half8_t x = __builtin_bit_cast(half8_t, *lds_ptr<const u32x4_t>(st_rd));
         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, pa, d, 0, 0, 0);
-        *reinterpret_cast<uint16_t*>(W + at) = (uint16_t)0u;
+        *lds_ptr<uint16_t>(at) = (uint16_t)0u;
     };
 
-    auto process = [&](const BatchA& P) {
-        const uint32_t c0 = P.c0;
-        const uint32_t c1 = P.c1;
-        const u32x4_t w = __builtin_bit_cast(u32x4_t, P.a);
+    // pair j of the ring pass whose index window is `win`
+    auto process = [&](const half8_t& pa, uint32_t win, int j) {
+        uint32_t c0, c1;
+        // this lane's block column (lane l: block l >> 5 of the pair)
+        uint32_t csel;
+        if constexpr (sizeof(I) == 4) {
+            c0 = (uint32_t)__builtin_amdgcn_readlane((int)win, 2 * j);
+            c1 = (uint32_t)__builtin_amdgcn_readlane((int)win, 2 * j + 1);
+            csel = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(csel_addr + 8u * (uint32_t)j), (int)win);
+        } else {
+            const uint32_t l0 = (uint32_t)__builtin_amdgcn_readlane((int)win, 4 * j);
+            const uint32_t h0 = (uint32_t)__builtin_amdgcn_readlane((int)win, 4 * j + 1);
+            const uint32_t l1 = (uint32_t)__builtin_amdgcn_readlane((int)win, 4 * j + 2);
+            const uint32_t h1 = (uint32_t)__builtin_amdgcn_readlane((int)win, 4 * j + 3);
+            c0 = h0 == 0u ? l0 : 0xffffffffu;
+            c1 = h1 == 0u ? l1 : 0xffffffffu;
+            // the low dword is enough: a set bit implies a valid column
+            csel = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(csel_addr + 16u * (uint32_t)j), (int)win);
+        }
+        const u32x4_t w = __builtin_bit_cast(u32x4_t, pa);
         uint32_t nz[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -1077,15 +1124,16 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
                 uint32_t, __builtin_elementwise_min(__builtin_bit_cast(ushort2_t, x),
                                                     __builtin_bit_cast(ushort2_t, one)));
         }
-        uint32_t v = nz[0] | (nz[1] << 2) | (nz[2] << 4) | (nz[3] << 6);
-        v = ((v | (v >> 15)) & 0xffu) << gshift;
+        uint32_t v = (nz[0] | (nz[1] << 1) | (nz[2] << 2) | (nz[3] << 3)) << gshift;
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
         v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
-        const uint32_t valid = (c0 < kb32 ? 0x0000ffffu : 0u) | (c1 < kb32 ? 0xffff0000u : 0u);
+        // block 0 owns groups 0 and 1 (bits 0..7, 16..23), block 1 the rest; a
+        // block column outside the grid (malformed input) contributes nothing
+        const uint32_t valid = (c0 < kb32 ? 0x00ff00ffu : 0u) | (c1 < kb32 ? 0xff00ff00u : 0u);
         const uint32_t pm = (uint32_t)__builtin_amdgcn_readlane((int)v, 63) & valid;
         if (pm == 0u) return;
         const uint32_t cnt = (uint32_t)__builtin_popcount(pm);
@@ -1096,10 +1144,8 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
         if constexpr (MODE != BatchMode::kCount) {
             const bool set = (pm & bitk) != 0u;
             const uint32_t rank = (uint32_t)__builtin_popcount(pm & (bitk - 1u)) + pending;
-            const uint32_t cb = 16u * (sel ? c1 : c0) + row_k;
-            *reinterpret_cast<uint32_t*>(W + (set ? kSlotOff + 4u * rank : kSlotPad)) = cb;
-            const uint32_t st = (rank & 15u) * (uint32_t)kApStride + st_k;
-            const half8_t pa = P.a;
+            *lds_ptr<uint32_t>(set ? slot_w + 4u * rank : slot_pad) = 16u * csel + row_k;
+            const uint32_t st = st_k + (rank & 15u) * (uint32_t)kApStride;
             const bool lo = rank < 16u;
             if (pending < 16u) round(d0, set & lo, st, pa);
             if (pending + cnt > 16u) round(d1, set & !lo, st, pa);
@@ -1108,10 +1154,13 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
     };
 
     if (wave < npairs) {
-        BatchA P0, P1, P2, P3, P4, P5;
+        half8_t P0, P1, P2, P3, P4, P5;
         constexpr int S = 4;
         constexpr int A = S * kBatchDepth;
         const int64_t q0 = wave;
+        // the window before the A loads, as in every later pass, so the
+        // loads complete in the same order on the first pass
+        uint32_t win = load_cols(q0);
         stage_a(q0, P0);
         stage_a(q0 + S, P1);
         stage_a(q0 + 2 * S, P2);
@@ -1119,22 +1168,25 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
         if constexpr (kBatchDepth > 4) stage_a(q0 + 4 * S, P4);
         if constexpr (kBatchDepth > 5) stage_a(q0 + 5 * S, P5);
         for (int64_t q = q0; q < npairs; q += A) {
-            process(P0);
+            // next pass's window, issued a pass ahead like the A loads
+            const uint32_t nwin = load_cols(q + A);
+            process(P0, win, 0);
             stage_a(q + A, P0);
-            process(P1);
+            process(P1, win, 1);
             stage_a(q + A + S, P1);
-            process(P2);
+            process(P2, win, 2);
             stage_a(q + A + 2 * S, P2);
-            process(P3);
+            process(P3, win, 3);
             stage_a(q + A + 3 * S, P3);
             if constexpr (kBatchDepth > 4) {
-                process(P4);
+                process(P4, win, 4);
                 stage_a(q + A + 4 * S, P4);
             }
             if constexpr (kBatchDepth > 5) {
-                process(P5);
+                process(P5, win, 5);
                 stage_a(q + A + 5 * S, P5);
             }
+            win = nwin;
         }
         if (pending > 0u) start(pending);
         if constexpr (MODE == BatchMode::kMultiply) {
