@@ -6,23 +6,25 @@
 // blocks become zero.  Rows >= M are not stored; B rows >= K and columns >= N
 // contribute nothing.
 //
-// fp16 path.  MFMA operands want K contiguous in every lane, while B is
-// row-major (N contiguous).  B is therefore first repacked into 16-row panels
-// laid out [block_col][n][k16] (pack_b_panels), zero-padded beyond K and N.
-// Two consecutive blocks of a block-row then form one K=32 operand pair for
-// v_mfma_f32_16x16x32_f16:
-//   A operand, lane l: block (l>>5), row l&15, k = 8*((l>>4)&1) .. +8  (16 bytes)
-//   B operand, lane l: panel of the same block, n = l&15, the same 8 k
-// so one 16-byte load per lane fetches each operand.  Output lane l holds
-// C[4*(l>>4) + r][l&15], r = 0..3.
+// fp16 kernels (v_mfma_f32_16x16x32_f16; MFMA operands want K contiguous in
+// every lane while B is row-major, so B reaches the matrix cores either through
+// the gfx950 LDS transpose read or through a repacked copy):
+//   spmm_f16_batch_kernel   default (N % 8 == 0): the non-zero block columns of
+//                           a row's block pairs are compacted into K = 32
+//                           batches and multiplied with their gathered B rows;
+//                           count / pack modes store the batches for
+//                           spmm_f16_packed_kernel (prepared products);
+//   spmm_f16_dense_kernel   (spmm_dense.hip) fully populated block grids;
+//   spmm_f16_gather_kernel  per-pair masked B-row gather (XSPMM_SPMM_KERNEL=gather);
+//   pack_b_panels + spmm_f16_kernel  any N: B repacked into 16-row panels laid
+//                           out [block_col][n][k16], two blocks per K = 32 operand.
 //
 // fp32 path.  v_mfma_f32_16x16x4f32 takes one k per lane, so B is read
 // row-major directly: lane l loads A[l&15][4g .. 4g+3] (g = l>>4) once per block
 // and issues four MFMAs, step s pairing A[i][4g+s] with B[16*col + 4g + s][n].
 //
-// Work split: one workgroup per block-row (grid.x), its waves own disjoint
-// groups of NTW 16-column tiles of C (grid.y covers wide N).  All waves of a
-// workgroup walk the same A blocks, which stay in the CU's L1.
+// Work split: one workgroup per block-row (grid.x, or the dispatch order of
+// order_rows_kernel), N split over grid.y.
 #include <cstdlib>
 #include <string>
 
@@ -468,45 +470,55 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
 }
 
 // ---------------------------------------------------------------------------
-// fp16 "column batch" tile kernel.
+// fp16 "column batch" tile kernel (the Tier-1 default where N % 8 == 0).
 //
 // All blocks of a block-row add into the same 16 rows of C, so the K extent
 // of a multiply does not have to follow block boundaries: the non-zero
 // columns of any blocks of the row can be stacked into one K = 32 operand.
-// Each wave streams its share of the row's block pairs and
-//   1. loads a pair in MFMA A-operand layout (16 bytes per lane), four pairs
-//      ahead of use;
+// The four waves of a workgroup take the row's block pairs in turn (wave w:
+// pairs w, w + 4, ...) and each wave
+//   1. streams its pairs in MFMA operand layout (16 bytes per lane, lane
+//      (r, g): row r, pair columns 8g .. 8g+7; non-temporal loads, kBatchDepth
+//      pairs in flight) and, one vector load per ring pass, the pairs' block
+//      columns;
 //   2. forms the pair's 32-bit mask of columns holding a non-zero (per-lane
-//      8-bit masks OR-ed over the 16 lanes of a k group by DPP);
-//   3. appends the masked columns to a batch of 32 K slots: the 16 values of
-//      each column go to A'[row][slot] in LDS (written by the 16 lanes that
-//      hold them, zeros included, so slots never need clearing) and the
-//      column's B row index to a slot list;
-//   4. when a pair does not fit the batch, starts the batch: reads its A'
-//      operand and issues the 16-byte loads of its 32 B rows (unused slots
-//      get an out-of-range offset, which reads zeros without touching memory);
-//      A pair with more than 24 non-zero columns is a batch by itself: its
-//      A registers are stored as the 32 slots in one go and its B rows are
-//      the two blocks' 16-row panels;
-//   5. one batch later (so the row loads have long arrived) writes those rows
-//      row-major into an LDS tile, reads them back with the gfx950 transpose
-//      read ds_read_b64_tr_b16 as MFMA B operands and issues one
-//      v_mfma_f32_16x16x32_f16 per 16-column tile.
-// Every masked column of every block goes through an MFMA; columns that are
-// zero in all 16 rows of a block are skipped, as they add exact zeros.
-// The four waves of a workgroup take the row's pairs in turn and their
-// partial tiles are summed in LDS.  grid = (block-rows, ceil(N / 128));
-// N % 8 == 0 and K * N * 2 <= 2^31 on this path.
+//      masks OR-ed over the wave by DPP);
+//   3. appends the masked columns to a batch of 32 K slots.  The columns are
+//      moved into their slots on the matrix cores: with the pair as the B
+//      operand and a one-hot selection S^T (16 slots x 32 pair columns) as
+//      the A operand,
+//          D_h += S_h^T * pair^T
+//      accumulates the transposed A' of slots 16h .. 16h+15 (lane (r, g) of
+//      D_h holds A'[r][16h + 4g .. +3]).  Each D entry receives one product
+//      x * 1.0 and zeros, so the compaction is exact (a -0.0 entry becomes
+//      +0.0, which changes no sum of products).  S^T lives in LDS, all zero
+//      between pairs: column lane (i < 8, g) of a set pair column writes 1.0
+//      at [slot][column] before the read and 0 after it, and the column's B
+//      row index into the slot list;
+//   4. when a pair does not fit, closes the batch: converts D to the fp16 A'
+//      operand, multiplies the previous batch, and issues the 16-byte loads
+//      of this batch's B rows (unused slots get an out-of-range offset, which
+//      reads zeros without touching memory);
+//   5. one batch later (the row loads have long arrived) writes those rows
+//      row-major into an XOR-swizzled LDS tile, reads them back with the
+//      gfx950 transpose read ds_read_b64_tr_b16 as MFMA B operands and issues
+//      one v_mfma_f32_16x16x32_f16 per 16-column tile.
+// A' carries, in MFMA K position k of lane group g (k = 8g .. 8g+7), slot
+// kslot(k) = 16 ((k >> 2) & 1) + 4 (k >> 3) + (k & 3); tile row k holds that
+// slot's B row.  Columns that are zero in all 16 rows of a block are skipped:
+// they add exact zeros.  The waves' partial tiles are summed in LDS.
+// grid = (block-rows, ceil(N / 128)); N % 8 == 0 and K * N * 2 <= 2^31.
 //
-// Per-wave LDS: B' tile 32 rows x 256 B (16-byte chunk c of row e stored at
+// Per-wave LDS: B tile 32 rows x 256 B (16-byte chunk c of row e stored at
 // chunk c ^ swz(e), which spreads the 16 rows one transpose read touches over
-// all banks), A' 16 rows x 80 B (32 slots + pad), slot list 32 x 4 B.
+// all banks), S^T 16 rows x 80 B (32 halves + pad: conflict-free 16-byte
+// reads), slot list 32 x 4 B.
 // ---------------------------------------------------------------------------
 constexpr int kBtRow = 256;
 constexpr int kBtBytes = 32 * kBtRow;
 constexpr int kApStride = 80;
-constexpr int kApOff = kBtBytes;
-constexpr int kSlotOff = kApOff + 16 * kApStride;
+constexpr int kApOff = kBtBytes;                     // S^T
+constexpr int kSlotOff = kApOff + 16 * kApStride;    // slot list
 constexpr int kBatchWaveLds = kSlotOff + 32 * 4;
 // each wave's region starts 16-byte aligned (128-bit LDS accesses)
 static_assert(kBatchWaveLds % 16 == 0 && kApOff % 16 == 0 && kSlotOff % 16 == 0,
@@ -518,8 +530,6 @@ static_assert(kBatchWaveLds % 16 == 0 && kApOff % 16 == 0 && kSlotOff % 16 == 0,
 #define XSPMM_BATCH_MIN_WAVES 1
 #endif
 constexpr int kBatchDepth = XSPMM_BATCH_DEPTH;  // A pairs in flight per wave (4..6)
-// a pair with more non-zero columns than this multiplies as a whole
-constexpr uint32_t kFullPairCols = 24;
 static_assert(kBatchDepth >= 4 && kBatchDepth <= 6, "batch depth must be 4, 5 or 6");
 
 // swizzle of row e: even values 0..14, each used by two of the 16 rows a
@@ -527,20 +537,6 @@ static_assert(kBatchDepth >= 4 && kBatchDepth <= 6, "batch depth must be 4, 5 or
 __device__ __forceinline__ uint32_t bt_swz(uint32_t e)
 {
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
-}
-
-struct BatchA {
-    half8_t a;    // A operand of the pair (in flight)
-    uint32_t c0;  // block columns of its two blocks (wave-uniform)
-    uint32_t c1;
-};
-
-// Low dword of a block column read with a wave-uniform address; an int64
-// index with a non-zero high dword becomes 0xffffffff (never a valid column).
-__device__ __forceinline__ uint32_t block_col_scalar(int32_t c) { return (uint32_t)c; }
-__device__ __forceinline__ uint32_t block_col_scalar(int64_t c)
-{
-    return ((uint64_t)c >> 32) == 0u ? (uint32_t)c : 0xffffffffu;
 }
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -599,299 +595,6 @@ __device__ __forceinline__ void batch_tile_store(const float4_t (&acc)[NT], unsi
     }
 }
 
-template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply>
-__global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_batch_kernel(const I* __restrict__ brp,
-                                                             const I* __restrict__ bci,
-                                                             const uint16_t* __restrict__ vals,
-                                                             const uint16_t* __restrict__ B,
-                                                             float* __restrict__ C, int64_t M,
-                                                             int64_t K, int64_t N, int64_t Kb,
-                                                             const int32_t* __restrict__ order,
-                                                             const I* __restrict__ row_map,
-                                                             BatchPack pk)
-{
-    static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
-    constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
-    constexpr int RPL = 64 / CPR;  // B rows per load instruction
-    __shared__ __align__(16) unsigned char smem[4 * kBatchWaveLds];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    unsigned char* const W = smem + wave * kBatchWaveLds;
-
-    // block-row: in dispatch order, or longest rows first when `order` is given
-    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
-    const int64_t n0 = (int64_t)blockIdx.y * 128;
-    const int64_t rs = brp[br];
-    const int64_t re = brp[br + 1];
-    const int64_t npairs = (re - rs + 1) >> 1;
-
-    const int li = lane & 15;
-    const int g = lane >> 4;
-    const int sel = lane >> 5;
-    const int kh = g & 1;
-
-    // --- buffer resources (reads past them return zeros) ---------------------
-    // The four waves take the row's pairs in turn (wave w: pairs w, w + 4,
-    // ...), so the workgroup reads the row front to back.  A is read with the
-    // non-temporal hint: it is used once and should not push B out of L2.
-    const uint32_t nblk = (uint32_t)(re - rs);
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + rs * 256, nblk * 512u);
-    const uint32_t b_bytes = (uint32_t)(K * N * 2);
-    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
-    const uint32_t a_voff = (uint32_t)(sel * 512 + li * 32 + kh * 16);
-    const uint32_t kb32 = (uint32_t)Kb;
-    const uint32_t k32 = (uint32_t)K;
-    const uint32_t rowbytes = (uint32_t)(2 * N);
-
-    // --- per-lane constants --------------------------------------------------
-    // A' slot writes: row li, byte li * kApStride + 2 * slot
-    const uint32_t ap_row = (uint32_t)(kApOff + li * kApStride);
-    // groups below this lane's group in the 32-bit pair mask
-    const uint32_t below_group = (1u << (8 * g)) - 1u;
-    // B row loads: load t moves row t * RPL + lane / CPR, chunk lane % CPR
-    const uint32_t ld_c = (uint32_t)(lane % CPR);
-    const uint32_t ld_r = (uint32_t)(lane / CPR);
-    const uint32_t ld_off = (uint32_t)(2 * n0) + 16u * ld_c;
-    // transpose reads: row 8g + 4h + (li >> 2), 8-byte piece of chunk
-    // 2j + ((li & 3) >> 1), byte 8 * (li & 1) within the chunk
-    const uint32_t tr_e0 = (uint32_t)(8 * g + (li >> 2));
-    // rows e and e + 4 share the swizzle (e & 4 == 0 here), so the second
-    // read of a tile sits 4 rows (1 KB) after the first
-    const uint32_t tr_base = tr_e0 * kBtRow + 16u * ((li & 3) >> 1) + 8u * (li & 1);
-    const uint32_t tr_swz16 = bt_swz(tr_e0) << 4;
-    // 0x00010001 from an SGPR the optimiser cannot see through, so
-    // min(halves, one) stays a single packed integer instruction
-    uint32_t one;
-    asm("s_mov_b32 %0, 0x10001" : "=s"(one));
-
-    // A' starts as zeros: a partial batch multiplies its unused slots (B rows
-    // read as zeros) and uninitialised LDS could hold non-finite bit patterns.
-    // Later batches leave finite values from earlier batches there.
-    for (int i = lane; i < 16 * kApStride / 4; i += kWave)
-        reinterpret_cast<uint32_t*>(W + kApOff)[i] = 0u;
-
-    float4_t acc[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    u32x4_t bv[NT];      // B rows of the started batch (in flight)
-    half8_t aop{};       // A' operand of the started batch
-    bool started = false;
-    uint32_t pending = 0;  // slots filled in the open batch (wave-uniform)
-
-    // Multiply the started batch: rows into the tile, transpose reads, MFMA.
-    auto finish = [&]() {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const uint32_t e = (uint32_t)(t * RPL) + ld_r;
-            *reinterpret_cast<u32x4_t*>(W + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[t];
-        }
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t a = tr_base + ((uint32_t)(32 * j) ^ tr_swz16);
-            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a));
-            const short4_t hi =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a + 4 * kBtRow));
-            const half8_t bop = __builtin_bit_cast(
-                half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
-        }
-    };
-    // Close the open batch of `cnt` slots: multiply the previous one, then
-    // read this one's A' operand and issue its row loads.
-    int64_t nbatch = 0;  // batches formed so far (count and pack modes)
-    int64_t pbase = 0;   // first output batch of this wave (pack mode)
-    if constexpr (MODE == BatchMode::kPack) pbase = pk.offsets[br * 4 + wave];
-    auto start = [&](uint32_t cnt) {
-        if constexpr (MODE != BatchMode::kMultiply) {
-            if constexpr (MODE == BatchMode::kPack) {
-                const int64_t bi = pbase + nbatch;
-                pk.a[bi * 64 + lane] = *reinterpret_cast<const u32x4_t*>(W + ap_row + 16u * (uint32_t)g);
-                if (lane < 32) {
-                    const uint32_t r = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * (uint32_t)lane);
-                    pk.rows[bi * 32 + lane] = (uint32_t)lane < cnt ? r : 0xffffffffu;
-                }
-            }
-            ++nbatch;
-            return;
-        }
-        if (started) finish();
-        aop = __builtin_bit_cast(half8_t,
-                                 *reinterpret_cast<const u32x4_t*>(W + ap_row + 16u * (uint32_t)g));
-        // all slot rows first (one LDS wait), then the loads
-        uint32_t row[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-            row[t] = *reinterpret_cast<const uint32_t*>(W + kSlotOff + 4u * ld_r +
-                                                        4u * (uint32_t)(t * RPL));
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            // slot t * RPL + ld_r is filled iff ld_r < cnt - t * RPL
-            const bool use = ((int)ld_r < (int)cnt - t * RPL) & (row[t] < k32);
-            const uint32_t at = __umul24(row[t], rowbytes) + ld_off;
-            const uint32_t off = use ? at : b_bytes + ld_off;
-            bv[t] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
-        }
-        started = true;
-    };
-
-    // Stage A: the pair's A operand (buffer load, zeros past this wave's
-    // blocks) and its two block columns (scalar loads at indices clamped into
-    // this wave's blocks; a clamped column only meets zero A data).
-    auto stage_a = [&](int64_t q, BatchA& P) {
-        const uint32_t pq = (uint32_t)q;
-        P.a = __builtin_bit_cast(
-            half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)(a_voff + pq * 1024u), 0, kNonTemporal));
-        const int64_t i0 = rs + ((int64_t)(2 * pq) < (int64_t)nblk ? (int64_t)(2 * pq) : (int64_t)nblk - 1);
-        const int64_t i1 = rs + ((int64_t)(2 * pq + 1) < (int64_t)nblk ? (int64_t)(2 * pq + 1) : (int64_t)nblk - 1);
-        P.c0 = block_col_scalar(bci[i0]);
-        P.c1 = block_col_scalar(bci[i1]);
-    };
-
-    auto process = [&](const BatchA& P) {
-        const uint32_t c0 = P.c0;
-        const uint32_t c1 = P.c1;
-        const u32x4_t w = __builtin_bit_cast(u32x4_t, P.a);
-        // bit e: half e of this lane's 8 is non-zero (a -0.0 counts as an
-        // entry; it adds an exact zero).  min(halves, 1) per dword is one
-        // packed instruction.  Each dword is copied to a scalar first:
-        // hipcc 7.2 compiles __builtin_bit_cast of a vector element w[d] as a
-        // read of element 0.
-        uint32_t nz[4];
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t x = w[d];
-            nz[d] = __builtin_bit_cast(
-                uint32_t, __builtin_elementwise_min(__builtin_bit_cast(ushort2_t, x),
-                                                    __builtin_bit_cast(ushort2_t, one)));
-        }
-        uint32_t v = nz[0] | (nz[1] << 2) | (nz[2] << 4) | (nz[3] << 6);
-        v = (v | (v >> 15)) & 0xffu;
-        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
-        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
-        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
-        v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
-        // a block column outside the grid (malformed input) contributes nothing
-        const uint32_t valid = (c0 < kb32 ? 0x0000ffffu : 0u) | (c1 < kb32 ? 0xffff0000u : 0u);
-        const uint32_t pm = ((uint32_t)__builtin_amdgcn_readlane((int)v, 0) |
-                             ((uint32_t)__builtin_amdgcn_readlane((int)v, 16) << 8) |
-                             ((uint32_t)__builtin_amdgcn_readlane((int)v, 32) << 16) |
-                             ((uint32_t)__builtin_amdgcn_readlane((int)v, 48) << 24)) &
-                            valid;
-        if (pm == 0u) return;
-        const uint32_t cnt = (uint32_t)__builtin_popcount(pm);
-        // A pair with more than kFullPairCols columns is a batch by itself:
-        // its A registers fill all 32 slots (slot e = column e of the pair,
-        // one 16-byte store per lane) and slot e's B row is row e & 15 of
-        // block e >> 4.  It stays open until the next pair or the end of the
-        // row, so a pair never starts two batches.
-        const bool full = cnt > kFullPairCols;
-        const uint32_t take = full ? 32u : cnt;
-        if (pending + take > 32u) {
-            start(pending);
-            pending = 0;
-        }
-        if (full) {
-            *reinterpret_cast<u32x4_t*>(W + ap_row + 16u * (uint32_t)g) = w;
-            if (lane < 32)
-                *reinterpret_cast<uint32_t*>(W + kSlotOff + 4u * (uint32_t)lane) =
-                    16u * (lane >= 16 ? c1 : c0) + (uint32_t)(lane & 15);
-        }
-        // this lane's group: its columns take consecutive slots from `base`
-        uint32_t rem = full ? 0u : (pm >> (8 * g)) & 0xffu;
-        const uint32_t base = pending + (uint32_t)__builtin_popcount(pm & below_group);
-        const uint32_t colbase = 16u * (sel ? c1 : c0) + 8u * (uint32_t)kh;
-        uint32_t slot = base;
-        do {
-            if (rem != 0u) {
-                const uint32_t b = (uint32_t)__builtin_ctz(rem);
-                rem &= rem - 1u;
-                const uint32_t word = (b & 4u) ? ((b & 2u) ? w[3] : w[2]) : ((b & 2u) ? w[1] : w[0]);
-                const uint16_t val = (uint16_t)(word >> ((b & 1u) << 4));
-                *reinterpret_cast<uint16_t*>(W + ap_row + 2u * slot) = val;
-                if (li == 0) *reinterpret_cast<uint32_t*>(W + kSlotOff + 4u * slot) = colbase + b;
-                ++slot;
-            }
-        } while (__builtin_amdgcn_ballot_w64(rem != 0u) != 0);
-        pending += take;
-    };
-
-    if (wave < npairs) {
-        // The ring is spelled out as separate variables: written as an
-        // unrolled loop over an array, hipcc 7.2 waits for every outstanding
-        // load at the top of each iteration instead of only for the oldest.
-        BatchA P0, P1, P2, P3, P4, P5;
-        constexpr int S = 4;                   // pair stride of a wave
-        constexpr int A = S * kBatchDepth;     // prefetch distance in pairs
-        const int64_t q0 = wave;
-        stage_a(q0, P0);
-        stage_a(q0 + S, P1);
-        stage_a(q0 + 2 * S, P2);
-        stage_a(q0 + 3 * S, P3);
-        if constexpr (kBatchDepth > 4) stage_a(q0 + 4 * S, P4);
-        if constexpr (kBatchDepth > 5) stage_a(q0 + 5 * S, P5);
-        for (int64_t q = q0; q < npairs; q += A) {
-            process(P0);
-            stage_a(q + A, P0);
-            process(P1);
-            stage_a(q + A + S, P1);
-            process(P2);
-            stage_a(q + A + 2 * S, P2);
-            process(P3);
-            stage_a(q + A + 3 * S, P3);
-            if constexpr (kBatchDepth > 4) {
-                process(P4);
-                stage_a(q + A + 4 * S, P4);
-            }
-            if constexpr (kBatchDepth > 5) {
-                process(P5);
-                stage_a(q + A + 5 * S, P5);
-            }
-        }
-        if (pending > 0u) start(pending);
-        if constexpr (MODE == BatchMode::kMultiply) {
-            if (started) finish();
-        }
-    }
-    if constexpr (MODE == BatchMode::kCount) {
-        if (lane == 0) pk.counts[br * 4 + wave] = (int32_t)nbatch;
-        return;
-    } else if constexpr (MODE == BatchMode::kPack) {
-        return;
-    } else {
-        batch_tile_store<I, NT>(acc, smem, wave, g, li, br, n0, M, N, C, row_map);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// fp16 column-batch kernel with the compaction on the matrix cores.
-//
-// Same batches as above (the non-zero block columns of a wave's pairs stacked
-// into K = 32 slots, then multiplied with their gathered B rows), but the
-// pair's columns are moved into their slots by an MFMA instead of per-column
-// LDS writes.  With the pair in registers as the B operand (lane (r, g): row
-// r, pair columns 8g .. 8g+7) and a one-hot selection S^T (16 slots x 32 pair
-// columns) as the A operand,
-//     D_h += S_h^T * pair^T
-// is the transposed A' of slots 16h .. 16h+15: lane (r, g) of D_h holds
-// A'[r][16h + 4g .. 16h + 4g + 3].  Each D entry receives one product
-// x * 1.0 and zeros, so the compaction is exact (a -0.0 entry becomes +0.0,
-// which changes no sum of products).  S^T lives in LDS (16 rows x 32 halves,
-// all zero between pairs): column lane (i < 8, g) of a set pair column
-// 8g + i writes 1.0 at [slot][8g + i] before the read and 0 after it, and its
-// B row index into the slot list.
-//
-// A' then carries, in MFMA K position k of lane group g (k = 8g .. 8g+7),
-// slot kslot(k) = 16 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3): the B tile row
-// of K position k holds the B row of slot kslot(k).  Pack mode stores A' and
-// the B rows in that K order, so spmm_f16_packed_kernel (tile row = K
-// position) multiplies the same operands in the same order.
-//
-// The per-pair column mask is formed as in the kernel above, placed in byte
-// g of each lane and OR-ed over the wave by DPP (row rotations, then the two
-// row broadcasts), so lane 63 holds the 32-bit pair mask.
-// ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) unsigned char lds_u8_t;
 // byte address in LDS of a pointer into a __shared__ array, and back
 __device__ __forceinline__ uint32_t lds_addr(const void* p)
@@ -904,13 +607,15 @@ __device__ __forceinline__ __attribute__((address_space(3))) T* lds_ptr(uint32_t
     return (__attribute__((address_space(3))) T*)(uintptr_t)a;
 }
 
+// batch slot carried in MFMA K position k of an A' operand (lane group
+// k >> 3 holds D_0 slots 4g .. 4g+3, then D_1 slots 16 + 4g .. +3)
 __device__ __forceinline__ constexpr uint32_t kslot(uint32_t k)
 {
     return 16u * ((k >> 2) & 1u) + 4u * (k >> 3) + (k & 3u);
 }
 
 template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply>
-__global__ __launch_bounds__(256, 4) void spmm_f16_cbatch_kernel(
+__global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
     int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map, BatchPack pk)
@@ -1432,18 +1137,6 @@ __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __res
 }
 
 // Launch geometry: waves per workgroup and 16-column tiles per wave.
-// Column-batch kernel used by the Tier-1 launcher and by the prepared products'
-// count and pack passes (they must be the same kernel: packed batches carry
-// its operand order).
-#ifndef XSPMM_BATCH_COMPACT
-#define XSPMM_BATCH_COMPACT 1
-#endif
-#if XSPMM_BATCH_COMPACT
-#define XSPMM_BATCH_KERNEL spmm_f16_cbatch_kernel
-#else
-#define XSPMM_BATCH_KERNEL spmm_f16_batch_kernel
-#endif
-
 struct Geometry {
     int ntw;
     int waves;
@@ -1504,7 +1197,7 @@ void spmm_f16_pack_count(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* 
                          const uint16_t* bvals, int32_t* counts, hipStream_t s)
 {
     BatchPack pk{counts, nullptr, nullptr, nullptr};
-    hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 1, BatchMode::kCount>), dim3((unsigned)Mb, 1),
+    hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kCount>), dim3((unsigned)Mb, 1),
                        dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
                        nullptr, nullptr, pk);
     XSPMM_LAUNCH_CHECK();
@@ -1516,7 +1209,7 @@ void spmm_f16_pack_fill(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
                         hipStream_t s)
 {
     BatchPack pk{nullptr, offsets, static_cast<u32x4_t*>(a), rows};
-    hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 1, BatchMode::kPack>), dim3((unsigned)Mb, 1),
+    hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kPack>), dim3((unsigned)Mb, 1),
                        dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
                        nullptr, nullptr, pk);
     XSPMM_LAUNCH_CHECK();
@@ -1627,16 +1320,16 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
                 order = order_buf.as<int32_t>();
             }
             if (N <= 16)
-                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 32)
-                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 64)
-                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else
-                hipLaunchKernelGGL((XSPMM_BATCH_KERNEL<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             XSPMM_LAUNCH_CHECK();
             return true;
