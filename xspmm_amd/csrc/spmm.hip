@@ -1051,14 +1051,16 @@ __global__ __launch_bounds__(kOrderThreads) void order_rows_kernel(const I* __re
 // fp32 x fp32 -> fp32 tile kernel.
 //
 // A workgroup of kF32Waves waves owns one block-row and NTW 16-column tiles
-// (up to 64 columns).  The waves split the row's blocks (wave w: blocks
-// w, w + kF32Waves, ...), two blocks per step with all their loads issued
-// before the MFMAs (v_mfma_f32_16x16x4_f32, four per block and tile), and
-// their partial tiles are summed through LDS in wave order.  Splitting the
-// row keeps short rows' dependent load chains short: a small matrix has few
-// block-rows, and one wave per row would leave the chip idle.
+// (up to 64 columns; the launcher narrows NTW when the grid would have fewer
+// than 512 workgroups).  The waves split the row's blocks (wave w: blocks
+// w, w + kF32Waves, ...), kF32Unroll blocks per step with all their loads
+// issued before the MFMAs (v_mfma_f32_16x16x4_f32, four per block and tile),
+// and their partial tiles are summed through LDS in wave order.  Splitting
+// the row keeps short rows' dependent load chains short: a small matrix has
+// few block-rows, and one wave per row would leave the chip idle.
 // ---------------------------------------------------------------------------
 constexpr int kF32Waves = 8;
+constexpr int kF32Unroll = 4;  // blocks per wave whose loads are in flight together
 
 template <typename I, int NTW>
 __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __restrict__ brp,
@@ -1102,18 +1104,22 @@ __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __res
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bv[j][s], acc[j], 0, 0, 0);
     };
 
+    // the wave's blocks rs + wave + 8 i in ascending order, kF32Unroll at a
+    // time: all their loads first, then their MFMAs
     int64_t blk = rs + wave;
-    for (; blk + kF32Waves < re; blk += 2 * kF32Waves) {
-        const float4_t a0 = *reinterpret_cast<const float4_t*>(vals + blk * 256 + li * 16 + g * 4);
-        const float4_t a1 =
-            *reinterpret_cast<const float4_t*>(vals + (blk + kF32Waves) * 256 + li * 16 + g * 4);
-        float b0[NTW][4], b1[NTW][4];
-        b_panel((int64_t)bci[blk], b0);
-        b_panel((int64_t)bci[blk + kF32Waves], b1);
-        multiply(a0, b0);
-        multiply(a1, b1);
+    for (; blk + (kF32Unroll - 1) * kF32Waves < re; blk += kF32Unroll * kF32Waves) {
+        float4_t a[kF32Unroll];
+        float bv[kF32Unroll][NTW][4];
+#pragma unroll
+        for (int u = 0; u < kF32Unroll; ++u) {
+            const int64_t b = blk + u * kF32Waves;
+            a[u] = *reinterpret_cast<const float4_t*>(vals + b * 256 + li * 16 + g * 4);
+            b_panel((int64_t)bci[b], bv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kF32Unroll; ++u) multiply(a[u], bv[u]);
     }
-    if (blk < re) {
+    for (; blk < re; blk += kF32Waves) {
         const float4_t a0 = *reinterpret_cast<const float4_t*>(vals + blk * 256 + li * 16 + g * 4);
         float b0[NTW][4];
         b_panel((int64_t)bci[blk], b0);
@@ -1373,7 +1379,11 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
         if (row_map) return false;  // the fp32 kernel stores rows in place
         const float* v = reinterpret_cast<const float*>(bvals);
         const float* b = reinterpret_cast<const float*>(B);
-        const int ntw = ntiles >= 4 ? 4 : (ntiles >= 2 ? 2 : 1);
+        // 16-column tiles per wave: 4 (fewer B loads per block) unless that
+        // leaves fewer than 512 workgroups, when narrower tiles spread the
+        // block-rows over more CUs
+        int ntw = ntiles >= 4 ? 4 : (ntiles >= 2 ? 2 : 1);
+        while (ntw > 1 && Mb * ((ntiles + ntw - 1) / ntw) < 512) ntw /= 2;
         const int64_t gy = (ntiles + ntw - 1) / ntw;
         if (gy > 65535) throw std::invalid_argument("xSpMM: N too large.");
         const dim3 fgrid((unsigned)Mb, (unsigned)gy);
