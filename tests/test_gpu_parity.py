@@ -147,8 +147,13 @@ def test_spmm_ragged_n_banded(torch, N):
         check_c(host(C), np.repeat(rs[:, None], N, axis=1), dtype)
 
 
+# The launcher picks 14- or 16-block-row tiles by how the grid fills the CUs.
+# On a 256-CU MI355X the small shapes (one round) take 14-row tiles; 16384 x 48
+# x 2048 (1024 block-rows, 8 column groups: 512 tiles of 16 = two full rounds)
+# takes 16-row tiles; 14300 x 40 x 2048 (894 block-rows: 448 tiles of 16 against
+# 512 of 14) takes 14-row tiles with a ragged last row group (12 of 14 rows).
 DENSE_SHAPES = [(16, 16, 8), (128, 64, 256), (130, 47, 72), (256, 512, 264), (300, 33, 520),
-                (48, 160, 16)]
+                (48, 160, 16), (16384, 48, 2048), (14300, 40, 2048)]
 
 
 @pytest.mark.parametrize("itype", [np.int32, np.int64])

@@ -14,12 +14,15 @@
 // (256 rows of C) and 256 columns; each wave owns 8 block-rows x 64 columns,
 // i.e. 8 x 4 MFMA tiles of 16 x 16 (128 fp32 accumulators per lane).  The
 // 256 x 256 tile keeps the cache traffic per MFMA low: every K step moves
-// 16 KB of A and 16 KB of B for 4.2 MFLOP.  K advances 32 at a time (two
-// block columns):
-//   * the 16 block-rows' two blocks (16 KB, contiguous per block-row) and the
-//     32 x 256 B panel (16 KB) go straight from memory into an LDS stage with
-//     direct-to-LDS buffer loads (no staging registers); the next step's
-//     loads are in flight while the current step multiplies;
+// 16 KB of A and 16 KB of B for 4.2 MFLOP.  Where that leaves the last round
+// of workgroups part-empty, 14-block-row tiles (7 per wave) may fill the CUs
+// better; the launcher picks the height.  K advances in slices of 32 (two
+// block columns), two slices per pipeline step:
+//   * each slice's 16 block-rows' two blocks (16 KB, contiguous per
+//     block-row) and its 32 x 256 B panel (16 KB) go straight from memory
+//     into an LDS stage with direct-to-LDS buffer loads (no staging
+//     registers); the next step's loads are issued between the current
+//     step's MFMAs;
 //   * a wave reads each of its block-rows' A operand with one ds_read_b128
 //     (the two blocks' rows in v_mfma_f32_16x16x32_f16 operand order, as
 //     loaded) and each of its four B operands with two ds_read_b64_tr_b16
@@ -29,6 +32,8 @@
 // grid: one workgroup per (row group, column group), ordered so that the
 // column groups of a row group run on the same XCD and meet its A tile in that
 // XCD's L2.
+#include <atomic>
+
 #include "internal.hpp"
 
 namespace xspmm {
@@ -42,9 +47,6 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-#ifndef XSPMM_DENSE_DR
-#define XSPMM_DENSE_DR 16
-#endif
 #ifndef XSPMM_DENSE_MINW
 #define XSPMM_DENSE_MINW 2
 #endif
@@ -54,26 +56,29 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 #ifndef XSPMM_DENSE_EPI
 #define XSPMM_DENSE_EPI 2
 #endif
-constexpr int kDR = XSPMM_DENSE_DR;          // block-rows per workgroup
-constexpr int kDN = 256;                     // columns per workgroup
-#ifndef XSPMM_DENSE_WAVES
-#define XSPMM_DENSE_WAVES 8
+#ifndef XSPMM_DENSE_KSUB
+#define XSPMM_DENSE_KSUB 2
 #endif
-constexpr int kDW = XSPMM_DENSE_WAVES;       // waves per workgroup (4 or 8)
+#ifndef XSPMM_DENSE_SPREAD
+#define XSPMM_DENSE_SPREAD 1
+#endif
+constexpr int kDN = 256;                     // columns per workgroup
+constexpr int kDW = 8;                       // waves per workgroup
 constexpr int kDThreads = 64 * kDW;
-// waves form a kWR x kWC grid; each owns 8 block-rows x kDTiles column tiles
-constexpr int kWR = kDR / 8;
+// waves form a kWR x kWC grid; each owns RW block-rows x kDTiles column tiles
+constexpr int kWR = 2;
 constexpr int kWC = kDW / kWR;
 constexpr int kDTiles = 16 / kWC;            // 16-column tiles per wave
-static_assert(kDR % 8 == 0 && kDW % kWR == 0 && 16 % kWC == 0, "wave grid");
-constexpr int kABytes = kDR * 1024;          // A stage: 8 block-rows x 2 blocks
+constexpr int kStageRows = 16;               // block-rows of an A stage (tile height <= 16)
+constexpr int kABytes = kStageRows * 1024;   // A stage: 16 block-rows x 2 blocks
 constexpr int kBRow = kDN * 2;               // B panel row: 512 bytes
 constexpr int kBBytes = 32 * kBRow;          // B stage: 32 rows
-constexpr int kStage = kABytes + kBBytes;    // 24 KB (three stages: 72 KB)
-constexpr int kAU = kDR / kDW;               // A block-rows loaded per wave
+constexpr int kStage = kABytes + kBBytes;    // 32 KB per 32-deep K slice
+constexpr int kAU = kStageRows / kDW;        // A block-rows loaded per wave
 constexpr int kBU = 16 / kDW;                // B panel row pairs loaded per wave
-constexpr int kLoadsPerStep = kAU + kBU;     // direct-to-LDS loads per wave per K step
-static_assert(kDR % kDW == 0 && kAU >= 1, "block-rows must split evenly over waves");
+constexpr int kKSub = XSPMM_DENSE_KSUB;      // 32-deep K slices per pipeline stage
+constexpr int kLoadsPerStep = kKSub * (kAU + kBU);  // direct-to-LDS loads per wave per stage
+static_assert(kStageRows % kDW == 0 && 16 % kWC == 0, "wave grid");
 constexpr int kRawWord3 = 0x00020000;        // raw dword buffer access (gfx9)
 constexpr int kXcds = 8;                     // accelerator dies of an MI355X
 
@@ -116,10 +121,11 @@ __device__ __forceinline__ uint32_t panel_swz(uint32_t e)
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
 }
 
-// RM: index type of the optional output row map (C row row_map[r] receives
-// product row r -- the clustered pipeline's un-permutation fused into the
-// store; null stores rows in place).
-template <typename RM>
+// RW: block-rows per wave (8: 256-row tiles; 7: 224-row tiles, whose A stage
+// rows 14 and 15 load as zeros).  RM: index type of the optional output row
+// map (C row row_map[r] receives product row r -- the clustered pipeline's
+// un-permutation fused into the store; null stores rows in place).
+template <int RW, typename RM>
 __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const uint16_t* __restrict__ vals,
                                                                  const uint16_t* __restrict__ B,
                                                                  float* __restrict__ C,
@@ -129,12 +135,15 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
                                                                  const RM* __restrict__ row_map)
 {
     constexpr int NS = XSPMM_DENSE_STAGES;
+    constexpr int kDR = kWR * RW;  // block-rows per workgroup
+    static_assert(RW >= 1 && kDR <= kStageRows, "tile height");
     static_assert(NS == 2 || NS == 3, "2 or 3 LDS stages");
-    __shared__ __align__(16) unsigned char smem[NS * kStage];
+    static_assert(NS * kKSub * kStage <= 160 * 1024, "LDS of one CU");
+    __shared__ __align__(16) unsigned char smem[NS * kKSub * kStage];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int wr = wave / kWC;  // this wave's block-rows: 8 wr .. 8 wr + 7
+    const int wr = wave / kWC;  // this wave's block-rows: RW wr .. RW wr + RW - 1
     const int wc = wave % kWC;  // and column tiles kDTiles wc .. + kDTiles - 1
     const int li = lane & 15;
     const int g = lane >> 4;
@@ -173,7 +182,7 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
 #pragma unroll
     for (int u = 0; u < kAU; ++u) {
         const int64_t br = br0 + kAU * wave + u;
-        a_row_ok[u] = br < Mb;
+        a_row_ok[u] = kAU * wave + u < kDR && br < Mb;
         a_off[u] = (uint32_t)((a_row_ok[u] ? br : 0) * Kb * 512) + 16u * (uint32_t)lane;
     }
     const bool a_second = lane >= 32;
@@ -187,22 +196,26 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
         b_row[u] = row;
         b_col_off[u] = col < N ? (uint32_t)(2 * col) : 0xffffffffu;
     }
-    const int64_t steps = (Kb + 1) / 2;
-    auto issue_step = [&](int64_t s) {
-        const uint32_t base = lds0 + (uint32_t)((s % NS) * kStage);
-#pragma unroll
-        for (int u = 0; u < kAU; ++u) {
-            const bool ok = a_row_ok[u] && (!a_second || 2 * s + 1 < Kb);
-            const uint32_t off = ok ? a_off[u] + (uint32_t)(s * 1024) : a_bytes;
+    // a stage holds kKSub slices of 32 K rows (two block columns) each, slice
+    // q of stage s being K slice ks = kKSub s + q
+    const int64_t steps = (Kb + 2 * kKSub - 1) / (2 * kKSub);
+    // load i (0 .. kLoadsPerStep - 1) of step s: slice i / (kAU + kBU), then
+    // the wave's kAU A block-rows and kBU B row pairs of that slice
+    auto issue_load = [&](int64_t s, int i) {
+        const int q = i / (kAU + kBU), u = i % (kAU + kBU);
+        const int64_t ks = kKSub * s + q;
+        const uint32_t base = lds0 + (uint32_t)(((s % NS) * kKSub + q) * kStage);
+        if (u < kAU) {
+            const bool ok = a_row_ok[u] && 2 * ks + (a_second ? 1 : 0) < Kb;
+            const uint32_t off = ok ? a_off[u] + (uint32_t)(ks * 1024) : a_bytes;
             load_to_lds(base + (uint32_t)((kAU * wave + u) * 1024), off, a_rsrc);
-        }
-#pragma unroll
-        for (int u = 0; u < kBU; ++u) {
-            const int64_t k = 32 * s + b_row[u];
-            const uint32_t off = (k < K && b_col_off[u] != 0xffffffffu)
-                                     ? (uint32_t)(k * N * 2) + b_col_off[u]
+        } else {
+            const int v = u - kAU;
+            const int64_t k = 32 * ks + b_row[v];
+            const uint32_t off = (k < K && b_col_off[v] != 0xffffffffu)
+                                     ? (uint32_t)(k * N * 2) + b_col_off[v]
                                      : b_bytes;
-            load_to_lds(base + (uint32_t)(kABytes + (2 * kBU * wave + 2 * u) * kBRow), off, b_rsrc);
+            load_to_lds(base + (uint32_t)(kABytes + (2 * kBU * wave + 2 * v) * kBRow), off, b_rsrc);
         }
     };
 
@@ -215,43 +228,62 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
     // A operand of a pair: block lane >> 5, row li, halves 8 * ((lane >> 4) & 1) .. +8
     const uint32_t a_lane = (uint32_t)((lane >> 5) * 512 + li * 32 + ((lane >> 4) & 1) * 16);
 
-    float4_t acc[8][kDTiles];
+    float4_t acc[RW][kDTiles];
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int j = 0; j < kDTiles; ++j) acc[r][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int stage) {
-        const unsigned char* S = smem + stage * kStage;
-        half8_t bop[kDTiles];
+    // One stage's MFMAs.  The loads of step `next` (none if next < 0) are
+    // spread over its kKSub * RW row groups rather than issued back to back:
+    // eight waves issuing all their loads at once queue behind one another at
+    // the CU's texture unit and hold up their MFMAs.
+    constexpr int kGroups = kKSub * RW;
+    auto compute_step = [&](int stage, int64_t next) {
 #pragma unroll
-        for (int j = 0; j < kDTiles; ++j) {
-            const uint32_t c = (uint32_t)(2 * (kDTiles * wc + j)) + tr_cc;
-            const uint32_t a = tr_base + ((c ^ tr_swz) << 4);
-            unsigned char* P = const_cast<unsigned char*>(S) + a;
-            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)P);
-            const short4_t hi =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(P + 4 * kBRow));
-            bop[j] = __builtin_bit_cast(half8_t,
-                                        __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
+        for (int q = 0; q < kKSub; ++q) {
+            const unsigned char* S = smem + (stage * kKSub + q) * kStage;
+            half8_t bop[kDTiles];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const half8_t aop = __builtin_bit_cast(
-                half8_t, *reinterpret_cast<const u32x4_t*>(S + (8 * wr + r) * 1024 + a_lane));
+            for (int j = 0; j < kDTiles; ++j) {
+                const uint32_t c = (uint32_t)(2 * (kDTiles * wc + j)) + tr_cc;
+                const uint32_t a = tr_base + ((c ^ tr_swz) << 4);
+                unsigned char* P = const_cast<unsigned char*>(S) + a;
+                const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)P);
+                const short4_t hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(P + 4 * kBRow));
+                bop[j] = __builtin_bit_cast(half8_t,
+                                            __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
 #pragma unroll
-            for (int j = 0; j < kDTiles; ++j)
-                acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[r][j], 0, 0, 0);
+            for (int r = 0; r < RW; ++r) {
+                const half8_t aop = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const u32x4_t*>(S + (RW * wr + r) * 1024 + a_lane));
+#pragma unroll
+                for (int j = 0; j < kDTiles; ++j)
+                    acc[r][j] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[j], acc[r][j], 0, 0, 0);
+                if (XSPMM_DENSE_SPREAD && next >= 0) {
+#pragma unroll
+                    for (int i = 0; i < kLoadsPerStep; ++i)
+                        if (i * kGroups / kLoadsPerStep == q * RW + r) issue_load(next, i);
+                }
+            }
         }
     };
 
-    // LDS ring of NS stages (two by default: with two workgroups per CU that
-    // measured faster than three).  Every wave issues exactly kLoadsPerStep
-    // loads per step and no other vector-memory loads, so "at most
-    // kLoadsPerStep outstanding" (three stages) or "none outstanding" (two)
-    // means this wave's loads of step s have landed; the barrier then makes
-    // every wave's visible and guarantees that the stage step s + NS - 1 is
-    // loaded into, last read at step s - 1, is free.
+    // LDS ring of NS stages of kKSub slices each (two stages of two slices by
+    // default; measured: three stages of one slice, or one slice per stage
+    // with the loads spread, are slower).  Every wave issues exactly
+    // kLoadsPerStep loads per step and no other vector-memory loads, so "at
+    // most kLoadsPerStep outstanding" (three stages) or "none outstanding"
+    // (two) means this wave's loads of step s have landed; the barrier then
+    // makes every wave's visible and guarantees that the stage step s + NS - 1
+    // is loaded into, last read at step s - 1, is free.
+    auto issue_step = [&](int64_t s) {
+#pragma unroll
+        for (int i = 0; i < kLoadsPerStep; ++i) issue_load(s, i);
+    };
     if (steps > 0) issue_step(0);
     if (NS == 3 && steps > 1) issue_step(1);
     for (int64_t s = 0; s < steps; ++s) {
@@ -260,13 +292,14 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (s + NS - 1 < steps) issue_step(s + NS - 1);
-        compute((int)(s % NS));
+        const int64_t next = s + NS - 1 < steps ? s + NS - 1 : -1;
+        if (!XSPMM_DENSE_SPREAD && next >= 0) issue_step(next);
+        compute_step((int)(s % NS), next);
     }
 
     // --- store: lane holds C[16 br + 4g + q][16 tile + li] ------------------
     if constexpr (XSPMM_DENSE_EPI == 2) {
-        // Through LDS, eight rounds: in round r every wave writes its r-th
+        // Through LDS, RW rounds: in round r every wave writes its r-th
         // block-row (16 x kDTiles*16 fp32, MFMA order) and the workgroup reads
         // the kWR * 16 rows back row-major, so every lane stores 16 contiguous
         // bytes (1 KB rows per workgroup).
@@ -278,14 +311,14 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
         const int row_l = t / TPR;
         const int col_l = (t % TPR) * 4;           // +4 * TPR per pass
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
+        for (int r = 0; r < RW; ++r) {
 #pragma unroll
             for (int j = 0; j < kDTiles; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     T[(16 * wr + 4 * g + q) * TS + 16 * kDTiles * wc + 16 * j + li] = acc[r][j][q];
             __syncthreads();
-            const int64_t row = 16 * (br0 + 8 * (row_l / 16) + r) + (row_l % 16);
+            const int64_t row = 16 * (br0 + RW * (row_l / 16) + r) + (row_l % 16);
             const int64_t crow = (row_map && row < M) ? (int64_t)row_map[row] : row;
 #pragma unroll
             for (int p = 0; p < kDN / (4 * TPR); ++p) {
@@ -303,8 +336,8 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
         }
     } else {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int64_t row0 = 16 * (br0 + 8 * wr + r) + 4 * g;
+        for (int r = 0; r < RW; ++r) {
+            const int64_t row0 = 16 * (br0 + RW * wr + r) + 4 * g;
 #pragma unroll
             for (int j = 0; j < kDTiles; ++j) {
                 const int64_t col = n0 + 16 * kDTiles * wc + 16 * j + li;
@@ -326,13 +359,46 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
 }  // namespace
 
 namespace {
-// workgroups of the dense grid: row groups padded to a multiple of the XCD
-// count (padding groups exit) times column groups
-int64_t dense_groups(int64_t Mb, int64_t N)
+// workgroups of the dense grid for tiles of dr block-rows: row groups padded
+// to a multiple of the XCD count (padding groups exit) times column groups
+int64_t dense_groups(int64_t Mb, int64_t N, int64_t dr)
 {
     const int64_t ncg = (N + kDN - 1) / kDN;
-    const int64_t nrg = (Mb + kDR - 1) / kDR;
+    const int64_t nrg = (Mb + dr - 1) / dr;
     return ((nrg + kXcds - 1) / kXcds) * kXcds * ncg;
+}
+
+// compute units of the current device (one workgroup of this kernel fits a
+// CU), queried once per device
+int64_t device_cus()
+{
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cus[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Tile height (block-rows per workgroup): 16 or 14.  A workgroup's time is
+// about proportional to its height and every CU holds one workgroup, so the
+// grid takes rounds(h) = ceil(tiles(h) / CUs) workgroup times of height h;
+// the height with the smaller rounds(h) * h wins (16 on ties: its loads per
+// MFMA are lower).  E.g. 896 block-rows x 8 column groups on 256 CUs: 448
+// tiles of 16 (two rounds, a quarter of the second idle) against 512 of 14
+// (two full rounds).
+int dense_tile_rows(int64_t Mb, int64_t N)
+{
+    const int64_t ncg = (N + kDN - 1) / kDN;
+    const int64_t cus = device_cus();
+    auto cost = [&](int64_t h) { return ((((Mb + h - 1) / h) * ncg + cus - 1) / cus) * h; };
+    return cost(14) < cost(16) ? 14 : 16;
 }
 }  // namespace
 
@@ -342,7 +408,7 @@ bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t
     if (nnzb != Mb * Kb || Mb <= 0 || Kb <= 0 || N <= 0) return false;
     if (N % 8 != 0) return false;
     if (Mb * Kb * 512 >= (int64_t(1) << 31) || K * N * 2 >= (int64_t(1) << 31)) return false;
-    return dense_groups(Mb, N) <= 0x7fffffffLL;
+    return dense_groups(Mb, N, 14) <= 0x7fffffffLL;
 }
 
 template <typename RM>
@@ -351,9 +417,14 @@ bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t n
                          hipStream_t s, const RM* row_map)
 {
     if (!spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N)) return false;
-    const int64_t groups = dense_groups(Mb, N);
-    hipLaunchKernelGGL(spmm_f16_dense_kernel<RM>, dim3((unsigned)groups), dim3(kDThreads), 0, s,
-                       bvals, B, C, M, K, N, Mb, Kb, row_map);
+    const int h = dense_tile_rows(Mb, N);
+    const int64_t groups = dense_groups(Mb, N, h);
+    if (h == 14)
+        hipLaunchKernelGGL((spmm_f16_dense_kernel<7, RM>), dim3((unsigned)groups), dim3(kDThreads), 0,
+                           s, bvals, B, C, M, K, N, Mb, Kb, row_map);
+    else
+        hipLaunchKernelGGL((spmm_f16_dense_kernel<8, RM>), dim3((unsigned)groups), dim3(kDThreads), 0,
+                           s, bvals, B, C, M, K, N, Mb, Kb, row_map);
     XSPMM_LAUNCH_CHECK();
     return true;
 }
