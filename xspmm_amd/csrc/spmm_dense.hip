@@ -62,6 +62,9 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 #ifndef XSPMM_DENSE_SPREAD
 #define XSPMM_DENSE_SPREAD 1
 #endif
+#ifndef XSPMM_DENSE_TILE_ROWS
+#define XSPMM_DENSE_TILE_ROWS 0  // 14 or 16 fixes the tile height; 0 lets the launcher choose
+#endif
 constexpr int kDN = 256;                     // columns per workgroup
 constexpr int kDW = 8;                       // waves per workgroup
 constexpr int kDThreads = 64 * kDW;
@@ -398,6 +401,7 @@ int dense_tile_rows(int64_t Mb, int64_t N)
     const int64_t ncg = (N + kDN - 1) / kDN;
     const int64_t cus = device_cus();
     auto cost = [&](int64_t h) { return ((((Mb + h - 1) / h) * ncg + cus - 1) / cus) * h; };
+    if (XSPMM_DENSE_TILE_ROWS == 14 || XSPMM_DENSE_TILE_ROWS == 16) return XSPMM_DENSE_TILE_ROWS;
     return cost(14) < cost(16) ? 14 : 16;
 }
 }  // namespace
