@@ -478,7 +478,7 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
 // The four waves of a workgroup take the row's block pairs in turn (wave w:
 // pairs w, w + 4, ...) and each wave
 //   1. streams its pairs in MFMA operand layout (16 bytes per lane, lane
-//      (r, g): row r, pair columns 8g .. 8g+7; non-temporal loads, kBatchDepth
+//      (r, g): row r, pair columns 8g .. 8g+7; non-temporal loads, batch_depth
 //      pairs in flight) and, one vector load per ring pass, the pairs' block
 //      columns;
 //   2. forms the pair's 32-bit mask of columns holding a non-zero (per-lane
@@ -526,11 +526,23 @@ static_assert(kBatchWaveLds % 16 == 0 && kApOff % 16 == 0 && kSlotOff % 16 == 0,
 #ifndef XSPMM_BATCH_DEPTH
 #define XSPMM_BATCH_DEPTH 5
 #endif
+#ifndef XSPMM_BATCH_DEPTH_NARROW
+#define XSPMM_BATCH_DEPTH_NARROW 8
+#endif
 #ifndef XSPMM_BATCH_MIN_WAVES
 #define XSPMM_BATCH_MIN_WAVES 1
 #endif
-constexpr int kBatchDepth = XSPMM_BATCH_DEPTH;  // A pairs in flight per wave (4..6)
-static_assert(kBatchDepth >= 4 && kBatchDepth <= 6, "batch depth must be 4, 5 or 6");
+// A pairs in flight per wave.  At 128 columns (NT = 8) five fill the 128-VGPR
+// budget of four waves per SIMD; narrower tiles need fewer accumulator and B
+// registers and keep more pairs in flight.
+template <int NT>
+constexpr int batch_depth()
+{
+    return NT >= 8 ? XSPMM_BATCH_DEPTH : XSPMM_BATCH_DEPTH_NARROW;
+}
+static_assert(XSPMM_BATCH_DEPTH >= 4 && XSPMM_BATCH_DEPTH <= 10 && XSPMM_BATCH_DEPTH_NARROW >= 4 &&
+                  XSPMM_BATCH_DEPTH_NARROW <= 10,
+              "batch depth must be 4 .. 10");
 
 // swizzle of row e: even values 0..14, each used by two of the 16 rows a
 // transpose read touches
@@ -621,7 +633,8 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
     int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map, BatchPack pk)
 {
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
-    static_assert(4 * kBatchDepth <= kWave, "one index window per ring pass");
+    constexpr int D = batch_depth<NT>();
+    static_assert(4 * D <= kWave, "one index window per ring pass");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
     constexpr int RPL = 64 / CPR;  // B rows per load instruction
     constexpr uint32_t kSel = kApOff;  // S^T: 16 rows x kApStride bytes
@@ -859,9 +872,9 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
     };
 
     if (wave < npairs) {
-        half8_t P0, P1, P2, P3, P4, P5;
+        half8_t P0, P1, P2, P3, P4, P5, P6, P7, P8, P9;
         constexpr int S = 4;
-        constexpr int A = S * kBatchDepth;
+        constexpr int A = S * D;
         const int64_t q0 = wave;
         // the window before the A loads, as in every later pass, so the
         // loads complete in the same order on the first pass
@@ -870,8 +883,12 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
         stage_a(q0 + S, P1);
         stage_a(q0 + 2 * S, P2);
         stage_a(q0 + 3 * S, P3);
-        if constexpr (kBatchDepth > 4) stage_a(q0 + 4 * S, P4);
-        if constexpr (kBatchDepth > 5) stage_a(q0 + 5 * S, P5);
+        if constexpr (D > 4) stage_a(q0 + 4 * S, P4);
+        if constexpr (D > 5) stage_a(q0 + 5 * S, P5);
+        if constexpr (D > 6) stage_a(q0 + 6 * S, P6);
+        if constexpr (D > 7) stage_a(q0 + 7 * S, P7);
+        if constexpr (D > 8) stage_a(q0 + 8 * S, P8);
+        if constexpr (D > 9) stage_a(q0 + 9 * S, P9);
         for (int64_t q = q0; q < npairs; q += A) {
             // next pass's window, issued a pass ahead like the A loads
             const uint32_t nwin = load_cols(q + A);
@@ -883,13 +900,29 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
             stage_a(q + A + 2 * S, P2);
             process(P3, win, 3);
             stage_a(q + A + 3 * S, P3);
-            if constexpr (kBatchDepth > 4) {
+            if constexpr (D > 4) {
                 process(P4, win, 4);
                 stage_a(q + A + 4 * S, P4);
             }
-            if constexpr (kBatchDepth > 5) {
+            if constexpr (D > 5) {
                 process(P5, win, 5);
                 stage_a(q + A + 5 * S, P5);
+            }
+            if constexpr (D > 6) {
+                process(P6, win, 6);
+                stage_a(q + A + 6 * S, P6);
+            }
+            if constexpr (D > 7) {
+                process(P7, win, 7);
+                stage_a(q + A + 7 * S, P7);
+            }
+            if constexpr (D > 8) {
+                process(P8, win, 8);
+                stage_a(q + A + 8 * S, P8);
+            }
+            if constexpr (D > 9) {
+                process(P9, win, 9);
+                stage_a(q + A + 9 * S, P9);
             }
             win = nwin;
         }
