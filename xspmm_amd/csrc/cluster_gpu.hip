@@ -63,6 +63,37 @@ __device__ __forceinline__ float jaccard_distance(int inter, int uni)
     return 1.0f - __fdiv_rn((float)inter, (float)uni);
 }
 
+// The reference's test d(inter, uni) <= thr, decided without the division
+// away from the threshold.  With x = inter / uni (exact), the float value
+// d = RN(1 - RN(x)) is within 2^-23 of 1 - x.  So d <= thr whenever
+// x >= 1 - thr + 2^-23, and d > thr whenever x < 1 - thr - 2^-23.  The
+// factors a_hi / a_lo add 2^-20 of margin on either side, which covers the
+// rounding of the products a * uni (uni < 2^24, so int -> float is exact).
+// Inside that band the division decides, exactly as the reference.
+struct JaccardTest {
+    float thr, a_hi, a_lo;
+    __device__ explicit JaccardTest(float t) : thr(t)
+    {
+        const float a = 1.0f - t;
+        a_hi = a + 0x1p-20f;
+        a_lo = a - 0x1p-20f;
+    }
+    __device__ __forceinline__ bool close(int inter, int uni) const
+    {
+        if (uni == 0) return 0.0f <= thr;
+        const float fi = (float)inter, fu = (float)uni;
+        if (fi >= a_hi * fu) return true;
+        if (fi < a_lo * fu) return false;
+        return jaccard_distance(inter, uni) <= thr;
+    }
+    // false when no pair of rows with popcounts mn <= mx can be close:
+    // |p & q| <= mn and |p | q| >= mx, so x <= mn / mx
+    __device__ __forceinline__ bool may_close(int mn, int mx) const
+    {
+        return !((float)mn < a_lo * (float)mx);
+    }
+};
+
 // Phase boundary of the clustering workgroup: every wave waits until its
 // global stores and atomics are acknowledged, then the barrier.  All waves
 // share one CU, so plain loads after the barrier see plain stores from
@@ -280,6 +311,7 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
     const int per = (tiles + (int)gridDim.y - 1) / (int)gridDim.y;
     const int jbeg = (int)blockIdx.y * per * kPairTile;
     const int jend = min(M, jbeg + per * kPairTile);
+    const JaccardTest jt(thr);
     for (int j0 = jbeg; j0 < jend; j0 += kPairTile) {
         __syncthreads();
         for (int x = t; x < kPairTile * MAXW; x += 256) {
@@ -295,15 +327,12 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
             if (j >= jend || j == i) continue;
             const int qj = tcount[jj];
             const int mn = qj < qc ? qj : qc, mx = qj < qc ? qc : qj;
-            if (jaccard_distance(mn, mx) > thr) continue;
-            int inter = 0, uni = 0;
+            if (!jt.may_close(mn, mx)) continue;
+            // |q_i | q_j| = |q_i| + |q_j| - |q_i & q_j| (counts are the popcounts)
+            int inter = 0;
 #pragma unroll
-            for (int w = 0; w < MAXW; ++w) {
-                const uint64_t y = tile[jj * MAXW + w];
-                inter += __popcll(q[w] & y);
-                uni += __popcll(q[w] | y);
-            }
-            if (jaccard_distance(inter, uni) <= thr) {
+            for (int w = 0; w < MAXW; ++w) inter += __popcll(q[w] & tile[jj * MAXW + w]);
+            if (jt.close(inter, qc + qj - inter)) {
                 const int k = atomicAdd(&pn[i], 1);
                 if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
             }
@@ -330,6 +359,7 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
     __shared__ int64_t red64[kClWaves];
     __shared__ int s_n, s_over, s_np;
     const int t = threadIdx.x;
+    const JaccardTest jt(thr);
     for (int i = blockIdx.x; i < M; i += gridDim.x) {
         const int qi = count[i];
         if (qi == 0) {
@@ -371,7 +401,7 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
                 if (j == i || s_over) continue;
                 const int qj = count[j];
                 const int mn = qj < qi ? qj : qi, mx = qj < qi ? qi : qj;
-                if (jaccard_distance(mn, mx) > thr) continue;
+                if (!jt.may_close(mn, mx)) continue;
                 uint32_t h = ((uint32_t)j * 2654435761u) & (kHashSlots - 1);
                 for (int probe = 0; probe < kHashSlots; ++probe) {
                     const int32_t old = atomicCAS(&hkey[h], -1, j);
@@ -390,7 +420,7 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
                 const int32_t j = hkey[h];
                 if (j < 0) continue;
                 const int inter = hval[h];
-                if (jaccard_distance(inter, qi + count[j] - inter) <= thr) {
+                if (jt.close(inter, qi + count[j] - inter)) {
                     const int k = atomicAdd(&s_np, 1);
                     if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
                 }
@@ -441,6 +471,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     const int M = (int)a.M;
     const int W = (int)a.W;  // 64-bit words per row bitmap
     const float thr = a.thresh;
+    const JaccardTest jt(thr);
     uint64_t* p64 = reinterpret_cast<uint64_t*>(p32);
 
     for (int i = t; i < M; i += kClThreads) {
@@ -542,7 +573,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
                     const int c = a.un[at];
                     const int qc = a.count[c];
                     const int mn = qc < pc ? qc : pc, mx = qc < pc ? pc : qc;
-                    if (jaccard_distance(mn, mx) <= thr) {  // |p&q| <= mn, |p|q| >= mx
+                    if (jt.may_close(mn, mx)) {  // |p&q| <= mn, |p|q| >= mx
                         const uint64_t* q = a.bits + (int64_t)c * W;
                         int inter = 0, uni = 0;
                         for (int w = 0; w < W; ++w) {
@@ -550,7 +581,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
                             inter += __popcll(x & y);
                             uni += __popcll(x | y);
                         }
-                        if (jaccard_distance(inter, uni) <= thr) key = at;
+                        if (jt.close(inter, uni)) key = at;
                     }
                 }
                 const int best = block_max(key, red);
@@ -700,7 +731,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
                 nxt[atomicAdd(&s_cnt[1], 1)] = r;
                 const int inter = __hip_atomic_load(&a.cnt[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const int uni = pc + a.count[r] - inter;
-                if (jaccard_distance(inter, uni) <= thr && pr > key) key = pr;
+                if (pr > key && jt.close(inter, uni)) key = pr;
             }
             const int best = block_max(key, red);
             int32_t* sw = cur;
