@@ -183,6 +183,46 @@ def test_spmm_full_block_grid(torch, shape, itype):
     check_c(host(C), D.astype(np.float64) @ B.astype(np.float64), np.float16)
 
 
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_spmm_b_beyond_32_bit_offsets(torch, dtype):
+    # B of more than 2^31 bytes (K * N * sizeof(T) > 2^31): the fp16
+    # column-batch kernel's 32-bit byte offsets do not apply, and the launcher
+    # must take a 64-bit path (fp16 panel kernel, fp32 kernel).  Rows touch
+    # the first and the last column of K, so the largest offsets are read.
+    K = 65536
+    N = 16392 if dtype == np.float16 else 8200
+    assert K * N * np.dtype(dtype).itemsize > 2 ** 31
+    M = 40
+    rng = np.random.default_rng(31)
+    rows = []
+    for r in range(M):
+        c = rng.choice(K, size=6, replace=False)
+        c = np.concatenate([c, [0, K - 1] if r % 3 == 0 else [K - 1 - r]])
+        rows.append(np.unique(c))
+    rp = np.zeros(M + 1, np.int64)
+    rp[1:] = np.cumsum([len(c) for c in rows])
+    ci = np.concatenate(rows).astype(np.int32)
+    vals = rng.uniform(-1, 1, len(ci)).astype(dtype)
+    note(f"B beyond 2^31 bytes: K={K} N={N} {dtype.__name__}")
+    A = X.CSRMatrix.from_host(M, K, rp.astype(np.int32), ci, vals)
+    Bm = X.csr_to_bcsr(A)
+    tdt = torch.float16 if dtype == np.float16 else torch.float32
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    Bd = torch.randn(K, N, generator=gen, dtype=torch.float32, device="cuda").to(tdt)
+    C = X.spmm(Bm, Bd, N=N)
+    # the prepared product (clustered: the un-permuted store through a workspace)
+    plan = X.SpMMPlan(A)
+    Cp = plan.execute(Bd)
+    torch.cuda.synchronize()
+    plan.close()
+    used, ci_sub = np.unique(ci, return_inverse=True)
+    Bsub = host(Bd[torch.as_tensor(used).long().cuda()]).astype(np.float64)
+    del Bd
+    ref = oracle.csr_spmm_f64(M, N, rp, ci_sub.astype(np.int64), vals, Bsub)
+    check_c(host(C), ref, dtype)
+    check_c(host(Cp), ref, dtype)
+
+
 @pytest.mark.parametrize("N", [64, 128])
 def test_spmm_many_skewed_block_rows(torch, N):
     # Mb = 3000 > 2048 block-rows with power-law lengths: the launcher orders
