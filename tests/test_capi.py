@@ -146,3 +146,17 @@ def test_product_clustering_templates_like_input():
         finally:
             del os.environ["XSPMM_CLUSTER_ENGINE"]
         np.testing.assert_array_equal(widen(got), want)
+
+
+@pytest.mark.parametrize("simd", ["scalar", "auto"])
+def test_product_clustering_scan_search_forms(simd, monkeypatch):
+    # the scan engine's search has a scalar and an AVX-512 (vpopcntq) form,
+    # picked by the host CPU; both give the reference's permutation (8-word
+    # vector steps and a scalar tail)
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", "scan")
+    monkeypatch.setenv("XSPMM_CLUSTER_SIMD", simd)
+    for M, seed in ((1024, 1), (8192, 2), (9216, 3)):  # bitmaps of 1, 8 and 9 words
+        p = synth.templates(M=M, n_templates=M // 16, seed=seed)
+        want = oracle.jaccard(p.M, p.K, p.rp, p.ci)
+        got = X.compute_1d_jaccard_clustering(p.M, p.K, p.rp, p.ci, nthreads=3)
+        np.testing.assert_array_equal(widen(got), want)

@@ -33,6 +33,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <immintrin.h>
 #include <queue>
 #include <stdexcept>
 #include <string>
@@ -50,6 +51,86 @@ inline float jaccard_distance(int64_t inter, int64_t uni)
 {
     if (uni == 0) return 0.0f;
     return 1.0f - (static_cast<float>(inter) / static_cast<float>(uni));
+}
+
+// The test jaccard_distance(inter, uni) <= t, decided without the division
+// away from the threshold.  With x = inter / uni (exact), the float value
+// RN(1 - RN(x)) is within 2^-23 of 1 - x, so it is <= t whenever
+// x >= 1 - t + 2^-23 and > t whenever x < 1 - t - 2^-23; the factors a_hi /
+// a_lo add 2^-20 on either side, which also covers the rounding of a * uni.
+// That needs inter and uni exact in float (below 2^24); larger counts, and
+// the band between the factors, take the division as the reference does.
+struct JaccardTest {
+    float t, a_hi, a_lo;
+    explicit JaccardTest(float thr) : t(thr), a_hi((1.0f - thr) + 0x1p-20f), a_lo((1.0f - thr) - 0x1p-20f) {}
+    bool close(int64_t inter, int64_t uni) const
+    {
+        if (uni == 0) return 0.0f <= t;
+        if (uni < (int64_t(1) << 24)) {
+            const float fi = static_cast<float>(inter), fu = static_cast<float>(uni);
+            if (fi >= a_hi * fu) return true;
+            if (fi < a_lo * fu) return false;
+        }
+        return jaccard_distance(inter, uni) <= t;
+    }
+    // false when no rows with popcounts mn <= mx can be close (x <= mn / mx)
+    bool may_close(int64_t mn, int64_t mx) const
+    {
+        if (mx >= (int64_t(1) << 24)) return jaccard_distance(mn, mx) <= t;
+        return !(static_cast<float>(mn) < a_lo * static_cast<float>(mx));
+    }
+};
+
+// One thread's share of the scan engine's search: the highest position in
+// [bot, top] whose row is close to the pattern p (popcount pc), or -1.
+// |p | q| = |p| + |q| - |p & q|, so only the intersection is counted.  The
+// AVX-512 instance (vpopcntq, 8 words per instruction) runs when the host CPU
+// has the VPOPCNTDQ extension; both instances return the same position.
+struct ScanArgs {
+    const uint64_t* bits;   // row bitmaps, W words each
+    const int32_t* count;   // their popcounts
+    const int64_t* un;      // position -> row
+    const uint64_t* p;      // pattern
+    int64_t W, pc;
+};
+
+inline int64_t and_popcount(const uint64_t* a, const uint64_t* b, int64_t n)
+{
+    int64_t s = 0;
+    for (int64_t w = 0; w < n; ++w) s += __builtin_popcountll(a[w] & b[w]);
+    return s;
+}
+
+__attribute__((target("avx512f,avx512vpopcntdq"))) inline int64_t and_popcount_avx512(
+    const uint64_t* a, const uint64_t* b, int64_t n)
+{
+    __m512i acc = _mm512_setzero_si512();
+    int64_t w = 0;
+    for (; w + 8 <= n; w += 8)
+        acc = _mm512_add_epi64(acc, _mm512_popcnt_epi64(_mm512_and_si512(
+                                        _mm512_loadu_si512(a + w), _mm512_loadu_si512(b + w))));
+    int64_t s = _mm512_reduce_add_epi64(acc);
+    for (; w < n; ++w) s += __builtin_popcountll(a[w] & b[w]);
+    return s;
+}
+
+template <bool AVX512, typename JT>
+inline int64_t scan_down(const ScanArgs& a, const JT& jt, int64_t top, int64_t bot)
+{
+    for (int64_t pos = top; pos >= bot; --pos) {
+        const int64_t cand = a.un[pos];
+        const int64_t qc = a.count[cand];
+        const int64_t mn = qc < a.pc ? qc : a.pc, mx = qc < a.pc ? a.pc : qc;
+        if (!jt.may_close(mn, mx)) continue;  // cannot reach t
+        const uint64_t* q = a.bits + cand * a.W;
+        int64_t inter;
+        if constexpr (AVX512)
+            inter = and_popcount_avx512(a.p, q, a.W);
+        else
+            inter = and_popcount(a.p, q, a.W);
+        if (jt.close(inter, a.pc + qc - inter)) return pos;
+    }
+    return -1;
 }
 
 struct Patterns {
@@ -132,10 +213,37 @@ private:
     const std::function<void(int)>* task_ = nullptr;
 };
 
+template <typename JT>
+int64_t scan_down_scalar(const ScanArgs& a, const JT& jt, int64_t top, int64_t bot)
+{
+    return scan_down<false>(a, jt, top, bot);
+}
+
+template <typename JT>
+__attribute__((target("avx512f,avx512vpopcntdq"))) int64_t scan_down_avx512(const ScanArgs& a,
+                                                                            const JT& jt,
+                                                                            int64_t top,
+                                                                            int64_t bot)
+{
+    return scan_down<true>(a, jt, top, bot);
+}
+
+// XSPMM_CLUSTER_SIMD=scalar forces the scalar search (for tests and CPUs
+// where the extension is reported but unwanted).
+bool host_has_vpopcntdq()
+{
+    if (const char* e = std::getenv("XSPMM_CLUSTER_SIMD"))
+        if (std::strcmp(e, "scalar") == 0) return false;
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512vpopcntdq");
+}
+
 template <typename I>
 void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
 {
     const int64_t M = P.M, W = P.words;
+    const JaccardTest jt(t);
+    const bool avx512 = host_has_vpopcntdq();
     std::vector<int64_t> un((size_t)M);
     for (int64_t i = 0; i < M; ++i) un[(size_t)i] = i;
     int64_t n_un = M, out = 0;
@@ -154,33 +262,20 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
         while (hi >= 0) {
             // First joining position in [lo, hi], scanning downwards.
             const int64_t lo = hi - stretch + 1 > 0 ? hi - stretch + 1 : 0;
-            auto test = [&](int64_t pos) {
-                const int64_t cand = un[(size_t)pos];
-                const int64_t qc = P.count[(size_t)cand];
-                const int64_t mn = qc < pc ? qc : pc, mx = qc < pc ? pc : qc;
-                if (jaccard_distance(mn, mx) > t) return false;  // cannot reach t
-                const uint64_t* q = P.row(cand);
-                int64_t inter = 0, uni = 0;
-                for (int64_t w = 0; w < W; ++w) {
-                    inter += __builtin_popcountll(p[(size_t)w] & q[w]);
-                    uni += __builtin_popcountll(p[(size_t)w] | q[w]);
-                }
-                return jaccard_distance(inter, uni) <= t;
+            const ScanArgs sa{P.bits.data(), P.count.data(), un.data(), p.data(), W, pc};
+            auto scan = [&](int64_t top, int64_t bot) {
+                return avx512 ? scan_down_avx512(sa, jt, top, bot) : scan_down_scalar(sa, jt, top, bot);
             };
             int64_t hit = -1;
             const int64_t len = hi - lo + 1;
             if (nt == 1 || len < 4 * nt) {
-                for (int64_t pos = hi; pos >= lo; --pos)
-                    if (test(pos)) { hit = pos; break; }
+                hit = scan(hi, lo);
             } else {
                 pool.run([&](int tid) {
                     const int64_t per = (len + nt - 1) / nt;
                     const int64_t top = hi - (int64_t)tid * per;
                     const int64_t bot = top - per + 1 > lo ? top - per + 1 : lo;
-                    int64_t f = -1;
-                    for (int64_t pos = top; pos >= bot; --pos)
-                        if (test(pos)) { f = pos; break; }
-                    found[(size_t)tid] = f;
+                    found[(size_t)tid] = top >= bot ? scan(top, bot) : -1;
                 });
                 for (int k = 0; k < nt; ++k)
                     if (found[(size_t)k] > hit) hit = found[(size_t)k];
@@ -211,6 +306,7 @@ void engine_index(const Patterns& P, float t, I* perm)
 {
     // Requires 0 <= t < 1 (checked by the caller).
     const int64_t M = P.M, W = P.words, NB = P.nblk;
+    const JaccardTest jt(t);
     // Row lists per block (CSR of the transposed pattern).
     std::vector<int64_t> start((size_t)NB + 1, 0);
     for (int64_t i = 0; i < M; ++i) {
@@ -290,7 +386,7 @@ void engine_index(const Patterns& P, float t, I* perm)
             limit = at;
             const int64_t inter = cnt[(size_t)r];
             const int64_t uni = pc + P.count[(size_t)r] - inter;
-            if (jaccard_distance(inter, uni) > t) continue;
+            if (!jt.close(inter, uni)) continue;
             perm[out++] = (I)r;
             done[(size_t)r] = 1;
             remove_at(at);
