@@ -251,6 +251,9 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
     Pool pool(nthreads);
     const int nt = pool.size();
     std::vector<int64_t> found((size_t)nt);
+    // positions searched per round before the range doubles: about 1024 per
+    // thread, so that a round's work outweighs waking the pool
+    const int64_t first_stretch = std::max<int64_t>(2048, 1024 * (int64_t)nt);
 
     while (n_un > 0) {
         const int64_t seed = un[(size_t)--n_un];
@@ -258,7 +261,7 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
         std::memcpy(p.data(), P.row(seed), (size_t)W * sizeof(uint64_t));
         int64_t pc = P.count[(size_t)seed];
         int64_t hi = n_un - 1;  // next position to visit
-        int64_t stretch = 2048;
+        int64_t stretch = first_stretch;
         while (hi >= 0) {
             // First joining position in [lo, hi], scanning downwards.
             const int64_t lo = hi - stretch + 1 > 0 ? hi - stretch + 1 : 0;
@@ -296,7 +299,7 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
             un[(size_t)hit] = un[(size_t)(n_un - 1)];
             --n_un;
             hi = hit - 1;
-            stretch = 2048;
+            stretch = first_stretch;
         }
     }
 }
