@@ -284,14 +284,15 @@ def main():
     print(f"[bench] {args.steps} steps, {ms:.4f} ms/step", file=sys.stderr, flush=True)
 
     # spot check of C on sampled rows against an fp64 numpy product
-    # (C is in the permuted row order: its row r is row perm[r] of A * B)
+    # (C is in the permuted row order: its row r is row perm[r] of A * B).
+    # Elementwise sums, not a BLAS call: BLAS worker threads keep spinning
+    # after a call and would slow the host clustering timed below.
     rows = np.random.default_rng(0).choice(M, size=min(256, M), replace=False)
     Ch = C.cpu().numpy()[rows].astype(np.float64)
-    Bf = p.B.astype(np.float64)
-    vf = p.vals.astype(np.float64)
     src = perm[rows]
-    ref = np.stack([vf[p.rp[r]:p.rp[r + 1]] @ Bf[p.ci[p.rp[r]:p.rp[r + 1]]] for r in src])
-    spot = float(np.linalg.norm(Ch - ref) / max(np.linalg.norm(ref), 1e-300))
+    ref = np.stack([(p.vals[p.rp[r]:p.rp[r + 1]].astype(np.float64)[:, None]
+                     * p.B[p.ci[p.rp[r]:p.rp[r + 1]]].astype(np.float64)).sum(axis=0) for r in src])
+    spot = float(np.sqrt(np.sum((Ch - ref) ** 2)) / max(np.sqrt(np.sum(ref ** 2)), 1e-300))
 
     sT = p.vals.dtype.itemsize
     sI = p.rp.dtype.itemsize
