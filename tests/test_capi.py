@@ -148,6 +148,20 @@ def test_product_clustering_templates_like_input():
         np.testing.assert_array_equal(widen(got), want)
 
 
+@pytest.mark.parametrize("n_templates,keep", [(16, 1.0), (64, 1.0), (64, 0.85), (63, 0.85)])
+def test_product_clustering_index_partner_lists(n_templates, keep, monkeypatch):
+    # the index engine's partner lists (at most 32 per row): 128 identical
+    # rows per template overflow them; 32 or 33 rows per template put the
+    # partner count at and just past the cap; keep < 1 makes the partners
+    # near-duplicates whose joins change the pattern
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", "index")
+    p = synth.templates(M=2048, n_templates=n_templates, keep=keep, seed=n_templates)
+    want = oracle.jaccard(p.M, p.K, p.rp, p.ci)
+    for nthreads in (1, 5):
+        got = X.compute_1d_jaccard_clustering(p.M, p.K, p.rp, p.ci, nthreads=nthreads)
+        np.testing.assert_array_equal(widen(got), want)
+
+
 @pytest.mark.parametrize("simd", ["scalar", "auto"])
 def test_product_clustering_scan_search_forms(simd, monkeypatch):
     # the scan engine's search has a scalar and an AVX-512 (vpopcntq) form,

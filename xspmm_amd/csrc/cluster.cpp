@@ -305,7 +305,7 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
 }
 
 template <typename I>
-void engine_index(const Patterns& P, float t, I* perm)
+void engine_index(const Patterns& P, float t, I* perm, int nthreads)
 {
     // Requires 0 <= t < 1 (checked by the caller).
     const int64_t M = P.M, W = P.words, NB = P.nblk;
@@ -327,6 +327,46 @@ void engine_index(const Patterns& P, float t, I* perm)
                 for (uint64_t b = q[w]; b; b &= b - 1)
                     rows[(size_t)fill[(size_t)(w * 64 + __builtin_ctzll(b))]++] = i;
         }
+    }
+
+    // Partner lists, all rows in parallel: row j is a partner of row i
+    // (j != i) when d(q_i, q_j) <= t.  Until its first join a cluster's
+    // pattern is q_seed, so a seed none of whose partners is still
+    // unclustered stays alone, and the greedy skips its search.  pn[i] = -1:
+    // the list was not kept (more than kPartnerCap partners, or an empty row).
+    constexpr int kPartnerCap = 32;
+    std::vector<int32_t> pn((size_t)M, -1);
+    std::vector<int64_t> plist((size_t)M * kPartnerCap);
+    {
+        Pool pool(nthreads);
+        const int nt = pool.size();
+        pool.run([&](int tid) {
+            std::vector<int32_t> c((size_t)M, 0);
+            std::vector<int64_t> seen;
+            for (int64_t i = tid; i < M; i += nt) {
+                const int64_t ci = P.count[(size_t)i];
+                if (ci == 0) continue;
+                const uint64_t* q = P.row(i);
+                for (int64_t w = 0; w < W; ++w)
+                    for (uint64_t b = q[w]; b; b &= b - 1) {
+                        const int64_t blk = w * 64 + __builtin_ctzll(b);
+                        for (int64_t k = start[(size_t)blk]; k < start[(size_t)blk + 1]; ++k) {
+                            const int64_t r = rows[(size_t)k];
+                            if (r != i && c[(size_t)r]++ == 0) seen.push_back(r);
+                        }
+                    }
+                int32_t np = 0;
+                for (const int64_t r : seen) {
+                    const int64_t inter = c[(size_t)r];
+                    c[(size_t)r] = 0;
+                    if (!jt.close(inter, ci + P.count[(size_t)r] - inter)) continue;
+                    if (np < kPartnerCap) plist[(size_t)i * kPartnerCap + np] = r;
+                    ++np;
+                }
+                seen.clear();
+                pn[(size_t)i] = np > kPartnerCap ? -1 : np;
+            }
+        });
     }
 
     std::vector<int64_t> un((size_t)M), pos((size_t)M);
@@ -365,6 +405,12 @@ void engine_index(const Patterns& P, float t, I* perm)
                 remove_at(pos[(size_t)e.second]);
             }
             continue;
+        }
+        if (pn[(size_t)seed] >= 0) {
+            bool any = false;
+            for (int32_t k = 0; k < pn[(size_t)seed] && !any; ++k)
+                any = !done[(size_t)plist[(size_t)seed * kPartnerCap + k]];
+            if (!any) continue;  // no unclustered partner: a cluster of one
         }
         std::memcpy(p.data(), P.row(seed), (size_t)W * sizeof(uint64_t));
         int64_t pc = P.count[(size_t)seed];
@@ -441,7 +487,7 @@ void jaccard_clustering_host(int64_t M, int64_t K, const I* rp, const I* ci, flo
         engine = (index_ok && index_cost < scan_cost) ? "index" : "scan";
     }
     if (engine == "index" && index_ok)
-        engine_index<I>(P, dist_thresh, perm);
+        engine_index<I>(P, dist_thresh, perm, nthreads);
     else
         engine_scan<I>(P, dist_thresh, perm, nthreads);
 }
