@@ -245,6 +245,25 @@ __global__ __launch_bounds__(kPrepThreads) void row_lists_kernel(const uint64_t*
     }
 }
 
+// Rows per column block, v_b, from the bitmaps without building any list:
+// thread b of grid.x counts bit b over its grid.y slice of rows (the 64
+// threads of a wave read the same word), then adds once.
+__global__ __launch_bounds__(kPrepThreads) void block_counts_kernel(const uint64_t* __restrict__ bits,
+                                                                    int64_t M, int64_t W, int64_t Kb,
+                                                                    int32_t* bl_count)
+{
+    const int64_t b = (int64_t)blockIdx.x * kPrepThreads + threadIdx.x;
+    if (b >= Kb) return;
+    const int64_t per = (M + gridDim.y - 1) / gridDim.y;
+    const int64_t r0 = (int64_t)blockIdx.y * per;
+    const int64_t r1 = r0 + per < M ? r0 + per : M;
+    const int64_t w = b >> 6;
+    const int sh = (int)(b & 63);
+    int32_t c = 0;
+    for (int64_t r = r0; r < r1; ++r) c += (int32_t)((bits[r * W + w] >> sh) & 1u);
+    if (c) atomicAdd(&bl_count[b], c);
+}
+
 // Row lists per block: bl_rows[bl_start[b] ...] (order within a list is free).
 __global__ __launch_bounds__(kPrepThreads) void block_lists_kernel(int64_t M,
                                                                    const int64_t* __restrict__ rb_start,
@@ -824,27 +843,71 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     hipLaunchKernelGGL(pattern_count_kernel, dim3(grid), dim3(kPrepThreads), 0, s,
                        bits.as<uint64_t>(), M, W, count.as<int32_t>());
     XSPMM_LAUNCH_CHECK();
+    const int64_t nb = Kb > 0 ? Kb : 1;
+    Scratch bl_count((size_t)nb * sizeof(int32_t), s);
+
+    // Engine and partner method, decided here so that the per-row and
+    // per-block lists are built only when a step reads them: the index
+    // engine and the row-list partner pass do, the scan engine and the
+    // bitmap partner pass do not.  The engine estimate needs only v_b.
+    int engine = kEngineAuto;
+    if (const char* e = std::getenv("XSPMM_CLUSTER_ENGINE")) {
+        if (std::strcmp(e, "scan") == 0) engine = kEngineScan;
+        else if (std::strcmp(e, "index") == 0) engine = kEngineIndex;
+    }
+    bool use_partners = true;
+    if (const char* e = std::getenv("XSPMM_CLUSTER_PARTNERS"))
+        use_partners = std::strcmp(e, "off") != 0;
+    const bool bitmap_partners = W <= 32 && (double)M * (double)M * (double)W <= 6.4e10;
+    // row list offsets: their total, sum_b v_b = sum_i |q_i|, bounds the
+    // engine estimate: (sum v_b)^2 / Kb <= sum v_b^2 <= sum v_b * min(M, sum v_b)
     Scratch rb_start((size_t)(M + 1) * sizeof(int64_t), s);
     device_exclusive_scan(ArrayValue<int32_t>{count.as<int32_t>()}, M, rb_start.as<int64_t>(), s);
     int64_t nrb = 0;
     XSPMM_HIP_CHECK(hipMemcpyAsync(&nrb, rb_start.as<int64_t>() + M, sizeof(int64_t),
                                    hipMemcpyDeviceToHost, s));
     XSPMM_HIP_CHECK(hipStreamSynchronize(s));
-    const int64_t nb = Kb > 0 ? Kb : 1;
-    Scratch rb((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
-    Scratch bl_count((size_t)nb * sizeof(int32_t), s);
-    XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
-    hipLaunchKernelGGL(row_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, bits.as<uint64_t>(),
-                       M, W, rb_start.as<int64_t>(), rb.as<int32_t>(), bl_count.as<int32_t>());
-    XSPMM_LAUNCH_CHECK();
-    Scratch bl_start((size_t)(nb + 1) * sizeof(int64_t), s);
-    device_exclusive_scan(ArrayValue<int32_t>{bl_count.as<int32_t>()}, nb, bl_start.as<int64_t>(), s);
-    XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
-    Scratch bl_rows((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
-    hipLaunchKernelGGL(block_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, M,
-                       rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
-                       bl_count.as<int32_t>(), bl_rows.as<int32_t>());
-    XSPMM_LAUNCH_CHECK();
+    const double scan_work = 0.5 * (double)M * (double)M * (double)W;
+    if (engine == kEngineAuto && Kb > 0) {
+        const double sv = (double)nrb;
+        if (3.0 * sv * sv / (double)Kb >= scan_work) engine = kEngineScan;
+        else if (3.0 * sv * std::min(sv, (double)M) < scan_work) engine = kEngineIndex;
+    }
+    if (engine == kEngineAuto) {
+        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
+        const int64_t gy = std::max<int64_t>(1, std::min<int64_t>(1024, (M + 255) / 256));
+        hipLaunchKernelGGL(block_counts_kernel, dim3((unsigned)((nb + kPrepThreads - 1) / kPrepThreads), (unsigned)gy),
+                           dim3(kPrepThreads), 0, s, bits.as<uint64_t>(), M, W, Kb,
+                           bl_count.as<int32_t>());
+        XSPMM_LAUNCH_CHECK();
+        std::vector<int32_t> h_bl((size_t)nb);
+        XSPMM_HIP_CHECK(hipMemcpyAsync(h_bl.data(), bl_count.get(), (size_t)nb * sizeof(int32_t),
+                                       hipMemcpyDeviceToHost, s));
+        XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+        int64_t sq = 0;
+        for (int64_t b = 0; b < Kb; ++b) sq += (int64_t)h_bl[(size_t)b] * h_bl[(size_t)b];
+        // the same estimate as the host engines: index ~ 3 * sum v_b^2
+        // counter updates, scan ~ M^2 * W / 2 word tests
+        engine = 3.0 * (double)sq < scan_work ? kEngineIndex : kEngineScan;
+    }
+    const bool need_lists = engine == kEngineIndex || (use_partners && !bitmap_partners);
+
+    Scratch rb, bl_start, bl_rows;
+    if (need_lists) {
+        rb = Scratch((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
+        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
+        hipLaunchKernelGGL(row_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, bits.as<uint64_t>(),
+                           M, W, rb_start.as<int64_t>(), rb.as<int32_t>(), bl_count.as<int32_t>());
+        XSPMM_LAUNCH_CHECK();
+        bl_start = Scratch((size_t)(nb + 1) * sizeof(int64_t), s);
+        device_exclusive_scan(ArrayValue<int32_t>{bl_count.as<int32_t>()}, nb, bl_start.as<int64_t>(), s);
+        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
+        bl_rows = Scratch((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
+        hipLaunchKernelGGL(block_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, M,
+                           rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
+                           bl_count.as<int32_t>(), bl_rows.as<int32_t>());
+        XSPMM_LAUNCH_CHECK();
+    }
 
     Scratch un((size_t)M * sizeof(int32_t), s), pos((size_t)M * sizeof(int32_t), s);
     Scratch cnt((size_t)M * sizeof(int32_t), s), logb((size_t)M * sizeof(int32_t), s);
@@ -855,12 +918,9 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     // partner lists (XSPMM_CLUSTER_PARTNERS=off leaves every seed on the full path)
     Scratch pn((size_t)M * sizeof(int32_t), s);
     Scratch partners((size_t)M * kPartnerCap * sizeof(int32_t), s);
-    bool use_partners = true;
-    if (const char* e = std::getenv("XSPMM_CLUSTER_PARTNERS"))
-        use_partners = std::strcmp(e, "off") != 0;
     if (use_partners) {
         const int Mi = (int)M, Wi = (int)W;
-        if (W <= 32 && (double)M * (double)M * (double)W <= 6.4e10) {
+        if (bitmap_partners) {
             XSPMM_HIP_CHECK(hipMemsetAsync(pn.get(), 0, (size_t)M * sizeof(int32_t), s));
             // about 2048 workgroups: the rows j are split over grid.y
             const int64_t gx = (M + kPairRows - 1) / kPairRows;
@@ -887,11 +947,6 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
         XSPMM_LAUNCH_CHECK();
     }
 
-    int engine = kEngineAuto;
-    if (const char* e = std::getenv("XSPMM_CLUSTER_ENGINE")) {
-        if (std::strcmp(e, "scan") == 0) engine = kEngineScan;
-        else if (std::strcmp(e, "index") == 0) engine = kEngineIndex;
-    }
     ClusterArgs args{M, W, Kb, dist_thresh, engine, bits.as<uint64_t>(), count.as<int32_t>(),
                      rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
                      bl_rows.as<int32_t>(), un.as<int32_t>(), pos.as<int32_t>(),
