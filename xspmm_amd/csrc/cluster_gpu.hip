@@ -307,8 +307,9 @@ constexpr int kHashSlots = 16384;
 
 // All pairs by bitmap popcounts (row bitmaps of at most MAXW words).
 // 256 threads: 64 rows i, four threads per row splitting each tile; the
-// rows j are split over gridDim.y workgroups.  pn[i] (zeroed first) ends as
-// the number of partners of row i; the first kPartnerCap are listed.
+// rows j are split over gridDim.y workgroups.  Each pair is tested once, as
+// j > i, and a close pair is listed for both rows.  pn[i] (zeroed first)
+// ends as the number of partners of row i; the first kPartnerCap are listed.
 template <int MAXW>
 __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __restrict__ bits,
                                                               const int32_t* __restrict__ count,
@@ -331,7 +332,11 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
     const int jbeg = (int)blockIdx.y * per * kPairTile;
     const int jend = min(M, jbeg + per * kPairTile);
     const JaccardTest jt(thr);
+    const int ibase = blockIdx.x * kPairRows;
     for (int j0 = jbeg; j0 < jend; j0 += kPairTile) {
+        // each pair once, as (i, j) with j > i: tiles wholly at or below this
+        // workgroup's first row hold none (a uniform skip)
+        if (j0 + kPairTile - 1 <= ibase) continue;
         __syncthreads();
         for (int x = t; x < kPairTile * MAXW; x += 256) {
             const int jj = x / MAXW, w = x % MAXW;
@@ -343,7 +348,7 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
         if (!vi) continue;
         for (int jj = part; jj < kPairTile; jj += 256 / kPairRows) {
             const int j = j0 + jj;
-            if (j >= jend || j == i) continue;
+            if (j >= jend || j <= i) continue;
             const int qj = tcount[jj];
             const int mn = qj < qc ? qj : qc, mx = qj < qc ? qc : qj;
             if (!jt.may_close(mn, mx)) continue;
@@ -351,9 +356,11 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
             int inter = 0;
 #pragma unroll
             for (int w = 0; w < MAXW; ++w) inter += __popcll(q[w] & tile[jj * MAXW + w]);
-            if (jt.close(inter, qc + qj - inter)) {
+            if (jt.close(inter, qc + qj - inter)) {  // partnership is symmetric
                 const int k = atomicAdd(&pn[i], 1);
                 if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
+                const int k2 = atomicAdd(&pn[j], 1);
+                if (k2 < kPartnerCap) partners[(int64_t)j * kPartnerCap + k2] = i;
             }
         }
     }
