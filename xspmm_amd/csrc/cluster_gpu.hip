@@ -307,7 +307,7 @@ constexpr int kHashSlots = 16384;
 
 // All pairs by bitmap popcounts (row bitmaps of at most MAXW words).
 // 256 threads: 64 rows i, four threads per row splitting each tile; the
-// rows j are split over gridDim.y workgroups.  Each pair is tested once, as
+// row tiles j are dealt over gridDim.y workgroups.  Each pair is tested once, as
 // j > i, and a close pair is listed for both rows.  pn[i] (zeroed first)
 // ends as the number of partners of row i; the first kPartnerCap are listed.
 template <int MAXW>
@@ -328,12 +328,13 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
     for (int w = 0; w < MAXW; ++w) q[w] = (vi && w < W) ? bits[(int64_t)i * W + w] : 0ULL;
     const int qc = vi ? count[i] : 0;
     const int tiles = (M + kPairTile - 1) / kPairTile;
-    const int per = (tiles + (int)gridDim.y - 1) / (int)gridDim.y;
-    const int jbeg = (int)blockIdx.y * per * kPairTile;
-    const int jend = min(M, jbeg + per * kPairTile);
+    const int jend = M;
     const JaccardTest jt(thr);
     const int ibase = blockIdx.x * kPairRows;
-    for (int j0 = jbeg; j0 < jend; j0 += kPairTile) {
+    // tiles of rows j dealt to the gridDim.y workgroups of a row block in
+    // turn, so that each gets its share of the tiles above the block
+    for (int tt = (int)blockIdx.y; tt < tiles; tt += (int)gridDim.y) {
+        const int j0 = tt * kPairTile;
         // each pair once, as (i, j) with j > i: tiles wholly at or below this
         // workgroup's first row hold none (a uniform skip)
         if (j0 + kPairTile - 1 <= ibase) continue;
