@@ -156,6 +156,28 @@ def _device(dev=None):
     return torch.device(dev)
 
 
+def _check_dense(t, name, rows, cols, dtype, device):
+    """Reject a dense operand the kernels cannot take as given: the kernels
+    read `rows` x `cols` elements row-major (ld = cols) from t.data_ptr() on
+    `device`.  Raised before any kernel is launched."""
+    torch = _torch()
+    if not torch.is_tensor(t):
+        raise TypeError(f"{name} must be a torch tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.device != torch.device(device):
+        raise ValueError(f"{name} is on {t.device}, the matrix is on {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous (row-major, ld = number of columns)")
+    shape = tuple(t.shape)
+    if t.dim() == 2:
+        ok = shape == (rows, cols)
+    else:
+        ok = t.dim() == 1 and t.numel() == rows * cols
+    if not ok:
+        raise ValueError(f"{name} has shape {shape}, expected ({rows}, {cols})")
+
+
 # ---------------------------------------------------------------------------
 # matrices
 # ---------------------------------------------------------------------------
@@ -238,10 +260,11 @@ def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
     L = load()
     if N is None:
         N = int(B.shape[1]) if B.dim() == 2 else int(B.numel() // max(A.num_cols, 1))
+    dev = A.row_ptr.device
     if C_out is None:
-        C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=A.row_ptr.device)
-    if A.values.dtype != B.dtype:
-        raise TypeError("A and B must share a value dtype")
+        C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=dev)
+    _check_dense(B, "B", A.num_cols, N, A.values.dtype, dev)
+    _check_dense(C_out, "C_out", A.num_rows, N, torch.float32, dev)
     _check(L.xspmm_bcsr_spmm(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows, A.num_cols,
                              A.num_block_rows, A.num_block_cols, A.num_blocks, _ptr(A.row_ptr),
                              _ptr(A.col_ind), _ptr(A.values), _ptr(B), _ptr(C_out), N, _stream()))
@@ -333,7 +356,12 @@ def unpermute_dense_matrix(C_in, perm, out=None):
     M, N = int(C_in.shape[0]), int(C_in.shape[1])
     if out is None:
         out = torch.empty_like(C_in)
+    _check_dense(C_in, "C_in", M, N, torch.float32, C_in.device)
+    _check_dense(out, "out", M, N, torch.float32, C_in.device)
     perm_t = perm if torch.is_tensor(perm) else torch.as_tensor(np.asarray(perm)).to(C_in.device)
+    if perm_t.device != C_in.device or perm_t.dim() != 1 or perm_t.numel() != M:
+        raise ValueError(f"perm must be a 1-D tensor of {M} entries on {C_in.device}")
+    perm_t = perm_t.contiguous()
     _check(L.xspmm_unpermute_dense(icode(perm_t.dtype), _ptr(C_in), _ptr(out), _ptr(perm_t), M, N,
                                    _stream()))
     return out
@@ -347,8 +375,11 @@ def spmm_pipeline(A: CSRMatrix, B, C_out=None, N: int | None = None, hw_block_si
     L = load()
     if N is None:
         N = int(B.shape[1])
+    dev = A.row_ptr.device
     if C_out is None:
-        C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=A.row_ptr.device)
+        C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=dev)
+    _check_dense(B, "B", A.num_cols, N, A.values.dtype, dev)
+    _check_dense(C_out, "C_out", A.num_rows, N, torch.float32, dev)
     t = (C.c_double * 6)() if timings else None
     _check(L.xspmm_spmm_pipeline(vcode(A.values.dtype), icode(A.row_ptr.dtype), A.num_rows,
                                  A.num_cols, A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind),
@@ -394,12 +425,12 @@ class SpMMPlan:
         torch = _torch()
         if self._h is None:
             raise RuntimeError("SpMMPlan is closed")
-        if B.dtype != self.value_dtype:
-            raise TypeError("B must have the plan's value dtype")
         if N is None:
             N = int(B.shape[1])
         if C_out is None:
             C_out = torch.empty((self.num_rows, N), dtype=torch.float32, device=self.device)
+        _check_dense(B, "B", self.num_cols, N, self.value_dtype, self.device)
+        _check_dense(C_out, "C_out", self.num_rows, N, torch.float32, self.device)
         _check(self._L.xspmm_plan_execute(self._h, _ptr(B), _ptr(C_out), N, _stream()))
         return C_out
 

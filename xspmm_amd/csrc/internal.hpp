@@ -59,6 +59,47 @@ private:
     hipStream_t s_ = nullptr;
 };
 
+// Device memory for a launcher's temporaries.  Without a region it makes
+// stream-ordered allocations (Scratch, released when the arena goes out of
+// scope); given a fixed region (the allocation-free entry point's scratch
+// array) it hands out 256-byte aligned pieces of it and throws
+// std::invalid_argument when a request does not fit.  Launchers take every
+// piece before they enqueue the first kernel that uses one, so a request
+// that does not fit leaves nothing half done.
+class TempArena {
+public:
+    explicit TempArena(hipStream_t s) : s_(s) {}
+    TempArena(void* base, size_t bytes, hipStream_t s)
+        : s_(s), base_(static_cast<char*>(base)), cap_(bytes) {}
+    TempArena(const TempArena&) = delete;
+    TempArena& operator=(const TempArena&) = delete;
+    bool fixed() const { return base_ != nullptr; }
+    size_t capacity() const { return cap_; }
+    void* take(size_t bytes) {
+        if (bytes == 0) return nullptr;
+        if (!base_) {
+            owned_.emplace_back(bytes, s_);
+            return owned_.back().get();
+        }
+        const size_t at = (used_ + 255) & ~size_t(255);
+        if (at > cap_ || bytes > cap_ - at)
+            throw std::invalid_argument(
+                "xSpMM: this product needs " + std::to_string(at + bytes) +
+                " bytes of scratch; the allocation-free entry point has " + std::to_string(cap_) +
+                " (use the allocating entry point for it).");
+        used_ = at + bytes;
+        return base_ + at;
+    }
+    template <typename T>
+    T* take_as(size_t count) { return static_cast<T*>(take(count * sizeof(T))); }
+
+private:
+    hipStream_t s_;
+    char* base_ = nullptr;
+    size_t cap_ = 0, used_ = 0;
+    std::vector<Scratch> owned_;
+};
+
 // Elapsed time of a stage bracketed by HIP events on stream s; stop() waits
 // for the stage and writes milliseconds.  A disabled timer does nothing.
 class StageTimer {
@@ -151,14 +192,16 @@ bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, c
                      const int32_t* order, const I* row_map, hipStream_t s);
 
 // Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb);
-// row_map (null: rows in place) as for bcsr_spmm_ex.  Returns false (and
-// launches nothing) when the shape is not covered; spmm_dense_f16_covers
-// tells in advance.
+// row_map (null: rows in place) as for bcsr_spmm_ex.  Each tile checks that
+// its block-rows hold the canonical layout (block br * Kb + c has column c)
+// and otherwise multiplies its blocks in stored order, so any block order
+// gives the right C.  Returns false (and launches nothing) when the shape is
+// not covered; spmm_dense_f16_covers tells in advance.
 bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N);
-template <typename RM>
+template <typename I>
 bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
-                         const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
-                         hipStream_t s, const RM* row_map);
+                         const I* brp, const I* bci, const uint16_t* bvals, const uint16_t* B,
+                         float* C, int64_t N, hipStream_t s, const I* row_map);
 
 // CSR -> BCSR.  count writes brp[Mb+1] and returns nnzb (synchronizes `s`);
 // it throws std::invalid_argument on an out-of-range column index.

@@ -1312,17 +1312,14 @@ void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s
 template void spmm_dispatch_order<int32_t>(const int32_t*, int64_t, int32_t*, hipStream_t);
 template void spmm_dispatch_order<int64_t>(const int64_t*, int64_t, int32_t*, hipStream_t);
 
-template <typename T, typename I>
-void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
-               const I* bci, const T* bvals, const T* B, float* C, int64_t N, hipStream_t s)
-{
-    (void)bcsr_spmm_ex<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr, s);
-}
+namespace {
 
+// The Tier-1 launcher: kernel choice as described at the top of this file;
+// temporaries (the dispatch order, repacked B panels) come from `arena`.
 template <typename T, typename I>
-bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
-                  const I* bci, const T* bvals, const T* B, float* C, int64_t N,
-                  const int32_t* order_in, const I* row_map, hipStream_t s)
+bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+                      const I* bci, const T* bvals, const T* B, float* C, int64_t N,
+                      const int32_t* order_in, const I* row_map, TempArena& arena, hipStream_t s)
 {
     check_shape(M, K, Mb, Kb, nnzb, N);
     if (M == 0 || N == 0 || Mb == 0) return true;
@@ -1341,7 +1338,7 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
         const Fp16Kernel choice = fp16_kernel_choice();
         // every block present: GEMM-tiled kernel (matrix-core bound)
         if (choice == Fp16Kernel::kAuto && spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N))
-            return bcsr_spmm_dense_f16<I>(M, K, Mb, Kb, nnzb, v, b, C, N, s, row_map);
+            return bcsr_spmm_dense_f16<I>(M, K, Mb, Kb, nnzb, brp, bci, v, b, C, N, s, row_map);
         const bool offsets32 = K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
                                Kb < (int64_t(1) << 20);
         const int64_t chunks = (N + 127) / 128;
@@ -1351,12 +1348,11 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
             offsets32) {
             // more block-rows than resident workgroups (4 per CU on 256 CUs,
             // times two): dispatch the longest rows first
-            Scratch order_buf;
             const int32_t* order = order_in;
             if (!order && spmm_order_wanted(Mb)) {
-                order_buf = Scratch((size_t)Mb * sizeof(int32_t), s);
-                spmm_dispatch_order<I>(brp, Mb, order_buf.as<int32_t>(), s);
-                order = order_buf.as<int32_t>();
+                int32_t* buf = arena.take_as<int32_t>((size_t)Mb);
+                spmm_dispatch_order<I>(brp, Mb, buf, s);
+                order = buf;
             }
             if (N <= 16)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
@@ -1385,26 +1381,25 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
             return true;
         }
         const int64_t Np = ntiles64 * 16;
-        Scratch bt((size_t)(Kb > 0 ? Kb : 1) * (size_t)Np * 16 * sizeof(uint16_t), s);
+        uint16_t* bt = arena.take_as<uint16_t>((size_t)(Kb > 0 ? Kb : 1) * (size_t)Np * 16);
         if (Kb > 0) {
             const int64_t per_kb = Np * 2;
             const dim3 pg((unsigned)((per_kb + 255) / 256), (unsigned)(Kb < 65535 ? Kb : 65535));
-            hipLaunchKernelGGL(pack_b_panels, pg, dim3(256), 0, s, b, bt.as<uint16_t>(), K, N, Kb,
-                               Np);
+            hipLaunchKernelGGL(pack_b_panels, pg, dim3(256), 0, s, b, bt, K, N, Kb, Np);
             XSPMM_LAUNCH_CHECK();
         }
         switch (geo.ntw) {
         case 4:
-            hipLaunchKernelGGL((spmm_f16_kernel<I, 4>), grid, block, 0, s, brp, bci, v,
-                               bt.as<uint16_t>(), C, M, N, Np, Kb, ntiles);
+            hipLaunchKernelGGL((spmm_f16_kernel<I, 4>), grid, block, 0, s, brp, bci, v, bt, C, M,
+                               N, Np, Kb, ntiles);
             break;
         case 2:
-            hipLaunchKernelGGL((spmm_f16_kernel<I, 2>), grid, block, 0, s, brp, bci, v,
-                               bt.as<uint16_t>(), C, M, N, Np, Kb, ntiles);
+            hipLaunchKernelGGL((spmm_f16_kernel<I, 2>), grid, block, 0, s, brp, bci, v, bt, C, M,
+                               N, Np, Kb, ntiles);
             break;
         default:
-            hipLaunchKernelGGL((spmm_f16_kernel<I, 1>), grid, block, 0, s, brp, bci, v,
-                               bt.as<uint16_t>(), C, M, N, Np, Kb, ntiles);
+            hipLaunchKernelGGL((spmm_f16_kernel<I, 1>), grid, block, 0, s, brp, bci, v, bt, C, M,
+                               N, Np, Kb, ntiles);
             break;
         }
         XSPMM_LAUNCH_CHECK();
@@ -1440,28 +1435,38 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
     return true;
 }
 
-#define XSPMM_SPMM_EX(T, I)                                                                  \
-    template bool bcsr_spmm_ex<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*,  \
-                                     const I*, const T*, const T*, float*, int64_t,          \
-                                     const int32_t*, const I*, hipStream_t);
+}  // namespace
+
+template <typename T, typename I>
+void bcsr_spmm(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+               const I* bci, const T* bvals, const T* B, float* C, int64_t N, hipStream_t s)
+{
+    TempArena arena(s);
+    (void)bcsr_spmm_launch<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr,
+                                 arena, s);
+}
+
+template <typename T, typename I>
+bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+                  const I* bci, const T* bvals, const T* B, float* C, int64_t N,
+                  const int32_t* order_in, const I* row_map, hipStream_t s)
+{
+    TempArena arena(s);
+    return bcsr_spmm_launch<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, order_in, row_map,
+                                  arena, s);
+}
+
+#define XSPMM_SPMM_EX(T, I)                                                                      \
+    template bool bcsr_spmm_ex<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*,      \
+                                     const I*, const T*, const T*, float*, int64_t,              \
+                                     const int32_t*, const I*, hipStream_t);                     \
+    template void bcsr_spmm<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*,         \
+                                  const I*, const T*, const T*, float*, int64_t, hipStream_t);
 XSPMM_SPMM_EX(uint16_t, int32_t)
 XSPMM_SPMM_EX(uint16_t, int64_t)
 XSPMM_SPMM_EX(float, int32_t)
 XSPMM_SPMM_EX(float, int64_t)
 #undef XSPMM_SPMM_EX
-
-template void bcsr_spmm<uint16_t, int32_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                           const int32_t*, const int32_t*, const uint16_t*,
-                                           const uint16_t*, float*, int64_t, hipStream_t);
-template void bcsr_spmm<uint16_t, int64_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                           const int64_t*, const int64_t*, const uint16_t*,
-                                           const uint16_t*, float*, int64_t, hipStream_t);
-template void bcsr_spmm<float, int32_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                        const int32_t*, const int32_t*, const float*,
-                                        const float*, float*, int64_t, hipStream_t);
-template void bcsr_spmm<float, int64_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                        const int64_t*, const int64_t*, const float*,
-                                        const float*, float*, int64_t, hipStream_t);
 
 }  // namespace detail
 }  // namespace xspmm

@@ -124,18 +124,114 @@ __device__ __forceinline__ uint32_t panel_swz(uint32_t e)
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
 }
 
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+// Whether the workgroup's block-rows [br0, br0 + rows) hold their blocks in
+// the canonical full-grid layout: row br spans [br * Kb, (br + 1) * Kb) and
+// block br * Kb + c has column c.  Every thread of the workgroup gets the
+// answer.  Loads go out eight at a time, so a tile of 16 rows x 256 columns
+// costs one memory round trip.
+template <typename I>
+__device__ bool tile_is_canonical(const I* __restrict__ brp, const I* __restrict__ bci,
+                                  int64_t br0, int rows, int64_t Kb)
+{
+    const int t = threadIdx.x;
+    bool ok = true;
+    if (t <= rows) ok = (int64_t)brp[br0 + t] == (br0 + t) * Kb;
+    // rows * Kb < 2^31: the launcher only takes grids with Mb * Kb * 512 < 2^31
+    const uint32_t total = (uint32_t)rows * (uint32_t)Kb;
+    const uint32_t kb = (uint32_t)Kb;
+    const I* base = bci + br0 * Kb;
+    for (uint32_t i0 = (uint32_t)t; i0 < total; i0 += 8u * kDThreads) {
+        I v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t i = i0 + (uint32_t)u * kDThreads;
+            v[u] = i < total ? base[i] : (I)(i % kb);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t i = i0 + (uint32_t)u * kDThreads;
+            ok &= (int64_t)v[u] == (int64_t)(i % kb);
+        }
+    }
+    return __syncthreads_and(ok ? 1 : 0) != 0;
+}
+
+// Product of a tile whose blocks are not in the canonical layout (a
+// caller-built matrix with nnzb == Mb * Kb but another block order): every
+// block of the row in stored order, as the reference tile kernel does
+// (src/common/spmm_math.hpp:68-114), with v_mfma_f32_16x16x16_f16 and B read
+// straight from memory.  Columns outside [0, Kb) contribute nothing, as in
+// the column-batch kernel.  Wave w takes block-rows br0 + w, br0 + w + 8, ...
+// and all 16 column tiles of the workgroup.  Slow, but only a malformed or
+// unusual input takes it.
+template <typename I>
+__device__ void dense_tile_generic(const I* __restrict__ brp, const I* __restrict__ bci,
+                                   const uint16_t* __restrict__ vals, const uint16_t* __restrict__ B,
+                                   float* __restrict__ C, int64_t M, int64_t K, int64_t N,
+                                   int64_t Mb, int64_t Kb, int64_t br0, int rows, int64_t n0,
+                                   const I* __restrict__ row_map)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const _Float16* Bh = reinterpret_cast<const _Float16*>(B);
+    for (int r = wave; r < rows; r += kDW) {
+        const int64_t br = br0 + r;
+        if (br >= Mb) break;
+        float4_t acc[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+        const int64_t be = (int64_t)brp[br + 1];
+        for (int64_t b = (int64_t)brp[br]; b < be; ++b) {
+            const int64_t col = (int64_t)bci[b];
+            if (col < 0 || col >= Kb) continue;
+            // A[li][4g .. 4g + 3] of the block
+            const half4_t a = *reinterpret_cast<const half4_t*>(vals + b * 256 + li * 16 + 4 * g);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int64_t n = n0 + 16 * j + li;
+                half4_t bo;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int64_t k = 16 * col + 4 * g + s;
+                    bo[s] = (k < K && n < N) ? Bh[k * N + n] : (_Float16)0.f;
+                }
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bo, acc[j], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int64_t n = n0 + 16 * j + li;
+            if (n >= N) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t row = 16 * br + 4 * g + q;
+                if (row >= M) continue;
+                const int64_t crow = row_map ? (int64_t)row_map[row] : row;
+                C[crow * N + n] = acc[j][q];
+            }
+        }
+    }
+}
+
 // RW: block-rows per wave (8: 256-row tiles; 7: 224-row tiles, whose A stage
-// rows 14 and 15 load as zeros).  RM: index type of the optional output row
-// map (C row row_map[r] receives product row r -- the clustered pipeline's
-// un-permutation fused into the store; null stores rows in place).
-template <int RW, typename RM>
-__global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const uint16_t* __restrict__ vals,
+// rows 14 and 15 load as zeros).  I: index type of brp / bci and of the
+// optional output row map (C row row_map[r] receives product row r -- the
+// clustered pipeline's un-permutation fused into the store; null stores rows
+// in place).
+template <int RW, typename I>
+__global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_kernel(const I* __restrict__ brp,
+                                                                 const I* __restrict__ bci,
+                                                                 const uint16_t* __restrict__ vals,
                                                                  const uint16_t* __restrict__ B,
                                                                  float* __restrict__ C,
                                                                  int64_t M, int64_t K,
                                                                  int64_t N, int64_t Mb,
                                                                  int64_t Kb,
-                                                                 const RM* __restrict__ row_map)
+                                                                 const I* __restrict__ row_map)
 {
     constexpr int NS = XSPMM_DENSE_STAGES;
     constexpr int kDR = kWR * RW;  // block-rows per workgroup
@@ -166,6 +262,13 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
     if (rg * kDR >= Mb) return;  // padding workgroups of the last row-group band
     const int64_t n0 = cg * kDN;
     const int64_t br0 = rg * kDR;
+    {
+        const int rows = (int)(Mb - br0 < kDR ? Mb - br0 : kDR);
+        if (!tile_is_canonical<I>(brp, bci, br0, rows, Kb)) {
+            dense_tile_generic<I>(brp, bci, vals, B, C, M, K, N, Mb, Kb, br0, rows, n0, row_map);
+            return;
+        }
+    }
 
     const uint32_t a_bytes = (uint32_t)(Mb * Kb * 512);
     const i32x4_t a_rsrc = raw_rsrc(vals, a_bytes);
@@ -415,30 +518,32 @@ bool spmm_dense_f16_covers(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t
     return dense_groups(Mb, N, 14) <= 0x7fffffffLL;
 }
 
-template <typename RM>
+template <typename I>
 bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
-                         const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
-                         hipStream_t s, const RM* row_map)
+                         const I* brp, const I* bci, const uint16_t* bvals, const uint16_t* B,
+                         float* C, int64_t N, hipStream_t s, const I* row_map)
 {
     if (!spmm_dense_f16_covers(M, K, Mb, Kb, nnzb, N)) return false;
     const int h = dense_tile_rows(Mb, N);
     const int64_t groups = dense_groups(Mb, N, h);
     if (h == 14)
-        hipLaunchKernelGGL((spmm_f16_dense_kernel<7, RM>), dim3((unsigned)groups), dim3(kDThreads), 0,
-                           s, bvals, B, C, M, K, N, Mb, Kb, row_map);
+        hipLaunchKernelGGL((spmm_f16_dense_kernel<7, I>), dim3((unsigned)groups), dim3(kDThreads), 0,
+                           s, brp, bci, bvals, B, C, M, K, N, Mb, Kb, row_map);
     else
-        hipLaunchKernelGGL((spmm_f16_dense_kernel<8, RM>), dim3((unsigned)groups), dim3(kDThreads), 0,
-                           s, bvals, B, C, M, K, N, Mb, Kb, row_map);
+        hipLaunchKernelGGL((spmm_f16_dense_kernel<8, I>), dim3((unsigned)groups), dim3(kDThreads), 0,
+                           s, brp, bci, bvals, B, C, M, K, N, Mb, Kb, row_map);
     XSPMM_LAUNCH_CHECK();
     return true;
 }
 
 template bool bcsr_spmm_dense_f16<int32_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                           const uint16_t*, const uint16_t*, float*, int64_t,
-                                           hipStream_t, const int32_t*);
+                                           const int32_t*, const int32_t*, const uint16_t*,
+                                           const uint16_t*, float*, int64_t, hipStream_t,
+                                           const int32_t*);
 template bool bcsr_spmm_dense_f16<int64_t>(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                           const uint16_t*, const uint16_t*, float*, int64_t,
-                                           hipStream_t, const int64_t*);
+                                           const int64_t*, const int64_t*, const uint16_t*,
+                                           const uint16_t*, float*, int64_t, hipStream_t,
+                                           const int64_t*);
 
 }  // namespace detail
 }  // namespace xspmm
