@@ -58,6 +58,31 @@ int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int6
                     const void* B, float* C, int64_t N, void* stream);
 
 /*
+ * Tier-1 BCSR SpMM that allocates nothing: the same arguments, kernels and
+ * result (bit for bit) as xspmm_bcsr_spmm, but every temporary the launch
+ * needs (the dispatch order of a long block-row grid, the repacked B panels
+ * of the N % 8 != 0 path) comes from a fixed device array of
+ * xspmm_noalloc_scratch_bytes() bytes (8 MiB) that each GPU holds for the
+ * life of the process.  No hipMalloc, hipFree or allocating library call is
+ * made (the array's device address is looked up once per device, on the
+ * first call there).  A product that needs more scratch than the array holds
+ * (e.g. more than 2^21 block-rows on the fp16 column-batch path) is rejected
+ * with XSPMM_ERR_INVALID before anything is launched.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be serialized by the caller.
+ * Asynchronous on `stream`.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).
+ */
+int xspmm_bcsr_spmm_noalloc(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                            int64_t nnzb, const void* brp, const void* bci, const void* bvals,
+                            const void* B, float* C, int64_t N, void* stream);
+
+/* Size in bytes of the per-GPU scratch array of xspmm_bcsr_spmm_noalloc. */
+int64_t xspmm_noalloc_scratch_bytes(void);
+
+/*
  * CSR -> BCSR, phase 1: writes bcsr_row_ptr[Mb+1] (device) for r x c blocks,
  * Mb = ceil(M/r), and stores nnzb in *nnzb_out (host).  Synchronizes `stream`.
  * Fails with XSPMM_ERR_INVALID if a column index lies outside [0, K).

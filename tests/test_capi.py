@@ -64,6 +64,22 @@ def test_negative_and_inconsistent_sizes_are_rejected_without_gpu():
     assert b"hw_block_size" in L.xspmm_last_error()
 
 
+def test_noalloc_entry_point_argument_errors_without_gpu():
+    # type codes and sizes are checked before the scratch array is looked up
+    L = X.load()
+    L.xspmm_bcsr_spmm_noalloc.restype = C.c_int
+    L.xspmm_bcsr_spmm_noalloc.argtypes = L.xspmm_bcsr_spmm.argtypes
+    L.xspmm_noalloc_scratch_bytes.restype = C.c_int64
+    assert L.xspmm_noalloc_scratch_bytes() == 8 << 20
+    rc = L.xspmm_bcsr_spmm_noalloc(7, X.I32, 16, 16, 1, 1, 0, None, None, None, None, None, 16,
+                                   None)
+    assert rc == X.ERR_INVALID and b"value type" in L.xspmm_last_error()
+    assert L.xspmm_bcsr_spmm_noalloc(X.F16, X.I32, -1, 16, 1, 1, 0, None, None, None, None, None,
+                                     16, None) == X.ERR_INVALID
+    assert L.xspmm_bcsr_spmm_noalloc(X.F16, X.I32, 33, 16, 2, 1, 0, None, None, None, None, None,
+                                     16, None) == X.ERR_INVALID
+
+
 def test_host_clustering_error_paths():
     with pytest.raises(X.XspmmInvalidArgument):
         X.compute_1d_jaccard_clustering(2, 16, np.array([0, 1, 2], np.int32),

@@ -103,6 +103,23 @@ int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int6
     });
 }
 
+int xspmm_bcsr_spmm_noalloc(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                            int64_t nnzb, const void* brp, const void* bci, const void* bvals,
+                            const void* B, float* C, int64_t N, void* stream)
+{
+    return guarded([&] {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            bcsr_spmm_noalloc<T, I>(M, K, Mb, Kb, nnzb, static_cast<const I*>(brp),
+                                    static_cast<const I*>(bci), static_cast<const T*>(bvals),
+                                    static_cast<const T*>(B), C, N, as_stream(stream));
+        });
+    });
+}
+
+int64_t xspmm_noalloc_scratch_bytes(void) { return (int64_t)kNoAllocScratchBytes; }
+
 int xspmm_csr_to_bcsr_count(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
                             const void* ci, int64_t r_block, int64_t c_block,
                             void* bcsr_row_ptr, int64_t* nnzb_out, void* stream)

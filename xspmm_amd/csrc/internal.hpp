@@ -160,6 +160,14 @@ template <typename T, typename I>
 bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
                   const I* bci, const T* bvals, const T* B, float* C, int64_t N,
                   const int32_t* order, const I* row_map, hipStream_t s);
+// Tier-1 without any allocation: the temporaries come from a fixed device
+// array of kNoAllocScratchBytes (one copy per GPU, shared by every call on
+// it).  Throws std::invalid_argument when a product needs more.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+template <typename T, typename I>
+void bcsr_spmm_noalloc(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+                       const I* bci, const T* bvals, const T* B, float* C, int64_t N,
+                       hipStream_t s);
 // Longest-block-row-first dispatch order of the fp16 batch kernel: whether
 // the grid is long enough to use one, and the kernel that writes it (Mb ids).
 bool spmm_order_wanted(int64_t Mb);

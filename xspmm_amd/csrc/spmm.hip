@@ -26,6 +26,7 @@
 // Work split: one workgroup per block-row (grid.x, or the dispatch order of
 // order_rows_kernel), N split over grid.y.
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "internal.hpp"
@@ -1435,6 +1436,37 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
     return true;
 }
 
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+// Scratch of the allocation-free entry point (bcsr_spmm_noalloc): the only
+// device memory it uses beyond its inputs and outputs.  Each GPU holds its
+// own copy for the life of the process; every call on a GPU shares it, so
+// calls that overlap on one GPU race.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a shadow variable, not device
+// memory): it uses the device address that hipGetSymbolAddress returns,
+// looked up once per device.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+void* noalloc_scratch(int dev)
+{
+    static std::mutex mu;
+    static void* ptr[kMaxDevices] = {};
+    if (dev < 0 || dev >= kMaxDevices)
+        throw std::invalid_argument("xSpMM: device index outside the allocation-free entry point's table.");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        XSPMM_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) throw std::runtime_error("xSpMM: no device address for the SpMM scratch array.");
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
+
 }  // namespace
 
 template <typename T, typename I>
@@ -1456,12 +1488,28 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
                                   arena, s);
 }
 
+template <typename T, typename I>
+void bcsr_spmm_noalloc(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
+                       const I* bci, const T* bvals, const T* B, float* C, int64_t N,
+                       hipStream_t s)
+{
+    check_shape(M, K, Mb, Kb, nnzb, N);
+    int dev = 0;
+    XSPMM_HIP_CHECK(hipGetDevice(&dev));
+    TempArena arena(noalloc_scratch(dev), kNoAllocScratchBytes, s);
+    (void)bcsr_spmm_launch<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr,
+                                 arena, s);
+}
+
 #define XSPMM_SPMM_EX(T, I)                                                                      \
     template bool bcsr_spmm_ex<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*,      \
                                      const I*, const T*, const T*, float*, int64_t,              \
                                      const int32_t*, const I*, hipStream_t);                     \
     template void bcsr_spmm<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*,         \
-                                  const I*, const T*, const T*, float*, int64_t, hipStream_t);
+                                  const I*, const T*, const T*, float*, int64_t, hipStream_t);   \
+    template void bcsr_spmm_noalloc<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*, \
+                                          const I*, const T*, const T*, float*, int64_t,         \
+                                          hipStream_t);
 XSPMM_SPMM_EX(uint16_t, int32_t)
 XSPMM_SPMM_EX(uint16_t, int64_t)
 XSPMM_SPMM_EX(float, int32_t)
