@@ -184,6 +184,9 @@ void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s
 // with the same order / row_map meaning); it returns false when N is not
 // covered (N % 8 != 0 or too large).
 bool spmm_f16_pack_supported(int64_t K, int64_t Mb, int64_t Kb);
+// Waves per workgroup of the batch kernels: the batch counts and offsets
+// hold this many entries per block-row.
+int spmm_batch_waves();
 // offsets[0..n] = exclusive scan of counts[0..n-1]; returns offsets[n]
 // (synchronizes s).
 int64_t spmm_f16_pack_offsets(const int32_t* counts, int64_t n, int64_t* offsets, hipStream_t s);

@@ -130,11 +130,11 @@ public:
         if (const char* e = std::getenv("XSPMM_PLAN_PACK"))
             if (std::strcmp(e, "off") == 0) return;
         const uint16_t* v = reinterpret_cast<const uint16_t*>(bvals_.as<T>());
-        Scratch counts((size_t)Mb_ * 4 * sizeof(int32_t), s);
+        Scratch counts((size_t)Mb_ * spmm_batch_waves() * sizeof(int32_t), s);
         spmm_f16_pack_count<I>(M_, K_, Mb_, Kb_, brp_.as<I>(), bci_.as<I>(), v,
                                counts.as<int32_t>(), s);
-        DeviceBuffer offsets((size_t)(Mb_ * 4 + 1) * sizeof(int64_t));
-        const int64_t nb = spmm_f16_pack_offsets(counts.as<int32_t>(), Mb_ * 4,
+        DeviceBuffer offsets((size_t)(Mb_ * spmm_batch_waves() + 1) * sizeof(int64_t));
+        const int64_t nb = spmm_f16_pack_offsets(counts.as<int32_t>(), Mb_ * spmm_batch_waves(),
                                                  offsets.as<int64_t>(), s);
         if ((double)nb * (1024.0 + 128.0) > 0.75 * (double)nnzb_ * 512.0) return;
         pa_.reset((size_t)(nb > 0 ? nb : 1) * 1024);

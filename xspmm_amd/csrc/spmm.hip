@@ -524,6 +524,15 @@ constexpr int kBatchWaveLds = kSlotOff + 32 * 4;
 // each wave's region starts 16-byte aligned (128-bit LDS accesses)
 static_assert(kBatchWaveLds % 16 == 0 && kApOff % 16 == 0 && kSlotOff % 16 == 0,
               "batch kernel LDS layout must keep 16-byte alignment");
+#ifndef XSPMM_BATCH_WAVES
+#define XSPMM_BATCH_WAVES 4
+#endif
+// Waves per workgroup of the column-batch kernels (count, pack, multiply and
+// the packed kernel): they take a block-row's pairs in turn and sum their
+// partial tiles in wave order.  The batch kernel is compiled for four
+// resident workgroups per CU, i.e. kBW waves per SIMD and 512 / kBW VGPRs.
+constexpr int kBW = XSPMM_BATCH_WAVES;
+static_assert(kBW >= 2 && kBW <= 4, "2 .. 4 waves per batch workgroup");
 #ifndef XSPMM_BATCH_DEPTH
 #define XSPMM_BATCH_DEPTH 5
 #endif
@@ -543,7 +552,7 @@ constexpr int batch_depth()
 }
 static_assert(XSPMM_BATCH_DEPTH >= 4 && XSPMM_BATCH_DEPTH <= 10 && XSPMM_BATCH_DEPTH_NARROW >= 4 &&
                   XSPMM_BATCH_DEPTH_NARROW <= 10,
-              "batch depth must be 4 .. 10");
+              "batch depth must be 4 .. 10 (the ring holds ten pairs)");
 
 // swizzle of row e: even values 0..14, each used by two of the 16 rows a
 // transpose read touches
@@ -568,7 +577,7 @@ struct BatchPack {
     uint32_t* rows;           // kPack: B-row indices
 };
 
-// Sum the four waves' partial 16 x (16 NT) tiles through LDS (in wave order)
+// Sum the kBW waves' partial 16 x (16 NT) tiles through LDS (in wave order)
 // and store C rows: product row r of the block-row goes to C row row_map[r]
 // when row_map is given (the un-permutation fused), else to row r.
 template <typename I, int NT>
@@ -578,32 +587,37 @@ __device__ __forceinline__ void batch_tile_store(const float4_t (&acc)[NT], unsi
                                                  const I* __restrict__ row_map)
 {
     __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);  // 4 x [16][128] fp32 = 32 KB
+    float* red = reinterpret_cast<float*>(smem);  // kBW x [16][128] fp32 = kBW x 8 KB
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[wave * 2048 + (4 * g + r) * 128 + 16 * j + li] = acc[j][r];
     __syncthreads();
-    const int t = threadIdx.x;
-    const int row = t >> 4;
-    const int c0 = (t & 15) * 8;
-    const int64_t grow = br * 16 + row;
-    if (grow < M && c0 < NT * 16) {
-        float out[8];
+    // 256 items of 8 columns (16 rows x 128 columns)
+    for (int t = threadIdx.x; t < 256; t += 64 * kBW) {
+        const int row = t >> 4;
+        const int c0 = (t & 15) * 8;
+        const int64_t grow = br * 16 + row;
+        if (grow < M && c0 < NT * 16) {
+            float out[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int o = row * 128 + c0 + e;
-            out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
-        }
-        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
-        float* dst = C + crow * N + n0 + c0;
-        if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
-            *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
-            *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
-        } else {
+            for (int e = 0; e < 8; ++e) {
+                const int o = row * 128 + c0 + e;
+                float v = red[o];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (n0 + c0 + e < N) dst[e] = out[e];
+                for (int w = 1; w < kBW; ++w) v += red[w * 2048 + o];
+                out[e] = v;
+            }
+            const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+            float* dst = C + crow * N + n0 + c0;
+            if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
+                *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+                *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (n0 + c0 + e < N) dst[e] = out[e];
+            }
         }
     }
 }
@@ -627,8 +641,10 @@ __device__ __forceinline__ constexpr uint32_t kslot(uint32_t k)
     return 16u * ((k >> 2) & 1u) + 4u * (k >> 3) + (k & 3u);
 }
 
+// (HIP's second __launch_bounds__ argument is the minimum number of waves per
+// SIMD: kBW, for four resident workgroups per CU.)
 template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply>
-__global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
+__global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
     int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map, BatchPack pk)
@@ -642,7 +658,7 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
     // discard word for slot-list writes of lanes without a column: pad bytes
     // 72..75 of S^T row 0 (reads cover bytes 0..63 of each row)
     constexpr uint32_t kSlotPad = kSel + 72;
-    __shared__ __align__(16) unsigned char smem[4 * kBatchWaveLds];
+    __shared__ __align__(16) unsigned char smem[kBW * kBatchWaveLds];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     unsigned char* const W = smem + wave * kBatchWaveLds;
@@ -668,13 +684,13 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
     const uint32_t kb32 = (uint32_t)Kb;
     const uint32_t k32 = (uint32_t)K;
     const uint32_t rowbytes = (uint32_t)(2 * N);
-    // index window of one ring pass (pairs q, q + 4, ..., q + 4 (depth - 1)
+    // index window of one ring pass (pairs q, q + kBW, ..., q + kBW (depth - 1)
     // of this wave): lane l holds dword l of their block columns in order,
     // so pair j's columns sit in lanes 2j, 2j + 1 (int64: 4j .. 4j + 3)
     const uint32_t cw_off = sizeof(I) == 4
-                                ? 32u * (uint32_t)(lane >> 1) + 4u * (uint32_t)(lane & 1)
-                                : 64u * (uint32_t)(lane >> 2) + 8u * (uint32_t)((lane >> 1) & 1) +
-                                      4u * (uint32_t)(lane & 1);
+                                ? 8u * kBW * (uint32_t)(lane >> 1) + 4u * (uint32_t)(lane & 1)
+                                : 16u * kBW * (uint32_t)(lane >> 2) +
+                                      8u * (uint32_t)((lane >> 1) & 1) + 4u * (uint32_t)(lane & 1);
 
     // --- per-lane constants --------------------------------------------------
     // Pair mask layout: lane (r, g)'s non-zero halves 2d go to bit 4g + d and
@@ -752,7 +768,7 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
     };
     int64_t nbatch = 0;
     int64_t pbase = 0;
-    if constexpr (MODE == BatchMode::kPack) pbase = pk.offsets[br * 4 + wave];
+    if constexpr (MODE == BatchMode::kPack) pbase = pk.offsets[br * kBW + wave];
     // Close the open batch of `cnt` slots: A' from the D registers (exact
     // fp16 values), then multiply the previous batch and issue this one's
     // B row loads in K order.
@@ -874,7 +890,7 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
 
     if (wave < npairs) {
         half8_t P0, P1, P2, P3, P4, P5, P6, P7, P8, P9;
-        constexpr int S = 4;
+        constexpr int S = kBW;
         constexpr int A = S * D;
         const int64_t q0 = wave;
         // the window before the A loads, as in every later pass, so the
@@ -933,7 +949,7 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
         }
     }
     if constexpr (MODE == BatchMode::kCount) {
-        if (lane == 0) pk.counts[br * 4 + wave] = (int32_t)nbatch;
+        if (lane == 0) pk.counts[br * kBW + wave] = (int32_t)nbatch;
         return;
     } else if constexpr (MODE == BatchMode::kPack) {
         return;
@@ -953,7 +969,7 @@ __global__ __launch_bounds__(256, 4) void spmm_f16_batch_kernel(
 // are loading.  LDS holds only the B tile of each wave (8 KB).  grid = (block-rows, ceil(N / 128)); N % 8 == 0, K * N * 2 <= 2^31.
 // ---------------------------------------------------------------------------
 template <typename I, int NT>
-__global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_kernel(
+__global__ __launch_bounds__(64 * kBW, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_kernel(
     const int64_t* __restrict__ offsets, const u32x4_t* __restrict__ pa,
     const uint32_t* __restrict__ prow, const uint16_t* __restrict__ B, float* __restrict__ C,
     int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ order, const I* __restrict__ row_map)
@@ -961,7 +977,7 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_ke
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
     constexpr int RPL = 64 / CPR;  // B rows per load instruction
-    __shared__ __align__(16) unsigned char smem[4 * kBtBytes];
+    __shared__ __align__(16) unsigned char smem[kBW * kBtBytes];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     unsigned char* const W = smem + wave * kBtBytes;
@@ -985,8 +1001,8 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_ke
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t b0 = offsets[br * 4 + wave];
-    const int nb = (int)(offsets[br * 4 + wave + 1] - b0);
+    const int64_t b0 = offsets[br * kBW + wave];
+    const int nb = (int)(offsets[br * kBW + wave + 1] - b0);
     if (nb > 0) {
         const u32x4_t* pa_w = pa + b0 * 64 + lane;
         const uint32_t* pr_w = prow + b0 * 32 + ld_r;
@@ -1046,7 +1062,10 @@ __global__ __launch_bounds__(256, XSPMM_BATCH_MIN_WAVES) void spmm_f16_packed_ke
 // changes: each row's result is computed exactly as before.
 // ---------------------------------------------------------------------------
 constexpr int kOrderThreads = 1024;
-constexpr int64_t kOrderMinRows = 2048;
+#ifndef XSPMM_ORDER_MIN_ROWS
+#define XSPMM_ORDER_MIN_ROWS 2048
+#endif
+constexpr int64_t kOrderMinRows = XSPMM_ORDER_MIN_ROWS;
 constexpr int kOrderBuckets = 33;
 
 template <typename I>
@@ -1227,6 +1246,8 @@ void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int
 
 bool spmm_order_wanted(int64_t Mb) { return Mb > kOrderMinRows && Mb <= 0x7fffffffLL; }
 
+int spmm_batch_waves() { return kBW; }
+
 bool spmm_f16_pack_supported(int64_t K, int64_t Mb, int64_t Kb)
 {
     return Mb > 0 && Mb <= 0x7fffffffLL && Kb < (int64_t(1) << 20) && K < (int64_t(1) << 24);
@@ -1238,7 +1259,7 @@ void spmm_f16_pack_count(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* 
 {
     BatchPack pk{counts, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kCount>), dim3((unsigned)Mb, 1),
-                       dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
+                       dim3(64 * kBW), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
                        nullptr, nullptr, pk);
     XSPMM_LAUNCH_CHECK();
 }
@@ -1250,7 +1271,7 @@ void spmm_f16_pack_fill(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
 {
     BatchPack pk{nullptr, offsets, static_cast<u32x4_t*>(a), rows};
     hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1, BatchMode::kPack>), dim3((unsigned)Mb, 1),
-                       dim3(256), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
+                       dim3(64 * kBW), 0, s, brp, bci, bvals, nullptr, nullptr, M, K, (int64_t)16, Kb,
                        nullptr, nullptr, pk);
     XSPMM_LAUNCH_CHECK();
 }
@@ -1267,16 +1288,16 @@ bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, c
     const dim3 grid((unsigned)Mb, (unsigned)chunks);
     const u32x4_t* pa = static_cast<const u32x4_t*>(a);
     if (N <= 16)
-        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 1>), grid, dim3(256), 0, s, offsets, pa, rows,
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 1>), grid, dim3(64 * kBW), 0, s, offsets, pa, rows,
                            B, C, M, K, N, order, row_map);
     else if (N <= 32)
-        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 2>), grid, dim3(256), 0, s, offsets, pa, rows,
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 2>), grid, dim3(64 * kBW), 0, s, offsets, pa, rows,
                            B, C, M, K, N, order, row_map);
     else if (N <= 64)
-        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 4>), grid, dim3(256), 0, s, offsets, pa, rows,
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 4>), grid, dim3(64 * kBW), 0, s, offsets, pa, rows,
                            B, C, M, K, N, order, row_map);
     else
-        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 8>), grid, dim3(256), 0, s, offsets, pa, rows,
+        hipLaunchKernelGGL((spmm_f16_packed_kernel<I, 8>), grid, dim3(64 * kBW), 0, s, offsets, pa, rows,
                            B, C, M, K, N, order, row_map);
     XSPMM_LAUNCH_CHECK();
     return true;
@@ -1356,16 +1377,16 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
                 order = buf;
             }
             if (N <= 16)
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 1>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 32)
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 2>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 64)
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             else
-                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(256), 0, s, brp, bci,
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             XSPMM_LAUNCH_CHECK();
             return true;
