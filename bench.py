@@ -196,6 +196,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="templates", choices=sorted(WORKLOADS))
+    ap.add_argument("--n", type=int, default=None,
+                    help="width N of B and C (default: the workload's own N)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cluster", choices=("config", "on", "off"), default="config",
                     help="override the workload's clustering setting")
@@ -227,7 +229,7 @@ def main():
     X.load()
 
     print(f"[bench] generating {args.config}", file=sys.stderr, flush=True)
-    p = synth.CONFIGS[args.config]()
+    p = synth.CONFIGS[args.config](**({"N": args.n} if args.n else {}))
     if args.cluster != "config":
         p.cluster = args.cluster == "on"
     M, K, N, nnz = p.M, p.K, p.N, p.nnz

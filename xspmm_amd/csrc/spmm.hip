@@ -542,16 +542,20 @@ static_assert(kBW >= 2 && kBW <= 4, "2 .. 4 waves per batch workgroup");
 #ifndef XSPMM_BATCH_MIN_WAVES
 #define XSPMM_BATCH_MIN_WAVES 1
 #endif
+#ifndef XSPMM_BATCH_DEPTH_WIDE
+#define XSPMM_BATCH_DEPTH_WIDE 10
+#endif
 // A pairs in flight per wave.  At 128 columns (NT = 8) five fill the 128-VGPR
 // budget of four waves per SIMD; narrower tiles need fewer accumulator and B
 // registers and keep more pairs in flight.
-template <int NT>
+template <int NT, int NC = 1>
 constexpr int batch_depth()
 {
-    return NT >= 8 ? XSPMM_BATCH_DEPTH : XSPMM_BATCH_DEPTH_NARROW;
+    return NC > 1 ? XSPMM_BATCH_DEPTH_WIDE : (NT >= 8 ? XSPMM_BATCH_DEPTH : XSPMM_BATCH_DEPTH_NARROW);
 }
 static_assert(XSPMM_BATCH_DEPTH >= 4 && XSPMM_BATCH_DEPTH <= 10 && XSPMM_BATCH_DEPTH_NARROW >= 4 &&
-                  XSPMM_BATCH_DEPTH_NARROW <= 10,
+                  XSPMM_BATCH_DEPTH_NARROW <= 10 && XSPMM_BATCH_DEPTH_WIDE >= 4 &&
+                  XSPMM_BATCH_DEPTH_WIDE <= 10,
               "batch depth must be 4 .. 10 (the ring holds ten pairs)");
 
 // swizzle of row e: even values 0..14, each used by two of the 16 rows a
@@ -641,16 +645,26 @@ __device__ __forceinline__ constexpr uint32_t kslot(uint32_t k)
     return 16u * ((k >> 2) & 1u) + 4u * (k >> 3) + (k & 3u);
 }
 
+// NC: 128-column chunks one workgroup multiplies each batch with (1, or 2
+// for N > 128: each pair is streamed and compacted once for 256 columns).
+// The chunks' products accumulate exactly as two NC = 1 workgroups would,
+// so C does not depend on NC.  With NC = 2 every wave holds the second
+// chunk's accumulators, B rows and LDS tile, and two workgroups fit a CU.
 // (HIP's second __launch_bounds__ argument is the minimum number of waves per
-// SIMD: kBW, for four resident workgroups per CU.)
-template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply>
-__global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
+// SIMD: kBW for four resident workgroups per CU, kBW / 2 for two.)
+template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply, int NC = 1>
+__global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_batch_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
     int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map, BatchPack pk)
 {
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
-    constexpr int D = batch_depth<NT>();
+    static_assert(NC == 1 || (NC == 2 && NT == 8 && MODE == BatchMode::kMultiply),
+                  "two chunks per workgroup: 128-column chunks, multiply mode");
+    constexpr int D = batch_depth<NT, NC>();
+    // per-wave LDS: the first chunk's B tile, S^T, the slot list, then the
+    // other chunks' B tiles
+    constexpr int kWaveLds = kBatchWaveLds + (NC - 1) * kBtBytes;
     static_assert(4 * D <= kWave, "one index window per ring pass");
     constexpr int CPR = 2 * NT;    // 16-byte chunks per B row
     constexpr int RPL = 64 / CPR;  // B rows per load instruction
@@ -658,13 +672,17 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     // discard word for slot-list writes of lanes without a column: pad bytes
     // 72..75 of S^T row 0 (reads cover bytes 0..63 of each row)
     constexpr uint32_t kSlotPad = kSel + 72;
-    __shared__ __align__(16) unsigned char smem[kBW * kBatchWaveLds];
+    __shared__ __align__(16) unsigned char smem[kBW * kWaveLds];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    unsigned char* const W = smem + wave * kBatchWaveLds;
+    unsigned char* const W = smem + wave * kWaveLds;
+    // B tile of chunk c
+    auto tile = [&](int c) __attribute__((always_inline)) -> unsigned char* {
+        return c == 0 ? W : W + kBatchWaveLds + (c - 1) * kBtBytes;
+    };
 
     const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
-    const int64_t n0 = (int64_t)blockIdx.y * 128;
+    const int64_t n0 = (int64_t)blockIdx.y * 128 * NC;
     const int64_t rs = brp[br];
     const int64_t re = brp[br + 1];
     const int64_t npairs = (re - rs + 1) >> 1;
@@ -734,36 +752,43 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     for (int i = lane; i < 16 * kApStride / 4; i += kWave)
         reinterpret_cast<uint32_t*>(W + kSel)[i] = 0u;
 
-    float4_t acc[NT];
+    float4_t acc[NC][NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[c][j] = float4_t{0.f, 0.f, 0.f, 0.f};
     float4_t d0 = float4_t{0.f, 0.f, 0.f, 0.f};  // A' slots 0..15 (transposed)
     float4_t d1 = float4_t{0.f, 0.f, 0.f, 0.f};  // A' slots 16..31
 
-    u32x4_t bv[NT];
+    u32x4_t bv[NC][NT];
     half8_t aop{};
     bool started = false;
     uint32_t pending = 0;
 
-    auto finish = [&]() {
+    auto finish = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const uint32_t e = (uint32_t)(t * RPL) + ld_r;
-            *reinterpret_cast<u32x4_t*>(W + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[t];
-        }
-        // read address of tile j: tr_a0 ^ 32 j (the swizzle XORs bits 5..7,
-        // which tr_base leaves clear); recomputed here rather than kept live
-        uint32_t a0 = tr_a0;
-        asm volatile("" : "+v"(a0));
+        for (int c = 0; c < NC; ++c) {
+            unsigned char* const T = tile(c);
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t a = a0 ^ (uint32_t)(32 * j);
-            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a));
-            const short4_t hi =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(W + a + 4 * kBtRow));
-            const half8_t bop = __builtin_bit_cast(
-                half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[j], 0, 0, 0);
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+                *reinterpret_cast<u32x4_t*>(T + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[c][t];
+            }
+            // read address of tile j: tr_a0 ^ 32 j (the swizzle XORs bits
+            // 5..7, which tr_base leaves clear); recomputed here rather than
+            // kept live
+            uint32_t a0 = tr_a0;
+            asm volatile("" : "+v"(a0));
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const uint32_t a = a0 ^ (uint32_t)(32 * j);
+                const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(T + a));
+                const short4_t hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(T + a + 4 * kBtRow));
+                const half8_t bop = __builtin_bit_cast(
+                    half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc[c][j], 0, 0, 0);
+            }
         }
     };
     int64_t nbatch = 0;
@@ -772,7 +797,7 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     // Close the open batch of `cnt` slots: A' from the D registers (exact
     // fp16 values), then multiply the previous batch and issue this one's
     // B row loads in K order.
-    auto start = [&](uint32_t cnt) {
+    auto start = [&](uint32_t cnt) __attribute__((always_inline)) {
         if constexpr (MODE == BatchMode::kCount) {
             ++nbatch;
             return;
@@ -800,21 +825,24 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
             row[t] = *reinterpret_cast<const uint32_t*>(
                 W + kSlotOff + 4u * ((uint32_t)ks_r + kslot((uint32_t)(t * RPL))));
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const bool use = (ks_r < (int)cnt - (int)kslot((uint32_t)(t * RPL))) & (row[t] < k32);
-            const uint32_t at = __umul24(row[t], rowbytes) + ld_off;
-            const uint32_t off = use ? at : b_bytes + ld_off;
-            bv[t] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
-        }
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const bool use = (ks_r < (int)cnt - (int)kslot((uint32_t)(t * RPL))) & (row[t] < k32);
+                // chunk c starts 128 columns (256 bytes) after chunk c - 1
+                const uint32_t at = __umul24(row[t], rowbytes) + ld_off + 256u * (uint32_t)c;
+                const uint32_t off = use ? at : b_bytes + ld_off;
+                bv[c][t] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+            }
         started = true;
     };
 
-    auto stage_a = [&](int64_t q, half8_t& P) {
+    auto stage_a = [&](int64_t q, half8_t& P) __attribute__((always_inline)) {
         P = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(
                                             a_rsrc, (int)(a_voff + (uint32_t)q * 1024u), 0, kNonTemporal));
     };
-    auto load_cols = [&](int64_t q) -> uint32_t {
+    auto load_cols = [&](int64_t q) __attribute__((always_inline)) -> uint32_t {
         return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
             c_rsrc, (int)(cw_off + (uint32_t)q * (uint32_t)(2 * sizeof(I))), 0, 0);
     };
@@ -823,7 +851,7 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     // 16h+15) set their S^T entry before the read and clear it after; the
     // other lanes write to the pad bytes of their S^T row, which no read sees.
     const uint16_t h_one = 0x3c00u;  // fp16 1.0
-    auto round = [&](float4_t& d, bool mine, uint32_t st, const half8_t& pa) {
+    auto round = [&](float4_t& d, bool mine, uint32_t st, const half8_t& pa) __attribute__((always_inline)) {
         const uint32_t at = mine ? st : st_pad;
         *lds_ptr<uint16_t>(at) = h_one;
         const half8_t x = __builtin_bit_cast(half8_t, *lds_ptr<const u32x4_t>(st_rd));
@@ -832,7 +860,7 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     };
 
     // pair j of the ring pass whose index window is `win`
-    auto process = [&](const half8_t& pa, uint32_t win, int j) {
+    auto process = [&](const half8_t& pa, uint32_t win, int j) __attribute__((always_inline)) {
         uint32_t c0, c1;
         // this lane's block column (lane l: block l >> 5 of the pair)
         uint32_t csel;
@@ -954,7 +982,11 @@ __global__ __launch_bounds__(64 * kBW, kBW) void spmm_f16_batch_kernel(
     } else if constexpr (MODE == BatchMode::kPack) {
         return;
     } else {
-        batch_tile_store<I, NT>(acc, smem, wave, g, li, br, n0, M, N, C, row_map);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (n0 + 128 * c < N)
+                batch_tile_store<I, NT>(acc[c], smem, wave, g, li, br, n0 + 128 * c, M, N, C,
+                                        row_map);
     }
 }
 
@@ -1232,6 +1264,20 @@ Fp16Kernel fp16_kernel_choice()
     return k;
 }
 
+// Whether N > 128 takes the two-chunk batch kernel: when its grid still has
+// at least 1024 workgroups (two fit a CU, so fewer would leave CUs short of
+// waves: configs[1], 512 block-rows at N = 256, runs 7 % slower with two
+// chunks, the headline matrix at N = 256 1.43x faster).  XSPMM_BATCH_WIDE=on
+// or off forces the choice; C is the same either way.  Read on every call,
+// so a process can compare the two.
+bool wide_batches(int64_t Mb, int64_t N)
+{
+    const char* e = std::getenv("XSPMM_BATCH_WIDE");
+    if (e && std::string(e) == "on") return true;
+    if (e && std::string(e) == "off") return false;
+    return Mb * ((N + 255) / 256) >= 1024;
+}
+
 void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N)
 {
     if (M < 0 || K < 0 || Mb < 0 || Kb < 0 || nnzb < 0 || N < 0)
@@ -1385,9 +1431,13 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
             else if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
-            else
+            else if (N <= 128 || !wide_batches(Mb, N))
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
+            else  // 256 columns per workgroup: each pair compacted once for two chunks
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8, BatchMode::kMultiply, 2>),
+                                   dim3((unsigned)Mb, (unsigned)((N + 255) / 256)), dim3(64 * kBW), 0,
+                                   s, brp, bci, v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
             XSPMM_LAUNCH_CHECK();
             return true;
         }

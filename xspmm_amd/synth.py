@@ -64,13 +64,12 @@ def _csr_from_coo(M: int, r: np.ndarray, c: np.ndarray):
     return rp.astype(np.int32), c.astype(np.int32), order
 
 
-def cpu_ref(seed: int = 0) -> Problem:
+def cpu_ref(seed: int = 0, N: int = 64) -> Problem:
     """M=K=1024 fp32.  Each row draws 10 + Bernoulli(0.24) distinct columns
     uniformly without replacement (E[nnz/row] = 10.24, i.e. 1 %); columns
     sorted.  Values U(-1,1).  B is 1024x64 U(-1,1).  No clustering."""
     rng = np.random.default_rng(seed)
     M = K = 1024
-    N = 64
     rows = []
     for _ in range(M):
         k = 10 + int(rng.random() < 0.24)
