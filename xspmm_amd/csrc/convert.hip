@@ -129,12 +129,18 @@ __global__ __launch_bounds__(kThreads) void conv_count_kernel(int64_t M, int64_t
     }
 }
 
+// err (nullable): the count pass's flag; when it is set (a strip held an
+// invalid row_ptr or column) no strip writes anything, so a BCSR buffer sized
+// from the bound min(nnz, Mb * Kb) is never overrun by offsets that a
+// malformed row_ptr can produce.
 template <typename T, typename I>
 __global__ __launch_bounds__(kThreads) void conv_fill_kernel(
     int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp, const I* __restrict__ ci,
     const T* __restrict__ vals, int64_t rb, int64_t cb, int64_t nwords,
-    const I* __restrict__ brp, I* __restrict__ bci, T* __restrict__ bvals)
+    const I* __restrict__ brp, I* __restrict__ bci, T* __restrict__ bvals,
+    const int* __restrict__ err)
 {
+    if (err && *err) return;  // uniform: before any barrier
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int s_unsorted, s_bad;
     __shared__ int64_t red[kThreads / 64];
@@ -239,21 +245,35 @@ template <typename I>
 int64_t csr_to_bcsr_count(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                           int64_t rb, int64_t cb, I* brp, hipStream_t s)
 {
+    const ConvGeometry g = conv_geometry(M, K, nnz, rb, cb);  // argument checks first
+    Scratch err(sizeof(int), s);
+    csr_to_bcsr_count_async<I>(M, K, nnz, rp, ci, rb, cb, brp, err.as<int>(), s);
+    return csr_to_bcsr_result<I>(brp, g.Mb, err.as<int>(), s);
+}
+
+template <typename I>
+void csr_to_bcsr_count_async(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                             int64_t rb, int64_t cb, I* brp, int* err, hipStream_t s)
+{
     const ConvGeometry g = conv_geometry(M, K, nnz, rb, cb);
     Scratch counts((size_t)(g.Mb > 0 ? g.Mb : 1) * sizeof(I), s);
-    Scratch err(sizeof(int), s);
-    hipLaunchKernelGGL(set_value_kernel<int>, dim3(1), dim3(64), 0, s, err.as<int>(), 0);
+    hipLaunchKernelGGL(set_value_kernel<int>, dim3(1), dim3(64), 0, s, err, 0);
     XSPMM_LAUNCH_CHECK();
     if (g.Mb > 0) {
         hipLaunchKernelGGL(conv_count_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), g.count_lds,
-                           s, M, K, nnz, rp, ci, rb, cb, g.nwords, counts.as<I>(), err.as<int>());
+                           s, M, K, nnz, rp, ci, rb, cb, g.nwords, counts.as<I>(), err);
         XSPMM_LAUNCH_CHECK();
     }
     device_exclusive_scan(ArrayValue<I>{counts.as<I>()}, g.Mb, brp, s);
+}
+
+template <typename I>
+int64_t csr_to_bcsr_result(const I* brp, int64_t Mb, const int* err, hipStream_t s)
+{
     I nnzb = 0;
     int bad = 0;
-    XSPMM_HIP_CHECK(hipMemcpyAsync(&nnzb, brp + g.Mb, sizeof(I), hipMemcpyDeviceToHost, s));
-    XSPMM_HIP_CHECK(hipMemcpyAsync(&bad, err.get(), sizeof(int), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipMemcpyAsync(&nnzb, brp + Mb, sizeof(I), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipMemcpyAsync(&bad, err, sizeof(int), hipMemcpyDeviceToHost, s));
     XSPMM_HIP_CHECK(hipStreamSynchronize(s));
     if (bad)
         throw std::invalid_argument(
@@ -264,25 +284,28 @@ int64_t csr_to_bcsr_count(int64_t M, int64_t K, int64_t nnz, const I* rp, const 
 template <typename T, typename I>
 void csr_to_bcsr_fill(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                       const T* vals, int64_t rb, int64_t cb, const I* brp, I* bci, T* bvals,
-                      hipStream_t s)
+                      hipStream_t s, const int* err)
 {
     const ConvGeometry g = conv_geometry(M, K, nnz, rb, cb);
     if (g.Mb == 0) return;
     hipLaunchKernelGGL((conv_fill_kernel<T, I>), dim3((unsigned)g.Mb), dim3(kThreads), g.fill_lds,
-                       s, M, K, nnz, rp, ci, vals, rb, cb, g.nwords, brp, bci, bvals);
+                       s, M, K, nnz, rp, ci, vals, rb, cb, g.nwords, brp, bci, bvals, err);
     XSPMM_LAUNCH_CHECK();
 }
 
-template int64_t csr_to_bcsr_count<int32_t>(int64_t, int64_t, int64_t, const int32_t*,
-                                            const int32_t*, int64_t, int64_t, int32_t*,
-                                            hipStream_t);
-template int64_t csr_to_bcsr_count<int64_t>(int64_t, int64_t, int64_t, const int64_t*,
-                                            const int64_t*, int64_t, int64_t, int64_t*,
-                                            hipStream_t);
+#define XSPMM_INST_COUNT(I)                                                                      \
+    template int64_t csr_to_bcsr_count<I>(int64_t, int64_t, int64_t, const I*, const I*, int64_t, \
+                                          int64_t, I*, hipStream_t);                             \
+    template void csr_to_bcsr_count_async<I>(int64_t, int64_t, int64_t, const I*, const I*,      \
+                                             int64_t, int64_t, I*, int*, hipStream_t);           \
+    template int64_t csr_to_bcsr_result<I>(const I*, int64_t, const int*, hipStream_t);
+XSPMM_INST_COUNT(int32_t)
+XSPMM_INST_COUNT(int64_t)
+#undef XSPMM_INST_COUNT
 #define XSPMM_INST_FILL(T, I)                                                                    \
     template void csr_to_bcsr_fill<T, I>(int64_t, int64_t, int64_t, const I*, const I*,         \
                                          const T*, int64_t, int64_t, const I*, I*, T*,          \
-                                         hipStream_t);
+                                         hipStream_t, const int*);
 XSPMM_INST_FILL(uint16_t, int32_t)
 XSPMM_INST_FILL(uint16_t, int64_t)
 XSPMM_INST_FILL(float, int32_t)

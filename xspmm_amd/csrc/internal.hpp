@@ -219,10 +219,21 @@ bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t n
 template <typename I>
 int64_t csr_to_bcsr_count(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                           int64_t rb, int64_t cb, I* brp, hipStream_t s);
+// The same count without waiting: brp[Mb+1] and the device flag *err (0 for a
+// valid CSR) are written on `s`; csr_to_bcsr_result later reads nnzb and the
+// flag back (synchronizing `s`) and throws as csr_to_bcsr_count does.
+template <typename I>
+void csr_to_bcsr_count_async(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                             int64_t rb, int64_t cb, I* brp, int* err, hipStream_t s);
+template <typename I>
+int64_t csr_to_bcsr_result(const I* brp, int64_t Mb, const int* err, hipStream_t s);
+// Fill of bci[nnzb] and bvals[nnzb * rb * cb].  err (nullable): the count's
+// flag; when set the fill writes nothing (used when the outputs are sized
+// from the bound min(nnz, Mb * Kb) before nnzb is known).
 template <typename T, typename I>
 void csr_to_bcsr_fill(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                       const T* vals, int64_t rb, int64_t cb, const I* brp, I* bci, T* bvals,
-                      hipStream_t s);
+                      hipStream_t s, const int* err = nullptr);
 
 // Row permutation new row i = old row perm[i] (outputs caller-allocated).
 template <typename T, typename I>

