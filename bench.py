@@ -46,6 +46,9 @@ WORKLOADS = {
     "pruned": "configs[4]: 14336x4096 fp16, 90% pruned, N=2048, clustering off",
     "gnn": "configs[3]: 131072^2 power-law adjacency fp16, N=64, clustering on",
 }
+for _d in ("90", "50", "5", "0.5", "0.1"):
+    WORKLOADS[f"banded{_d}"] = (f"examples/05 density sweep: banded 16384^2 at {_d}% "
+                                "(bandwidth density*K/2), fp16, B = ones, N=128, Tier-1")
 
 
 def host_threads() -> int:

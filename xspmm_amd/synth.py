@@ -221,6 +221,34 @@ def banded(M: int = 1024, bandwidth: int = 8, N: int = 32, seed: int = 42,
     return Problem("banded", M, M, N, rp, ci, vals, B, cluster=False)
 
 
+# the density sweep of examples/05_core_spmm_benchmark.cpp:67-77
+SWEEP_DENSITIES = {"90": 0.90, "50": 0.50, "5": 0.05, "0.5": 0.005, "0.1": 0.001}
+
+
+def banded_sweep(density: float, M: int = 16384, N: int = 128, seed: int = 42,
+                 dtype=np.float16) -> Problem:
+    """The reference's Tier-1 density sweep (examples/05_core_spmm_benchmark.cpp:
+    56-77, :103-117): A = M x M banded, bandwidth int(density * M / 2)
+    (at least 1), every entry |i - j| <= bandwidth present with a value
+    U(0.1, 1) (utils/matrix_gen.hpp:69-90; seeded here with numpy, not the
+    reference's mt19937); B = ones, so C[i, :] is row i's sum; N = 128."""
+    bw = max(1, int(density * M / 2.0))
+    i = np.arange(M, dtype=np.int64)
+    start = np.maximum(0, i - bw)
+    end = np.minimum(M - 1, i + bw)
+    lens = end - start + 1
+    rp = np.zeros(M + 1, np.int64)
+    np.cumsum(lens, out=rp[1:])
+    nnz = int(rp[-1])
+    # column of entry e in row r: start[r] + (e - rp[r])
+    ci = (np.arange(nnz, dtype=np.int64) - np.repeat(rp[:-1] - start, lens)).astype(np.int32)
+    rng = np.random.default_rng(seed)
+    vals = rng.uniform(0.1, 1.0, size=nnz).astype(dtype)
+    B = np.ones((M, N), dtype)
+    return Problem(f"banded{density * 100:g}", M, M, N, rp.astype(np.int32), ci, vals, B,
+                   cluster=False, meta=dict(bandwidth=bw, density=density))
+
+
 def random_csr(M: int, K: int, N: int, density: float, seed: int = 0, dtype=np.float16,
                unsorted: bool = False, dup_frac: float = 0.0) -> Problem:
     """Uniform random CSR for parity tests: Binomial row lengths, optional
@@ -248,3 +276,5 @@ CONFIGS = {
     "gnn": gnn,
     "pruned": pruned,
 }
+for _name, _d in SWEEP_DENSITIES.items():
+    CONFIGS[f"banded{_name}"] = (lambda d: lambda **kw: banded_sweep(d, **kw))(_d)
