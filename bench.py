@@ -315,7 +315,8 @@ def main():
     else:
         roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": achieved / HBM_PEAK_GBS}
-    roofline.update({"traffic": load_traffic(args.config), "kernel": tier1_kernel(sT, K, N, nnzb, Mb),
+    traffic_key = args.config if args.n is None else f"{args.config}_n{args.n}"
+    roofline.update({"traffic": load_traffic(traffic_key), "kernel": tier1_kernel(sT, K, N, nnzb, Mb),
                      "alg_bytes_per_call": alg_bytes,
                      "padded_flops_per_call": 2.0 * nnzb * 256 * N})
 
