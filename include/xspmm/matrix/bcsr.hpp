@@ -49,11 +49,13 @@ public:
         : exec_(std::move(o.exec_)),
           num_block_rows_(o.num_block_rows_), num_block_cols_(o.num_block_cols_), num_blocks_(o.num_blocks_),
           r_block_(o.r_block_), c_block_(o.c_block_), num_rows_(o.num_rows_), num_cols_(o.num_cols_),
-          bcsr_row_ptr_(o.bcsr_row_ptr_), bcsr_col_ind_(o.bcsr_col_ind_), bcsr_values_(o.bcsr_values_)
+          bcsr_row_ptr_(o.bcsr_row_ptr_), bcsr_col_ind_(o.bcsr_col_ind_), bcsr_values_(o.bcsr_values_),
+          dispatch_order_(o.dispatch_order_)
     {
         o.bcsr_row_ptr_ = nullptr;
         o.bcsr_col_ind_ = nullptr;
         o.bcsr_values_ = nullptr;
+        o.dispatch_order_ = nullptr;
     }
 
     BCSRMatrix& operator=(BCSRMatrix&& o) noexcept {
@@ -70,9 +72,11 @@ public:
             bcsr_row_ptr_ = o.bcsr_row_ptr_;
             bcsr_col_ind_ = o.bcsr_col_ind_;
             bcsr_values_ = o.bcsr_values_;
+            dispatch_order_ = o.dispatch_order_;
             o.bcsr_row_ptr_ = nullptr;
             o.bcsr_col_ind_ = nullptr;
             o.bcsr_values_ = nullptr;
+            o.dispatch_order_ = nullptr;
         }
         return *this;
     }
@@ -101,9 +105,24 @@ public:
 
     std::shared_ptr<const Executor> get_executor() const { return exec_; }
 
+    // Dispatch order of the fp16 Tier-1 kernel (block-row ids, longest rows
+    // first; num_block_rows int32 entries on the executor), which csr_to_bcsr
+    // computes once for grids with many block-rows so that Tier-1 calls do
+    // not order the rows again.  Null: Tier-1 orders them on each call when
+    // it needs to.  set_dispatch_order takes ownership of an array allocated
+    // with this matrix's executor; copy_from_host drops it (the row lengths
+    // may change).
+    const int32_t* get_dispatch_order() const { return dispatch_order_; }
+    void set_dispatch_order(int32_t* order)
+    {
+        free_dispatch_order();
+        dispatch_order_ = order;
+    }
+
     void copy_from_host(const IndexType* host_row_ptr, const IndexType* host_col_ind,
                         const ValueType* host_values)
     {
+        free_dispatch_order();
         exec_->copy_from_host(bcsr_row_ptr_, host_row_ptr,
                               (static_cast<size_t>(num_block_rows_) + 1) * sizeof(IndexType));
         if (num_blocks_ > 0) {
@@ -119,8 +138,19 @@ private:
                static_cast<size_t>(c_block_) * sizeof(ValueType);
     }
 
+    void free_dispatch_order() noexcept {
+        if (exec_ && dispatch_order_) {
+            try {
+                exec_->free(dispatch_order_);
+            } catch (...) {
+            }
+        }
+        dispatch_order_ = nullptr;
+    }
+
     void release() noexcept {
         if (!exec_) return;
+        free_dispatch_order();
         try {
             if (bcsr_row_ptr_) exec_->free(bcsr_row_ptr_);
             if (bcsr_col_ind_) exec_->free(bcsr_col_ind_);
@@ -144,6 +174,7 @@ private:
     IndexType* bcsr_row_ptr_ = nullptr;
     IndexType* bcsr_col_ind_ = nullptr;
     ValueType* bcsr_values_ = nullptr;
+    int32_t* dispatch_order_ = nullptr;
 };
 
 }  // namespace xspmm

@@ -83,6 +83,34 @@ int xspmm_bcsr_spmm_noalloc(int vtype, int itype, int64_t M, int64_t K, int64_t 
 int64_t xspmm_noalloc_scratch_bytes(void);
 
 /*
+ * Dispatch order of the fp16 Tier-1 kernel for a block-row grid: when Tier-1
+ * would order this grid's rows (more than 2048 block-rows), writes the Mb
+ * block-row ids (int32, longest rows first) to `order` and sets
+ * *written = 1; otherwise writes nothing and sets *written = 0.
+ * Asynchronous on `stream`.
+ * No counterpart in the reference: Tier-1 computes this order on every call
+ * on long grids; a caller that multiplies one matrix many times computes it
+ * once (as csr_to_bcsr does for a C++ BCSRMatrix) and passes it to
+ * xspmm_bcsr_spmm_ordered.
+ */
+int xspmm_bcsr_dispatch_order(int itype, int64_t Mb, const void* brp, int32_t* order,
+                              int* written, void* stream);
+
+/*
+ * xspmm_bcsr_spmm with a dispatch order from xspmm_bcsr_dispatch_order
+ * (NULL: Tier-1 orders the rows itself, as xspmm_bcsr_spmm does).  C is the
+ * same bit for bit: the order only decides which workgroup takes which
+ * block-row.  `order` holds Mb int32 entries, a permutation of [0, Mb); an
+ * id outside [0, Mb) is skipped, and a block-row that no entry names is not
+ * written.  Asynchronous on `stream`.
+ * No counterpart in the reference (see xspmm_bcsr_dispatch_order).
+ */
+int xspmm_bcsr_spmm_ordered(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                            int64_t nnzb, const void* brp, const void* bci, const void* bvals,
+                            const void* B, float* C, int64_t N, const int32_t* order,
+                            void* stream);
+
+/*
  * CSR -> BCSR, phase 1: writes bcsr_row_ptr[Mb+1] (device) for r x c blocks,
  * Mb = ceil(M/r), and stores nnzb in *nnzb_out (host).  Synchronizes `stream`.
  * Fails with XSPMM_ERR_INVALID if a column index lies outside [0, K).

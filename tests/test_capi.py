@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     assert len(syms) >= 9
     for s in syms:
         assert hasattr(L, s), s
-    assert L.xspmm_abi_version() == 3
+    assert L.xspmm_abi_version() == 4
     assert L.xspmm_last_error() == b""
 
 

@@ -245,6 +245,62 @@ def test_spmm_many_skewed_block_rows(torch, N):
     check_c(host(C), ref, np.float16)
 
 
+@pytest.mark.parametrize("itype", [np.int32, np.int64])
+def test_spmm_cached_dispatch_order(torch, itype):
+    # Mb = 3000 > 2048: csr_to_bcsr keeps the longest-first dispatch order and
+    # Tier-1 passes it (xspmm_bcsr_spmm_ordered); C equals the C of the entry
+    # point that orders the rows on every call, bit for bit.  An order whose
+    # ids fall outside the grid skips those block-rows (their C rows stay as
+    # they were), and an in-place change of row_ptr makes the view recompute it.
+    import ctypes as C
+    rng = np.random.default_rng(5)
+    M, K, N = 48000, 4096, 64
+    deg = np.minimum((rng.pareto(1.2, M) + 1) * 3, K).astype(np.int64)
+    rows = [np.sort(rng.choice(K, size=d, replace=False)) for d in deg]
+    rp = np.zeros(M + 1, np.int64); rp[1:] = np.cumsum(deg)
+    ci = np.concatenate(rows)
+    vals = rng.uniform(-1, 1, len(ci)).astype(np.float16)
+    A = X.CSRMatrix.from_host(M, K, rp.astype(itype), ci.astype(itype), vals)
+    Bm = X.csr_to_bcsr(A)
+    order = Bm._order
+    assert order is not None and order.dtype == torch.int32
+    assert np.array_equal(np.sort(host(order)), np.arange(Bm.num_block_rows))
+    B = dev(torch, rng.standard_normal((K, N)).astype(np.float16))
+    C1 = X.spmm(Bm, B)
+    L = X.load()
+    ptr = lambda t: C.c_void_p(t.data_ptr())
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = (X.vcode(Bm.values.dtype), X.icode(Bm.row_ptr.dtype), Bm.num_rows, Bm.num_cols,
+            Bm.num_block_rows, Bm.num_block_cols, Bm.num_blocks, ptr(Bm.row_ptr),
+            ptr(Bm.col_ind), ptr(Bm.values), ptr(B))
+    C2 = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    assert L.xspmm_bcsr_spmm(*args, ptr(C2), N, stream) == X.OK
+    torch.cuda.synchronize()
+    assert torch.equal(C1, C2)
+    # ids outside [0, Mb) are skipped
+    bad = order.clone()
+    skipped = host(bad[:5]).copy()
+    bad[:5] = Bm.num_block_rows + 7
+    C3 = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    assert L.xspmm_bcsr_spmm_ordered(*args, ptr(C3), N, ptr(bad), stream) == X.OK
+    torch.cuda.synchronize()
+    lost = np.zeros(M, bool)
+    for br in skipped:
+        lost[16 * br:16 * br + 16] = True
+    C3h = host(C3)
+    assert np.all(np.isnan(C3h[lost]))
+    assert np.array_equal(C3h[~lost], host(C1)[~lost])
+    # an in-place change of row_ptr: the cached order is recomputed
+    key = Bm._order_key
+    Bm.row_ptr.add_(0)
+    assert Bm.dispatch_order() is not None and Bm._order_key != key
+    C4 = X.spmm(Bm, B)
+    torch.cuda.synchronize()
+    assert torch.equal(C4, C1)
+    ref = oracle.csr_spmm_f64(M, N, rp, ci, vals, host(B))
+    check_c(host(C1), ref, np.float16)
+
+
 def test_spmm_empty_and_odd_block_rows(torch):
     # block-rows with 0, 1, 2, 3 blocks; C must be overwritten (zeros where empty)
     rows = []

@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 
@@ -62,6 +62,11 @@ def load():
     L.xspmm_abi_version.argtypes = []
     L.xspmm_bcsr_spmm.restype = i32
     L.xspmm_bcsr_spmm.argtypes = [i32, i32, i64, i64, i64, i64, i64, p, p, p, p, p, i64, p]
+    L.xspmm_bcsr_spmm_ordered.restype = i32
+    L.xspmm_bcsr_spmm_ordered.argtypes = [i32, i32, i64, i64, i64, i64, i64, p, p, p, p, p, i64,
+                                          p, p]
+    L.xspmm_bcsr_dispatch_order.restype = i32
+    L.xspmm_bcsr_dispatch_order.argtypes = [i32, i64, p, p, C.POINTER(C.c_int), p]
     L.xspmm_csr_to_bcsr_count.restype = i32
     L.xspmm_csr_to_bcsr_count.argtypes = [i32, i64, i64, i64, p, p, i64, i64, p,
                                           C.POINTER(C.c_int64), p]
@@ -221,10 +226,33 @@ class BCSRMatrix:
     row_ptr: object   # [Mb+1]
     col_ind: object   # [nnzb]
     values: object    # [nnzb * r * c]
+    # The fp16 Tier-1 kernel's dispatch order (block-row ids, longest rows
+    # first), computed once for grids with more than 2048 block-rows and kept
+    # with the row_ptr tensor it came from (its identity and version): Tier-1
+    # would otherwise order the rows on every call.
+    _order: object = field(default=None, repr=False, compare=False)
+    _order_key: object = field(default=None, repr=False, compare=False)
 
     @property
     def num_blocks(self) -> int:
         return int(self.col_ind.numel())
+
+    def dispatch_order(self):
+        """The cached dispatch order for the current row_ptr (computed on
+        first use), or None when Tier-1 does not order this grid."""
+        key = (id(self.row_ptr), self.row_ptr.data_ptr(), self.row_ptr._version,
+               int(self.num_block_rows))
+        if self._order_key != key:
+            torch = _torch()
+            order = torch.empty(max(int(self.num_block_rows), 1), dtype=torch.int32,
+                                device=self.row_ptr.device)
+            written = C.c_int(0)
+            _check(load().xspmm_bcsr_dispatch_order(icode(self.row_ptr.dtype),
+                                                    int(self.num_block_rows), _ptr(self.row_ptr),
+                                                    _ptr(order), C.byref(written), _stream()))
+            self._order = order if written.value else None
+            self._order_key = key
+        return self._order
 
 
 # ---------------------------------------------------------------------------
@@ -250,7 +278,10 @@ def csr_to_bcsr(A: CSRMatrix, r_block: int = 16, c_block: int = 16) -> BCSRMatri
     _check(L.xspmm_csr_to_bcsr_fill(vcode(A.values.dtype), icode(it), A.num_rows, A.num_cols,
                                     A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values),
                                     r_block, c_block, _ptr(brp), _ptr(bci), _ptr(bv), _stream()))
-    return BCSRMatrix(Mb, Kb, r_block, c_block, A.num_rows, A.num_cols, brp, bci, bv)
+    out = BCSRMatrix(Mb, Kb, r_block, c_block, A.num_rows, A.num_cols, brp, bci, bv)
+    if A.values.dtype == torch.float16 and r_block == 16 and c_block == 16:
+        out.dispatch_order()  # once here rather than in every Tier-1 call
+    return out
 
 
 def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
@@ -265,9 +296,12 @@ def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
         C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=dev)
     _check_dense(B, "B", A.num_cols, N, A.values.dtype, dev)
     _check_dense(C_out, "C_out", A.num_rows, N, torch.float32, dev)
-    _check(L.xspmm_bcsr_spmm(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows, A.num_cols,
-                             A.num_block_rows, A.num_block_cols, A.num_blocks, _ptr(A.row_ptr),
-                             _ptr(A.col_ind), _ptr(A.values), _ptr(B), _ptr(C_out), N, _stream()))
+    order = A.dispatch_order() if B.dtype == torch.float16 else None
+    _check(L.xspmm_bcsr_spmm_ordered(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows,
+                                     A.num_cols, A.num_block_rows, A.num_block_cols, A.num_blocks,
+                                     _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values), _ptr(B),
+                                     _ptr(C_out), N, _ptr(order) if order is not None else None,
+                                     _stream()))
     return C_out
 
 

@@ -165,10 +165,10 @@ void spmm(const BCSRMatrix<InputType, IndexType>& A, const InputType* B, OutputT
         if (A.get_r_block() != 16 || A.get_c_block() != 16)
             throw std::invalid_argument("xSpMM: the MFMA tile kernel requires 16x16 blocks.");
         use_device(h);
-        detail::bcsr_spmm<dev_t<InputType>, IndexType>(
+        (void)detail::bcsr_spmm_ex<dev_t<InputType>, IndexType>(
             A.get_num_rows(), A.get_num_cols(), A.get_num_block_rows(), A.get_num_block_cols(),
             A.get_num_blocks(), A.get_bcsr_row_ptr(), A.get_bcsr_col_ind(), dev(A.get_bcsr_values()),
-            dev(B), C, N, kStream);
+            dev(B), C, N, A.get_dispatch_order(), nullptr, kStream);
         return;
     }
     throw std::runtime_error("xSpMM: CPU SpMM fallback is not yet implemented. Please use a GPU Executor.");
@@ -282,6 +282,13 @@ BCSRMatrix<ValueType, IndexType> csr_to_bcsr(std::shared_ptr<const Executor> tar
         detail::csr_to_bcsr_fill<dev_t<ValueType>, IndexType>(
             M, K, nnz, src.d_rp, src.d_ci, dev(src.d_vals), r_block, c_block, brp.as<IndexType>(),
             out.get_bcsr_col_ind(), dev(out.get_bcsr_values()), kStream);
+        // the fp16 Tier-1 kernel's dispatch order, once (see BCSRMatrix)
+        if (sizeof(ValueType) == 2 && r_block == 16 && c_block == 16 && detail::spmm_order_wanted(Mb)) {
+            int32_t* order = nullptr;
+            target_exec->allocate(reinterpret_cast<void**>(&order), (size_t)Mb * sizeof(int32_t));
+            detail::spmm_dispatch_order<IndexType>(out.get_bcsr_row_ptr(), Mb, order, kStream);
+            out.set_dispatch_order(order);
+        }
     } else {
         // GPU-resident input, host target: convert on the GPU, then copy down.
         detail::Scratch bci((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(IndexType), kStream);

@@ -86,7 +86,7 @@ extern "C" {
 
 const char* xspmm_last_error(void) { return g_last_error.c_str(); }
 
-int xspmm_abi_version(void) { return 3; }
+int xspmm_abi_version(void) { return 4; }
 
 int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
                     int64_t nnzb, const void* brp, const void* bci, const void* bvals,
@@ -119,6 +119,39 @@ int xspmm_bcsr_spmm_noalloc(int vtype, int itype, int64_t M, int64_t K, int64_t 
 }
 
 int64_t xspmm_noalloc_scratch_bytes(void) { return (int64_t)kNoAllocScratchBytes; }
+
+int xspmm_bcsr_dispatch_order(int itype, int64_t Mb, const void* brp, int32_t* order,
+                              int* written, void* stream)
+{
+    return guarded([&] {
+        if (Mb < 0) throw std::invalid_argument("xSpMM: negative number of block-rows.");
+        if (!written) throw std::invalid_argument("xSpMM: written must not be NULL.");
+        *written = 0;
+        if (!spmm_order_wanted(Mb)) return;
+        if (!brp || !order) throw std::invalid_argument("xSpMM: brp and order must not be NULL.");
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            spmm_dispatch_order<I>(static_cast<const I*>(brp), Mb, order, as_stream(stream));
+        });
+        *written = 1;
+    });
+}
+
+int xspmm_bcsr_spmm_ordered(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                            int64_t nnzb, const void* brp, const void* bci, const void* bvals,
+                            const void* B, float* C, int64_t N, const int32_t* order, void* stream)
+{
+    return guarded([&] {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
+            using I = typename decltype(ti)::type;
+            (void)bcsr_spmm_ex<T, I>(M, K, Mb, Kb, nnzb, static_cast<const I*>(brp),
+                                     static_cast<const I*>(bci), static_cast<const T*>(bvals),
+                                     static_cast<const T*>(B), C, N, order, nullptr,
+                                     as_stream(stream));
+        });
+    });
+}
 
 int xspmm_csr_to_bcsr_count(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
                             const void* ci, int64_t r_block, int64_t c_block,

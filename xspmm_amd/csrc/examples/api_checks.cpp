@@ -236,6 +236,56 @@ void check_ragged_n(std::shared_ptr<const xspmm::Executor> ex, const char* tname
     report(std::string("ragged N banded ") + tname, ok, worst);
 }
 
+// A grid of more than 2048 block-rows: csr_to_bcsr computes the fp16 Tier-1
+// dispatch order once (the matrix owns it, a move hands it over); Tier-1 C
+// with it equals C from the same blocks without it (copy_from_host drops the
+// order, so that call orders the rows itself), and the row sums.
+template <typename I>
+void check_dispatch_order(std::shared_ptr<const xspmm::Executor> ex, const char* tname)
+{
+    const I M = 40000, N = 64;
+    auto h = banded<I>(M, 20, 5);
+    std::vector<__half> hv;
+    auto A = upload<__half, I>(ex, h, hv);
+    auto Ab = xspmm::csr_to_bcsr(ex, A, (I)16, (I)16);
+    bool ok = Ab.get_dispatch_order() != nullptr;
+    auto Am = std::move(Ab);
+    ok = ok && Am.get_dispatch_order() != nullptr && Ab.get_dispatch_order() == nullptr;
+    const I Mb = Am.get_num_block_rows(), nnzb = Am.get_num_blocks();
+    std::vector<I> brp((size_t)Mb + 1), bci((size_t)nnzb);
+    std::vector<__half> bv((size_t)nnzb * 256);
+    ex->copy_to_host(brp.data(), Am.get_bcsr_row_ptr(), sizeof(I) * brp.size());
+    ex->copy_to_host(bci.data(), Am.get_bcsr_col_ind(), sizeof(I) * bci.size());
+    ex->copy_to_host(bv.data(), Am.get_bcsr_values(), sizeof(__half) * bv.size());
+    xspmm::BCSRMatrix<__half, I> Ac(ex, Mb, Am.get_num_block_cols(), nnzb, 16, 16);
+    Ac.set_shape(M, M);
+    Ac.copy_from_host(brp.data(), bci.data(), bv.data());
+    ok = ok && Ac.get_dispatch_order() == nullptr;
+    std::vector<__half> hB((size_t)M * N, __half(1.0f));
+    __half* d_B = nullptr;
+    float *d_C1 = nullptr, *d_C2 = nullptr;
+    ex->allocate(reinterpret_cast<void**>(&d_B), sizeof(__half) * hB.size());
+    ex->allocate(reinterpret_cast<void**>(&d_C1), sizeof(float) * (size_t)M * N);
+    ex->allocate(reinterpret_cast<void**>(&d_C2), sizeof(float) * (size_t)M * N);
+    ex->copy_from_host(d_B, hB.data(), sizeof(__half) * hB.size());
+    xspmm::spmm(Am, d_B, d_C1, N);
+    xspmm::spmm(Ac, d_B, d_C2, N);
+    ex->synchronize();
+    std::vector<float> C1((size_t)M * N), C2((size_t)M * N);
+    ex->copy_to_host(C1.data(), d_C1, sizeof(float) * C1.size());
+    ex->copy_to_host(C2.data(), d_C2, sizeof(float) * C2.size());
+    ex->free(d_B);
+    ex->free(d_C1);
+    ex->free(d_C2);
+    ok = ok && std::memcmp(C1.data(), C2.data(), sizeof(float) * C1.size()) == 0;
+    std::vector<double> rs((size_t)M, 0.0);
+    for (I r = 0; r < M; ++r)
+        for (I k = h.rp[(size_t)r]; k < h.rp[(size_t)r + 1]; ++k) rs[(size_t)r] += (float)hv[(size_t)k];
+    const double rf = rel_frob_vs_rowsums(C1, rs, (size_t)N);
+    report(std::string("cached dispatch order ") + tname, ok && rf < 1e-5,
+           "rel_frob " + std::to_string(rf));
+}
+
 // CPU and GPU conversions of the same matrix agree bit for bit.
 template <typename I>
 void check_cpu_gpu_conversion(std::shared_ptr<const xspmm::Executor> gpu)
@@ -361,6 +411,8 @@ int main()
         check_tier2<__half, int64_t>(ex, false, "f16/i64");
         check_ragged_n<float, int32_t>(ex, "f32/i32");
         check_ragged_n<__half, int32_t>(ex, "f16/i32");
+        check_dispatch_order<int32_t>(ex, "i32");
+        check_dispatch_order<int64_t>(ex, "i64");
         check_cpu_gpu_conversion<int32_t>(ex);
         check_cpu_gpu_conversion<int64_t>(ex);
         check_errors(ex);

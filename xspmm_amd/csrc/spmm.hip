@@ -682,6 +682,9 @@ __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_ba
     };
 
     const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    // a caller-supplied order holds a permutation of the block-rows; an id
+    // outside the grid is skipped rather than read past row_ptr
+    if ((uint64_t)br >= (uint64_t)gridDim.x) return;
     const int64_t n0 = (int64_t)blockIdx.y * 128 * NC;
     const int64_t rs = brp[br];
     const int64_t re = brp[br + 1];
@@ -1014,6 +1017,9 @@ __global__ __launch_bounds__(64 * kBW, XSPMM_BATCH_MIN_WAVES) void spmm_f16_pack
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     unsigned char* const W = smem + wave * kBtBytes;
     const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    // a caller-supplied order holds a permutation of the block-rows; an id
+    // outside the grid is skipped rather than read past row_ptr
+    if ((uint64_t)br >= (uint64_t)gridDim.x) return;
     const int64_t n0 = (int64_t)blockIdx.y * 128;
     const int li = lane & 15;
     const int g = lane >> 4;
