@@ -553,6 +553,56 @@ constexpr int batch_depth()
 {
     return NC > 1 ? XSPMM_BATCH_DEPTH_WIDE : (NT >= 8 ? XSPMM_BATCH_DEPTH : XSPMM_BATCH_DEPTH_NARROW);
 }
+// Wave priority by remaining work.  A SIMD issues from its oldest ready wave
+// first, so of the four workgroups sharing a CU the one dispatched first runs
+// fastest and the last one slowest: on equal block-rows (the templates
+// workload) they ended 59.6, 64.8, 71.1 and 77.0 us in dispatch order while
+// the CU idled the early finishers' slots.  Each wave sets its priority
+// (s_setprio) from the work it has left -- ring passes in the batch kernel,
+// batches in the packed kernel: more than T3 gives 3, more than T2 gives 2,
+// more than T1 gives 1, else 0 -- so the waves furthest from done issue
+// first and the CU's workgroups end close together.  Scheduling only: no
+// operand or summation order changes.
+#ifndef XSPMM_BATCH_PRIO
+#define XSPMM_BATCH_PRIO 1
+#endif
+#ifndef XSPMM_BATCH_PRIO_T3
+#define XSPMM_BATCH_PRIO_T3 12
+#endif
+#ifndef XSPMM_BATCH_PRIO_T2
+#define XSPMM_BATCH_PRIO_T2 6
+#endif
+#ifndef XSPMM_BATCH_PRIO_T1
+#define XSPMM_BATCH_PRIO_T1 2
+#endif
+#ifndef XSPMM_PACKED_PRIO
+#define XSPMM_PACKED_PRIO 1
+#endif
+#ifndef XSPMM_PACKED_PRIO_T3
+#define XSPMM_PACKED_PRIO_T3 8
+#endif
+#ifndef XSPMM_PACKED_PRIO_T2
+#define XSPMM_PACKED_PRIO_T2 4
+#endif
+#ifndef XSPMM_PACKED_PRIO_T1
+#define XSPMM_PACKED_PRIO_T1 2
+#endif
+constexpr bool kBatchPrio = XSPMM_BATCH_PRIO != 0;
+constexpr bool kPackedPrio = XSPMM_PACKED_PRIO != 0;
+// the level for `rem` units of work left under thresholds t3 > t2 > t1
+__device__ __forceinline__ int prio_level(int64_t rem, int t3, int t2, int t1)
+{
+    return rem > t3 ? 3 : rem > t2 ? 2 : rem > t1 ? 1 : 0;
+}
+__device__ __forceinline__ void set_wave_prio(int level)
+{
+    switch (level) {
+    case 3: __builtin_amdgcn_s_setprio(3); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    default: __builtin_amdgcn_s_setprio(0); break;
+    }
+}
 static_assert(XSPMM_BATCH_DEPTH >= 4 && XSPMM_BATCH_DEPTH <= 10 && XSPMM_BATCH_DEPTH_NARROW >= 4 &&
                   XSPMM_BATCH_DEPTH_NARROW <= 10 && XSPMM_BATCH_DEPTH_WIDE >= 4 &&
                   XSPMM_BATCH_DEPTH_WIDE <= 10,
@@ -937,7 +987,20 @@ __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_ba
         if constexpr (D > 7) stage_a(q0 + 7 * S, P7);
         if constexpr (D > 8) stage_a(q0 + 8 * S, P8);
         if constexpr (D > 9) stage_a(q0 + 9 * S, P9);
+        // this wave's ring passes
+        const int64_t passes = ((npairs - q0 + S - 1) / S + D - 1) / D;
+        int64_t pass = 0;
+        int level = -1;
         for (int64_t q = q0; q < npairs; q += A) {
+            if constexpr (kBatchPrio) {
+                const int lv = prio_level(passes - pass, XSPMM_BATCH_PRIO_T3, XSPMM_BATCH_PRIO_T2,
+                                          XSPMM_BATCH_PRIO_T1);
+                if (lv != level) {
+                    level = lv;
+                    set_wave_prio(lv);
+                }
+                ++pass;
+            }
             // next pass's window, issued a pass ahead like the A loads
             const uint32_t nwin = load_cols(q + A);
             process(P0, win, 0);
@@ -1058,7 +1121,16 @@ __global__ __launch_bounds__(64 * kBW, XSPMM_BATCH_MIN_WAVES) void spmm_f16_pack
 #pragma unroll
             for (int t = 0; t < NT; ++t) row[t] = pr_w[nx * 32 + t * RPL];
         }
+        int level = -1;
         for (int bi = 0; bi < nb; ++bi) {
+            if constexpr (kPackedPrio) {
+                const int lv = prio_level(nb - bi, XSPMM_PACKED_PRIO_T3, XSPMM_PACKED_PRIO_T2,
+                                          XSPMM_PACKED_PRIO_T1);
+                if (lv != level) {
+                    level = lv;
+                    set_wave_prio(lv);
+                }
+            }
             const bool more = bi + 1 < nb;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
