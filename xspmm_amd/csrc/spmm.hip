@@ -542,6 +542,14 @@ static_assert(kBW >= 2 && kBW <= 4, "2 .. 4 waves per batch workgroup");
 #ifndef XSPMM_BATCH_MIN_WAVES
 #define XSPMM_BATCH_MIN_WAVES 1
 #endif
+// B rows of a batch go straight from memory into the wave's LDS tile
+// (buffer_load ... lds) at 128-column tiles, instead of through 32 VGPRs
+// and ds_write_b128 (0 selects the register path)
+#ifndef XSPMM_BATCH_DMA
+#define XSPMM_BATCH_DMA 1
+#endif
+constexpr bool kBatchDma = XSPMM_BATCH_DMA != 0;
+typedef __attribute__((address_space(3))) void lds_void_t;
 #ifndef XSPMM_BATCH_DEPTH_WIDE
 #define XSPMM_BATCH_DEPTH_WIDE 10
 #endif
@@ -711,6 +719,10 @@ __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_ba
     static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "NT must be a power of two <= 8");
     static_assert(NC == 1 || (NC == 2 && NT == 8 && MODE == BatchMode::kMultiply),
                   "two chunks per workgroup: 128-column chunks, multiply mode");
+    // B rows straight into the LDS tile at 128-column tiles, where one load
+    // covers four whole tile rows (narrower tiles use half of each 256-byte
+    // row and keep the register path)
+    constexpr bool kDma = kBatchDma && NT == 8 && MODE == BatchMode::kMultiply;
     constexpr int D = batch_depth<NT, NC>();
     // per-wave LDS: the first chunk's B tile, S^T, the slot list, then the
     // other chunks' B tiles
@@ -822,10 +834,12 @@ __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_ba
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             unsigned char* const T = tile(c);
+            if constexpr (!kDma) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const uint32_t e = (uint32_t)(t * RPL) + ld_r;
-                *reinterpret_cast<u32x4_t*>(T + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[c][t];
+                for (int t = 0; t < NT; ++t) {
+                    const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+                    *reinterpret_cast<u32x4_t*>(T + e * kBtRow + ((ld_c ^ bt_swz(e)) << 4)) = bv[c][t];
+                }
             }
             // read address of tile j: tr_a0 ^ 32 j (the swizzle XORs bits
             // 5..7, which tr_base leaves clear); recomputed here rather than
@@ -877,16 +891,30 @@ __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_ba
         for (int t = 0; t < NT; ++t)
             row[t] = *reinterpret_cast<const uint32_t*>(
                 W + kSlotOff + 4u * ((uint32_t)ks_r + kslot((uint32_t)(t * RPL))));
+        // the tile's transposed reads (finish) complete before loads rewrite it
+        if constexpr (kDma) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const bool use = (ks_r < (int)cnt - (int)kslot((uint32_t)(t * RPL))) & (row[t] < k32);
-                // chunk c starts 128 columns (256 bytes) after chunk c - 1
-                const uint32_t at = __umul24(row[t], rowbytes) + ld_off + 256u * (uint32_t)c;
-                const uint32_t off = use ? at : b_bytes + ld_off;
-                bv[c][t] = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+                if constexpr (kDma) {
+                    // load t fills tile bytes [1024 t, 1024 t + 1024) lane by
+                    // lane: lane l writes position l % 16 of tile row
+                    // 4 t + l / 16, which holds chunk position ^ swizzle
+                    const uint32_t e = (uint32_t)(t * RPL) + ld_r;
+                    const uint32_t at = __umul24(row[t], rowbytes) + (uint32_t)(2 * n0) +
+                                        16u * (ld_c ^ bt_swz(e)) + 256u * (uint32_t)c;
+                    const uint32_t off = use ? at : b_bytes + ld_off;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_void_t*)(tile(c) + t * 1024),
+                                                             16, (int)off, 0, 0, 0);
+                } else {
+                    // chunk c starts 128 columns (256 bytes) after chunk c - 1
+                    const uint32_t at = __umul24(row[t], rowbytes) + ld_off + 256u * (uint32_t)c;
+                    const uint32_t off = use ? at : b_bytes + ld_off;
+                    bv[c][t] = __builtin_bit_cast(
+                        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+                }
             }
         started = true;
     };
