@@ -1,0 +1,28 @@
+"""GPU: the direct-to-LDS load properties the batch kernel relies on when it
+loads a batch's B rows straight into its LDS tile (xspmm_amd/csrc/spmm.hip,
+start of a batch): lane l of `buffer_load_dwordx4 ... lds` writes its 16 bytes
+at LDS offset 16 l of the 1 KB the load fills, and a lane whose offset lies past
+the buffer resource's size writes zeros.  xspmm_amd/bin/lds_dma_probe checks
+both on one wave with every access in bounds."""
+from __future__ import annotations
+
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+PROG = os.path.join(ROOT, "xspmm_amd", "bin", "lds_dma_probe")
+
+
+def test_lds_dma_layout_and_zero_fill():
+    if not os.path.exists(PROG):
+        pytest.fail(f"{PROG} is not built (make -C xspmm_amd/csrc examples)")
+    print("running", PROG, flush=True)
+    out = subprocess.run([PROG], capture_output=True, text=True, timeout=120)
+    print(out.stdout)
+    print(out.stderr)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "lds dma probe ok" in out.stdout
