@@ -499,11 +499,16 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
 //   4. when a pair does not fit, closes the batch: converts D to the fp16 A'
 //      operand, multiplies the previous batch, and issues the 16-byte loads
 //      of this batch's B rows (unused slots get an out-of-range offset, which
-//      reads zeros without touching memory);
-//   5. one batch later (the row loads have long arrived) writes those rows
-//      row-major into an XOR-swizzled LDS tile, reads them back with the
+//      reads zeros without touching memory).  At 128-column tiles the loads
+//      go straight into the wave's XOR-swizzled LDS tile (buffer_load ...
+//      lds: lane l of load t fetches the chunk the swizzle puts at position
+//      l % 16 of tile row 4 t + l / 16); narrower tiles load into registers;
+//   5. one batch later (the row loads have long arrived; narrower tiles
+//      first write their rows into the tile) reads the tile back with the
 //      gfx950 transpose read ds_read_b64_tr_b16 as MFMA B operands and issues
 //      one v_mfma_f32_16x16x32_f16 per 16-column tile.
+//   Each wave sets its issue priority from the ring passes it has left, so
+//   that the workgroups sharing a CU end together (see kBatchPrio).
 // A' carries, in MFMA K position k of lane group g (k = 8g .. 8g+7), slot
 // kslot(k) = 16 ((k >> 2) & 1) + 4 (k >> 3) + (k & 3); tile row k holds that
 // slot's B row.  Columns that are zero in all 16 rows of a block are skipped:
