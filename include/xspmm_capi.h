@@ -49,7 +49,11 @@ int xspmm_abi_version(void);
  * A has 16x16 blocks: brp[Mb+1], bci[nnzb], bvals[nnzb*256] (row-major
  * blocks).  M <= 16*Mb and K <= 16*Kb are the element shape; rows of C
  * beyond M are not written and B rows beyond K are not read.  C is
- * overwritten.  Asynchronous on `stream`.
+ * overwritten.  bvals (and B when it is fp16) must start on a 16-byte
+ * boundary: the kernels read them 16 bytes at a time, and a pointer off that
+ * boundary fails with XSPMM_ERR_INVALID before anything is launched (the
+ * same holds for the entry points below that take them).  Asynchronous on
+ * `stream`.
  * Replaces xspmm::spmm(const BCSRMatrix<In, Idx>&, const In* B, Out* C, Idx N)
  * (reference include/xspmm/xspmm.hpp:14-18, src/hip/unstructured_mtx_mul.hip:108-146).
  */

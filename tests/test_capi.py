@@ -64,6 +64,25 @@ def test_negative_and_inconsistent_sizes_are_rejected_without_gpu():
     assert b"hw_block_size" in L.xspmm_last_error()
 
 
+def test_misaligned_operands_are_rejected_without_gpu():
+    # the kernels read the block values (and fp16 B) 16 bytes at a time; a
+    # pointer off a 16-byte boundary is refused before anything is launched
+    # (the addresses below are never dereferenced)
+    L = X.load()
+    L.xspmm_bcsr_spmm_noalloc.restype = C.c_int
+    L.xspmm_bcsr_spmm_noalloc.argtypes = L.xspmm_bcsr_spmm.argtypes
+    for entry in (L.xspmm_bcsr_spmm, L.xspmm_bcsr_spmm_noalloc):
+        for vt in (X.F16, X.F32):
+            rc = entry(vt, X.I32, 16, 16, 1, 1, 1, 0x1000, 0x2000, 0x3008, 0x4000, 0x5000, 16, None)
+            assert rc == X.ERR_INVALID, (entry, vt)
+            assert b"block values must be 16-byte aligned" in L.xspmm_last_error()
+        rc = entry(X.F16, X.I64, 16, 16, 1, 1, 1, 0x1000, 0x2000, 0x3000, 0x4002, 0x5000, 16, None)
+        assert rc == X.ERR_INVALID and b"fp16 B must be 16-byte aligned" in L.xspmm_last_error()
+    rc = L.xspmm_bcsr_spmm_ordered(X.F16, X.I32, 16, 16, 1, 1, 1, 0x1000, 0x2000, 0x3000, 0x4008,
+                                   0x5000, 16, None, None)
+    assert rc == X.ERR_INVALID and b"fp16 B must be 16-byte aligned" in L.xspmm_last_error()
+
+
 def test_noalloc_entry_point_argument_errors_without_gpu():
     # type codes and sizes are checked before the scratch array is looked up
     L = X.load()

@@ -338,6 +338,14 @@ def test_dense_operands_rejected_before_launch(torch):
         (B[:-1], ValueError),                                     # fewer than K rows
         (torch.as_tensor(p.B.T.copy()).cuda().t(), ValueError),  # transposed view
     ]
+    if B.dtype == torch.float16:
+        # a contiguous view that starts 2 bytes into its allocation: the
+        # kernels read fp16 B rows 16 bytes at a time
+        flat = torch.zeros(p.K * p.N + 8, dtype=torch.float16, device="cuda")
+        off = flat[1:1 + p.K * p.N].view(p.K, p.N)
+        off.copy_(B)
+        assert off.is_contiguous() and off.data_ptr() % 16 == 2
+        bad_B.append((off, ValueError))
     for b, err in bad_B:
         with pytest.raises(err):
             X.spmm(Bm, b, C, p.N)
@@ -357,6 +365,9 @@ def test_dense_operands_rejected_before_launch(torch):
     plan = X.SpMMPlan(A)
     with pytest.raises(ValueError):
         plan.execute(B[:-1], C, p.N)
+    if B.dtype == torch.float16:
+        with pytest.raises(ValueError):
+            plan.execute(off, C, p.N)
     with pytest.raises(ValueError):
         plan.execute(B, C[:, :-1], p.N)
     plan.close()

@@ -164,7 +164,8 @@ def _device(dev=None):
 def _check_dense(t, name, rows, cols, dtype, device):
     """Reject a dense operand the kernels cannot take as given: the kernels
     read `rows` x `cols` elements row-major (ld = cols) from t.data_ptr() on
-    `device`.  Raised before any kernel is launched."""
+    `device`, and read fp16 B with 16-byte vector loads, so an fp16 B must
+    start on a 16-byte boundary.  Raised before any kernel is launched."""
     torch = _torch()
     if not torch.is_tensor(t):
         raise TypeError(f"{name} must be a torch tensor")
@@ -181,6 +182,8 @@ def _check_dense(t, name, rows, cols, dtype, device):
         ok = t.dim() == 1 and t.numel() == rows * cols
     if not ok:
         raise ValueError(f"{name} has shape {shape}, expected ({rows}, {cols})")
+    if name == "B" and dtype == torch.float16 and t.data_ptr() % 16 != 0:
+        raise ValueError(f"{name} must start on a 16-byte boundary (fp16 rows are read 16 bytes at a time)")
 
 
 # ---------------------------------------------------------------------------

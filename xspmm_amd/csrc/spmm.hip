@@ -1399,6 +1399,17 @@ void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int
         throw std::invalid_argument("xSpMM: too many block-rows for one launch.");
 }
 
+// The kernels read the block values, and fp16 B rows, with 16-byte vector
+// loads (fp16 B also straight into LDS); a pointer off a 16-byte boundary (a
+// tensor view starting mid-row, for instance) is rejected before any launch.
+void check_alignment(const void* bvals, const void* B, bool b_vector)
+{
+    if ((reinterpret_cast<uintptr_t>(bvals) & 15) != 0)
+        throw std::invalid_argument("xSpMM: the block values must be 16-byte aligned.");
+    if (b_vector && (reinterpret_cast<uintptr_t>(B) & 15) != 0)
+        throw std::invalid_argument("xSpMM: fp16 B must be 16-byte aligned.");
+}
+
 }  // namespace
 
 bool spmm_order_wanted(int64_t Mb) { return Mb > kOrderMinRows && Mb <= 0x7fffffffLL; }
@@ -1439,6 +1450,7 @@ bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, c
                      const int32_t* order, const I* row_map, hipStream_t s)
 {
     if (M == 0 || N == 0 || Mb == 0) return true;
+    check_alignment(a, B, true);
     if (N % 8 != 0 || K * N * 2 > (int64_t(1) << 31) || N >= (int64_t(1) << 22)) return false;
     const int64_t chunks = (N + 127) / 128;
     if (chunks > 65535) return false;
@@ -1502,6 +1514,7 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
 {
     check_shape(M, K, Mb, Kb, nnzb, N);
     if (M == 0 || N == 0 || Mb == 0) return true;
+    check_alignment(bvals, B, sizeof(T) == 2);
     const int64_t ntiles64 = (N + 15) / 16;
     if (ntiles64 > (1 << 24)) throw std::invalid_argument("xSpMM: N too large.");
     const int ntiles = (int)ntiles64;
@@ -1676,6 +1689,7 @@ void bcsr_spmm_noalloc(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnz
                        hipStream_t s)
 {
     check_shape(M, K, Mb, Kb, nnzb, N);
+    if (M > 0 && N > 0 && Mb > 0) check_alignment(bvals, B, sizeof(T) == 2);
     int dev = 0;
     XSPMM_HIP_CHECK(hipGetDevice(&dev));
     TempArena arena(noalloc_scratch(dev), kNoAllocScratchBytes, s);
