@@ -21,7 +21,10 @@ input handling.
     tile-kernel product (reference src/common/spmm_math.hpp:68-114 sums a
     row's blocks in stored order).
   * dense operands the kernels cannot take (wrong device, shape, dtype, a
-    transposed view) are rejected before any kernel runs.
+    transposed view, an fp16 B off a 16-byte boundary) are rejected before
+    any kernel runs; a C that starts 4 bytes into its allocation is taken
+    (the batch, GEMM-tiled, fp32 and pipeline paths store into it the same
+    values as into an aligned C).
 """
 from __future__ import annotations
 
@@ -377,3 +380,40 @@ def test_dense_operands_rejected_before_launch(torch):
         X.unpermute_dense_matrix(C, torch.arange(p.M - 1, device="cuda"))
     torch.cuda.synchronize()
     assert bool(torch.all(C == sentinel))
+
+
+def c_view_off_by_one(torch, M, N):
+    """A contiguous M x N fp32 C that starts 4 bytes into its allocation."""
+    flat = torch.full((M * N + 4,), float("nan"), dtype=torch.float32, device="cuda")
+    C = flat[1:1 + M * N].view(M, N)
+    assert C.is_contiguous() and C.data_ptr() % 16 == 4
+    return C
+
+
+@pytest.mark.parametrize("path", ["batch", "dense", "fp32", "pipeline"])
+def test_c_off_a_16_byte_boundary(torch, path):
+    """C may be any contiguous view; its vector stores fall back to scalar ones
+    when C does not start on a 16-byte boundary (same result as an aligned C)."""
+    if path == "dense":
+        M, K, N = 130, 47, 72
+        _, Bm, Bh = full_grid(torch, M, K, N, np.int32, 5)
+        A = None
+    else:
+        dtype = np.float32 if path == "fp32" else np.float16
+        p = synth.random_csr(200, 144, 128, 0.05, seed=11, dtype=dtype)
+        M, K, N, Bh = p.M, p.K, p.N, p.B
+        A = X.CSRMatrix.from_host(M, K, p.rp, p.ci, p.vals)
+        Bm = X.csr_to_bcsr(A)
+    B = torch.as_tensor(Bh).cuda()
+    Ca = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    Cm = c_view_off_by_one(torch, M, N)
+    if path == "pipeline":
+        X.spmm_pipeline(A, B, Ca, N, optimize_pattern=True, timings=False)
+        X.spmm_pipeline(A, B, Cm, N, optimize_pattern=True, timings=False)
+    else:
+        X.spmm(Bm, B, Ca, N)
+        X.spmm(Bm, B, Cm, N)
+    torch.cuda.synchronize()
+    note(f"C off a 16-byte boundary, {path}: M={M} N={N}")
+    assert np.all(np.isfinite(host(Ca)))
+    assert np.array_equal(host(Ca), host(Cm))

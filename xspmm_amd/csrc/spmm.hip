@@ -459,7 +459,7 @@ __global__ __launch_bounds__(256) void spmm_f16_gather_kernel(const I* __restric
             out[e] = red[o] + red[2048 + o] + red[4096 + o] + red[6144 + o];
         }
         float* dst = C + grow * N + n0 + c0;
-        if (n0 + c0 + 8 <= N && (N & 3) == 0) {
+        if (n0 + c0 + 8 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
             *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
             *reinterpret_cast<float4*>(dst + 4) = make_float4(out[4], out[5], out[6], out[7]);
         } else {

@@ -432,7 +432,8 @@ __global__ __launch_bounds__(kDThreads, XSPMM_DENSE_MINW) void spmm_f16_dense_ke
                 const float4_t v = *reinterpret_cast<const float4_t*>(T + row_l * TS + c);
                 const int64_t col = n0 + c;
                 if (row < M && col < N) {
-                    if (col + 4 <= N && (N & 3) == 0)
+                    // 16-byte stores only where C's rows stay 16-byte aligned
+                    if (col + 4 <= N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0)
                         __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(C + crow * N + col));
                     else
                         for (int e = 0; e < 4 && col + e < N; ++e) C[crow * N + col + e] = v[e];
