@@ -7,6 +7,10 @@ The permutation must equal the reference's bit for bit:
     forced and with the automatic choice;
   * against the oracle's greedy on seeded random, template-like, skewed and
     empty-row inputs, int32 and int64, both engines;
+  * both with the partner lists (all pairs on the int8 matrix cores by
+    default, or by VALU popcounts with XSPMM_CLUSTER_PARTNERS=popcount) and
+    without them (XSPMM_CLUSTER_PARTNERS=off), and with both partner passes
+    at row bitmaps of 1 to 32 words;
   * at the headline size (templates, 16384 rows) against the oracle, and on
     the 131072-row power-law graph against the product's host engine (the
     oracle's scan would take minutes there; the host engine is pinned to the
@@ -67,14 +71,14 @@ def expected_engine(forced, thr):
 JAC = golden_cases("jaccard")
 
 
-@pytest.mark.parametrize("partners", ["on", "off"])
+@pytest.mark.parametrize("partners", ["on", "popcount", "off"])
 @pytest.mark.parametrize("engine", ["scan", "index", "auto"])
 @pytest.mark.parametrize("case", JAC, ids=[c["name"] for c in JAC])
 def test_gpu_clustering_matches_reference_golden(torch, case, engine, partners, monkeypatch):
     monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
     monkeypatch.setenv("XSPMM_CLUSTER_PARTNERS", partners)
     thr = float(case["thresh"])
-    note(f"golden {case['name']} engine={engine} M={int(case['M'])} thr={thr}")
+    note(f"golden {case['name']} engine={engine} partners={partners} M={int(case['M'])} thr={thr}")
     perm, used = gpu_perm(torch, int(case["M"]), int(case["K"]), case["rp"], case["ci"], thr,
                           int(case["bw"]))
     assert perm.dtype == case["rp"].dtype
@@ -99,7 +103,7 @@ def skewed_csr(rng, M, K):
     return rp, ci
 
 
-@pytest.mark.parametrize("partners", ["on", "off"])
+@pytest.mark.parametrize("partners", ["on", "popcount", "off"])
 @pytest.mark.parametrize("itype", [np.int32, np.int64])
 @pytest.mark.parametrize("engine", ["scan", "index"])
 @pytest.mark.parametrize("seed", range(8))
@@ -189,13 +193,15 @@ def test_gpu_clustering_headline_size_matches_oracle(torch):
     p = synth.templates()
     note(f"templates M={p.M} nnz={int(p.rp[-1])}")
     want = oracle.jaccard(p.M, p.K, p.rp, p.ci)
-    for engine in ("auto", "scan", "index"):
+    for engine, partners in (("auto", "on"), ("scan", "on"), ("index", "on"), ("auto", "popcount")):
         os.environ["XSPMM_CLUSTER_ENGINE"] = engine
+        os.environ["XSPMM_CLUSTER_PARTNERS"] = partners
         try:
             got, used = gpu_perm(torch, p.M, p.K, p.rp, p.ci)
         finally:
             del os.environ["XSPMM_CLUSTER_ENGINE"]
-        note(f"templates engine={engine} ran={used}")
+            del os.environ["XSPMM_CLUSTER_PARTNERS"]
+        note(f"templates engine={engine} partners={partners} ran={used}")
         np.testing.assert_array_equal(widen(got), want)
 
 
@@ -218,6 +224,27 @@ def many_joins_csr(rng, M, K, n_patterns=40):
     rp = np.zeros(M + 1, np.int64)
     rp[1:] = np.cumsum([len(x) for x in rows])
     return rp, np.concatenate(rows).astype(np.int64)
+
+
+@pytest.mark.parametrize("W", [1, 4, 5, 8, 9, 16, 17, 28, 32])
+def test_gpu_partner_passes_across_bitmap_widths(torch, W, monkeypatch):
+    # The matrix-core partner pass stages W words per row (1, 2, 4 or 8 word
+    # quads by W) and the popcount pass one of three register widths: both
+    # must give the oracle's permutation at every width, for thresholds that
+    # make its candidate bound tight (0) or loose (0.8); 700 rows is six
+    # 128-row tiles, the last one ragged.
+    rng = np.random.default_rng(500 + W)
+    M, bw = 700, 16
+    K = bw * (64 * (W - 1) + 33)  # Kb = 64 (W - 1) + 33 blocks: W words per row
+    rp, ci = many_joins_csr(rng, M, K)
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", "scan")
+    for thr in (0.0, 0.3, 0.5, 0.8):
+        want = oracle.jaccard(M, K, rp, ci, thr, bw)
+        for partners in ("on", "popcount"):
+            monkeypatch.setenv("XSPMM_CLUSTER_PARTNERS", partners)
+            note(f"bitmap width W={W} thr={thr} partners={partners}")
+            got, _ = gpu_perm(torch, M, K, rp, ci, thr, bw)
+            np.testing.assert_array_equal(widen(got), want)
 
 
 @pytest.mark.parametrize("itype", [np.int32, np.int64])

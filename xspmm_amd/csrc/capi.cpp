@@ -251,9 +251,6 @@ int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
             require(M >= 0 && K >= 0 && nnz >= 0 && N >= 0, "CSR dimensions must be non-negative.");
             require(hw_block_size == 16,
                     "xSpMM: the MFMA tile kernel requires hw_block_size == 16.");
-            int dev = 0;
-            XSPMM_HIP_CHECK(hipGetDevice(&dev));
-            init_device_pool(dev);
             spmm_pipeline<T, I>(M, K, nnz, static_cast<const I*>(rp), static_cast<const I*>(ci),
                                 static_cast<const T*>(vals), static_cast<const T*>(B), C, N,
                                 hw_block_size, optimize_pattern != 0, timings, as_stream(stream));

@@ -173,11 +173,18 @@ __device__ __forceinline__ int64_t block_exscan64(int64_t v, int64_t* total, int
 
 // --- preparation kernels (one wave per row) ---------------------------------
 
+// column block of column c: a shift when the block width is a power of two
+// (sh >= 0), else a division
+__device__ __forceinline__ int64_t column_block(int64_t c, int64_t bw, int sh)
+{
+    return sh >= 0 ? c >> sh : c / bw;
+}
+
 template <typename I>
 __global__ __launch_bounds__(kPrepThreads) void pattern_bits_kernel(const I* __restrict__ rp,
                                                                     const I* __restrict__ ci,
                                                                     int64_t M, int64_t K,
-                                                                    int64_t nnz, int64_t bw,
+                                                                    int64_t nnz, int64_t bw, int sh,
                                                                     int64_t W, uint64_t* bits,
                                                                     int* bad)
 {
@@ -194,9 +201,54 @@ __global__ __launch_bounds__(kPrepThreads) void pattern_bits_kernel(const I* __r
                 *bad = 1;
                 continue;
             }
-            const int64_t b = c / bw;
+            const int64_t b = column_block(c, bw, sh);
             atomicOr((unsigned long long*)(q + (b >> 6)), 1ULL << (b & 63));
         }
+    }
+}
+
+// Row bitmaps of at most 64 words and their popcounts in one pass: each wave
+// ORs its row's bits into a bitmap in LDS (a wave's LDS operations complete
+// in order), then stores its W words and the popcount -- no global atomics
+// and no separate count pass.
+template <typename I>
+__global__ __launch_bounds__(kPrepThreads) void pattern_bits_lds_kernel(const I* __restrict__ rp,
+                                                                        const I* __restrict__ ci,
+                                                                        int64_t M, int64_t K,
+                                                                        int64_t nnz, int64_t bw, int sh,
+                                                                        int W, uint64_t* __restrict__ bits,
+                                                                        int32_t* __restrict__ count,
+                                                                        int* bad)
+{
+    __shared__ unsigned long long lbits[kPrepThreads / 64][64];
+    const int lane = threadIdx.x & 63;
+    unsigned long long* const q = lbits[threadIdx.x >> 6];
+    const int64_t nw = (int64_t)gridDim.x * (kPrepThreads / 64);
+    for (int64_t r = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) >> 6; r < M; r += nw) {
+        if (lane < W) q[lane] = 0ULL;
+        __builtin_amdgcn_wave_barrier();
+        int64_t s = (int64_t)rp[r], e = (int64_t)rp[r + 1];
+        s = s < 0 ? 0 : s;
+        e = e > nnz ? nnz : e;
+        for (int64_t j = s + lane; j < e; j += 64) {
+            const int64_t c = (int64_t)ci[j];
+            if (c < 0 || c >= K) {
+                *bad = 1;
+                continue;
+            }
+            const int64_t b = column_block(c, bw, sh);
+            atomicOr(q + (b >> 6), 1ULL << (b & 63));
+        }
+        __builtin_amdgcn_wave_barrier();
+        int64_t n = 0;
+        if (lane < W) {
+            const uint64_t v = q[lane];
+            bits[r * W + lane] = v;
+            n = __popcll(v);
+        }
+        n = wave_sum64(n);
+        if (lane == 0) count[r] = (int32_t)n;
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -290,6 +342,17 @@ __global__ void reversed_perm_kernel(I* perm, int64_t M)
         perm[i] = (I)(M - 1 - i);
 }
 
+// The row list total and the bad-column flag side by side, for one copy to
+// the host.
+__global__ void status_kernel(const int64_t* __restrict__ total, const int* __restrict__ bad,
+                              int64_t* __restrict__ status)
+{
+    if (threadIdx.x == 0) {
+        status[0] = *total;
+        status[1] = *bad;
+    }
+}
+
 // --- partner lists -------------------------------------------------------------
 // Row j is a partner of row i (j != i) when d(q_i, q_j) <= dist_thresh.  Until
 // the first join of a cluster the pattern is exactly q_seed, so its first
@@ -365,6 +428,179 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
             }
         }
     }
+}
+
+// All pairs on the int8 matrix cores: |q_i & q_j| is entry (i, j) of the
+// Gram matrix Q Q^T of the 0/1 row bitmaps, an exact integer dot product.
+// A workgroup of four waves takes a 128 x 128 tile (rows i of tile ti, rows
+// j of tile tj >= ti: the upper triangle, numbered row by row), each wave a
+// 64 x 64 quarter as 4 x 4 products v_mfma_i32_16x16x64_i8.  The tile's
+// 256 bitmap rows and their counts are staged in LDS first (rows padded to
+// 4 NQ + 1 words for W <= 4 NQ, the words past W zero; the odd stride
+// spreads a read's 16 rows over the banks).  Lane group g of a wave reads word 4q + g
+// of its rows for word quad q and spreads 16 of its bits per product into
+// 16 bytes 0 / -1.  The A and B operands of a product come from the same
+// spreading of the same word, so whatever K order the instruction's lane
+// layout implies, it pairs equal bits of q_i and q_j, and (-1)(-1) = 1.
+// Every pair j > i of the tile whose product passes a cheap bound (below)
+// gets the exact Jaccard test in the accumulator layout (lane (l, g) holds
+// rows 4g .. 4g+3 of column l of each 16 x 16 block), and a close pair is
+// listed for both rows, as in the popcount kernel.
+constexpr int kGramTile = 128;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+
+// bits 15-s, 31-s, 47-s and 63-s of w (0 <= s < 16) as four bytes 0 or -1:
+// v_perm_b32 selectors 8..11 replicate the top bits of bytes 1, 3, 5 and 7.
+// One 64-bit shift per dword (the compiler would split it into two 32-bit
+// operations).
+template <int S>
+__device__ __forceinline__ int spread_bits(uint64_t w)
+{
+    static_assert(S >= 0 && S < 16, "shift of 0 .. 15");
+    uint64_t y = w;
+    if constexpr (S != 0) asm("v_lshlrev_b64 %0, %1, %2" : "=v"(y) : "i"(S), "v"(w));
+    return (int)__builtin_amdgcn_perm((uint32_t)(y >> 32), (uint32_t)y, 0x0b0a0908u);
+}
+// the 16 bytes of bits 16 C .. 16 C + 15 of the spreading order
+template <int C>
+__device__ __forceinline__ i32x4_t spread_chunk(uint64_t w)
+{
+    return i32x4_t{spread_bits<4 * C>(w), spread_bits<4 * C + 1>(w), spread_bits<4 * C + 2>(w),
+                   spread_bits<4 * C + 3>(w)};
+}
+
+// NQ: word quads per row (W <= 4 NQ)
+template <int NQ>
+__global__ __launch_bounds__(256, 3) void partners_gram_kernel(const uint64_t* __restrict__ bits,
+                                                             const int32_t* __restrict__ count,
+                                                             int M, int W, int T, float thr,
+                                                             int32_t* pn, int32_t* partners)
+{
+    constexpr int wp = 4 * NQ + 1;
+    __shared__ uint64_t gram_lds[2 * kGramTile * wp + kGramTile];  // words, then 256 counts
+    // tile (ti, tj): row t of the triangle holds T - t tiles, so the rows
+    // above t hold start(t) = t T - t (t - 1) / 2; ti is the largest t with
+    // start(t) <= id (the smaller root of start(t) = id, then corrected)
+    const int64_t id = blockIdx.x;
+    auto start = [&](int64_t t) { return t * T - t * (t - 1) / 2; };
+    const double b2 = 2.0 * T + 1.0;
+    int64_t ti = (int64_t)((b2 - sqrt(fmax(b2 * b2 - 8.0 * (double)id, 0.0))) * 0.5);
+    ti = min(max(ti, (int64_t)0), (int64_t)T - 1);
+    while (ti > 0 && start(ti) > id) --ti;
+    while (ti + 1 < T && start(ti + 1) <= id) ++ti;
+    const int64_t tj = ti + (id - start(ti));
+
+    // stage rows i (local 0..127) and rows j (local 128..255): four threads
+    // per row, each taking every fourth word; rows past M read as zeros
+    int32_t* const lcount = reinterpret_cast<int32_t*>(gram_lds + 2 * kGramTile * wp);
+    {
+        const int t = threadIdx.x;
+        for (int rr = t >> 2; rr < 2 * kGramTile; rr += 64) {
+            const int64_t row = rr < kGramTile ? ti * kGramTile + rr : tj * kGramTile + rr - kGramTile;
+            const bool valid = row < M;
+            const uint64_t* src = bits + (valid ? row : 0) * W;
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                const int w = 4 * u + (t & 3);
+                gram_lds[rr * wp + w] = valid && w < W ? src[w] : 0ULL;
+            }
+        }
+        const int64_t row = t < kGramTile ? ti * kGramTile + t : tj * kGramTile + t - kGramTile;
+        lcount[t] = row < M ? count[row] : 0;
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int li = lane & 15, g = lane >> 4;
+    const int il0 = (wave >> 1) * 64;               // local row of the quarter's first i
+    const int jl0 = kGramTile + (wave & 1) * 64;    // and of its first j
+    const int64_t i0 = ti * kGramTile + il0;
+    const int64_t j0 = tj * kGramTile + jl0 - kGramTile;
+    // a quarter wholly on or below the diagonal, or past the last row, holds
+    // no pair j > i (no barrier follows: the wave may leave)
+    if (j0 + 63 <= i0 || i0 >= M || j0 >= M) return;
+
+    // Candidates.  close() holds only if inter >= RN(a_lo uni) >= a' uni
+    // with a' = a_lo (1 - 2^-24) and uni = c_i + c_j - inter, that is only if
+    // inter >= a' / (1 + a') (c_i + c_j).  beta rounds that factor down by
+    // 2^-16 (more than its float roundings), so f = floor(beta c) gives
+    // f_i + f_j <= a' / (1 + a') (c_i + c_j): each accumulator starts at
+    // -(f_i + f_j), and a pair whose product ends below zero is not close.
+    const JaccardTest jt(thr);
+    const float beta = jt.a_lo > 0.0f ? jt.a_lo / (1.0f + jt.a_lo) * (1.0f - 0x1p-16f) : 0.0f;
+    int fi[4][4], fj[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // rows il0 + 16 m + 4 g + r (r = 0..3) and row jl0 + 16 m + li
+        const int4 c4 = *reinterpret_cast<const int4*>(lcount + il0 + 16 * m + 4 * g);
+        fi[m][0] = (int)(beta * (float)c4.x);
+        fi[m][1] = (int)(beta * (float)c4.y);
+        fi[m][2] = (int)(beta * (float)c4.z);
+        fi[m][3] = (int)(beta * (float)c4.w);
+        fj[m] = (int)(beta * (float)lcount[jl0 + 16 * m + li]);
+    }
+    i32x4_t acc[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[m][n][r] = -(fi[m][r] + fj[n]);
+
+    const uint64_t* const wi = gram_lds + (il0 + li) * wp + g;
+    const uint64_t* const wj = gram_lds + (jl0 + li) * wp + g;
+    // (eight quads unrolled would need more than 256 registers)
+#pragma unroll(NQ > 4 ? 4 : NQ)
+    for (int q = 0; q < NQ; ++q) {
+        uint64_t a[4], b[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            a[m] = wi[16 * m * wp + 4 * q];
+            b[m] = wj[16 * m * wp + 4 * q];
+        }
+        auto chunk = [&]<int C>() __attribute__((always_inline)) {
+            i32x4_t A[4], B[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                A[m] = spread_chunk<C>(a[m]);
+                B[m] = spread_chunk<C>(b[m]);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int n = 0; n < 4; ++n)
+                    acc[m][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], B[n], acc[m][n], 0, 0, 0);
+        };
+        chunk.template operator()<0>();
+        chunk.template operator()<1>();
+        chunk.template operator()<2>();
+        chunk.template operator()<3>();
+    }
+
+    // every pair of the quarter has i < j < M (uniform)
+    const bool interior = j0 >= i0 + 64 && j0 + 64 <= M;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                if (acc[m][n][r] < 0) continue;
+                const int inter = acc[m][n][r] + fi[m][r] + fj[n];
+                // row numbers fit 31 bits (M < 2^31)
+                const int i = (int)i0 + 16 * m + 4 * g + r;
+                const int j = (int)j0 + 16 * n + li;
+                if (!interior && (i >= M || j >= M || j <= i)) continue;
+                const int ci = lcount[il0 + 16 * m + 4 * g + r], cj = lcount[jl0 + 16 * n + li];
+                if (jt.close(inter, ci + cj - inter)) {  // partnership is symmetric
+                    const int k = atomicAdd(&pn[i], 1);
+                    if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
+                    const int k2 = atomicAdd(&pn[j], 1);
+                    if (k2 < kPartnerCap) partners[(int64_t)j * kPartnerCap + k2] = i;
+                }
+            }
 }
 
 // Pairs through the per-block row lists: one workgroup per row i counts
@@ -809,6 +1045,17 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
 
 }  // namespace
 
+// Offsets of 256-byte aligned pieces of one allocation
+struct Carve {
+    size_t end = 0;
+    size_t take(size_t bytes)
+    {
+        const size_t at = (end + 255) & ~size_t(255);
+        end = at + bytes;
+        return at;
+    }
+};
+
 template <typename I>
 void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                                float dist_thresh, int64_t block_width, I* perm, hipStream_t s,
@@ -822,24 +1069,65 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
         throw std::invalid_argument("clustering: shape beyond the GPU engine's limits.");
     const int64_t W = Kb > 0 ? (Kb + 63) / 64 : 1;
 
-    Scratch bad_d(sizeof(int) * 2, s);
-    XSPMM_HIP_CHECK(hipMemsetAsync(bad_d.get(), 0, sizeof(int) * 2, s));
-    int* bad = bad_d.as<int>();
-    Scratch bits((size_t)(M * W) * sizeof(uint64_t), s);
-    XSPMM_HIP_CHECK(hipMemsetAsync(bits.get(), 0, (size_t)(M * W) * sizeof(uint64_t), s));
+    // One allocation for the fixed-size temporaries (a stream-ordered
+    // allocation costs host time; the call makes two).  The pieces cleared
+    // before use -- flags, the greedy's counters, partner counts and the row
+    // bitmaps -- come first and are cleared by one memset.
+    const int64_t nb = Kb > 0 ? Kb : 1;
+    Carve cv;
+    const size_t o_flags = cv.take(2 * sizeof(int));
+    const size_t o_cnt = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_pn = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_bits = cv.take((size_t)(M * W) * sizeof(uint64_t));
+    const size_t zeroed = cv.end;
+    const size_t o_count = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_rbs = cv.take((size_t)(M + 1) * sizeof(int64_t));
+    const size_t o_blc = cv.take((size_t)nb * sizeof(int32_t));
+    const size_t o_un = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_pos = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_logb = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_ca = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_cb = cv.take((size_t)M * sizeof(int32_t));
+    const size_t o_plist = cv.take((size_t)nb * sizeof(int32_t));
+    const size_t o_partners = cv.take((size_t)M * kPartnerCap * sizeof(int32_t));
+    const size_t o_status = cv.take(2 * sizeof(int64_t));
+    Scratch tmp(cv.end, s);
+    char* const base = tmp.as<char>();
+    XSPMM_HIP_CHECK(hipMemsetAsync(base, 0, zeroed, s));
+    int* const bad = reinterpret_cast<int*>(base + o_flags);  // [0] bad column, [1] engine used
+    uint64_t* const bits = reinterpret_cast<uint64_t*>(base + o_bits);
+    int32_t* const count = reinterpret_cast<int32_t*>(base + o_count);
+    int64_t* const rb_start = reinterpret_cast<int64_t*>(base + o_rbs);
+    int32_t* const bl_count = reinterpret_cast<int32_t*>(base + o_blc);
+    int32_t* const pn = reinterpret_cast<int32_t*>(base + o_pn);
+    int32_t* const partners = reinterpret_cast<int32_t*>(base + o_partners);
+
     const unsigned grid = (unsigned)std::min<int64_t>((M + 3) / 4, 65536);
-    hipLaunchKernelGGL(pattern_bits_kernel<I>, dim3(grid), dim3(kPrepThreads), 0, s, rp, ci, M, K,
-                       nnz, block_width, W, bits.as<uint64_t>(), bad);
+    const int sh = (block_width & (block_width - 1)) == 0 ? __builtin_ctzll((unsigned long long)block_width) : -1;
+    // bitmaps of up to 64 words come with their popcounts
+    const bool lds_bits = W <= 64;
+    if (lds_bits)
+        hipLaunchKernelGGL(pattern_bits_lds_kernel<I>, dim3(grid), dim3(kPrepThreads), 0, s, rp, ci, M, K,
+                           nnz, block_width, sh, (int)W, bits, count, bad);
+    else
+        hipLaunchKernelGGL(pattern_bits_kernel<I>, dim3(grid), dim3(kPrepThreads), 0, s, rp, ci, M, K,
+                           nnz, block_width, sh, W, bits, bad);
     XSPMM_LAUNCH_CHECK();
+    // an out-of-range column (skipped by the kernel) is reported before
+    // anything writes perm: here on the closed-form path, else with the row
+    // list total below
     int h_bad = 0;
-    XSPMM_HIP_CHECK(hipMemcpyAsync(&h_bad, bad, sizeof(int), hipMemcpyDeviceToHost, s));
-    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
-    if (h_bad) throw std::invalid_argument("clustering: column index out of range.");
+    auto check_bad = [&] {
+        if (h_bad) throw std::invalid_argument("clustering: column index out of range.");
+    };
 
     // d <= t never holds for t < 0 (or NaN) and always holds for t >= 1:
     // no row joins, or every row joins the first cluster in visiting order;
     // either way perm = [M-1, ..., 0].
     if (!(dist_thresh >= 0.0f && dist_thresh < 1.0f)) {
+        XSPMM_HIP_CHECK(hipMemcpyAsync(&h_bad, bad, sizeof(int), hipMemcpyDeviceToHost, s));
+        XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+        check_bad();
         hipLaunchKernelGGL(reversed_perm_kernel<I>, dim3((unsigned)std::min<int64_t>((M + 255) / 256, 4096)),
                            dim3(256), 0, s, perm, M);
         XSPMM_LAUNCH_CHECK();
@@ -847,12 +1135,10 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
         return;
     }
 
-    Scratch count((size_t)M * sizeof(int32_t), s);
-    hipLaunchKernelGGL(pattern_count_kernel, dim3(grid), dim3(kPrepThreads), 0, s,
-                       bits.as<uint64_t>(), M, W, count.as<int32_t>());
-    XSPMM_LAUNCH_CHECK();
-    const int64_t nb = Kb > 0 ? Kb : 1;
-    Scratch bl_count((size_t)nb * sizeof(int32_t), s);
+    if (!lds_bits) {
+        hipLaunchKernelGGL(pattern_count_kernel, dim3(grid), dim3(kPrepThreads), 0, s, bits, M, W, count);
+        XSPMM_LAUNCH_CHECK();
+    }
 
     // Engine and partner method, decided here so that the per-row and
     // per-block lists are built only when a step reads them: the index
@@ -863,18 +1149,58 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
         if (std::strcmp(e, "scan") == 0) engine = kEngineScan;
         else if (std::strcmp(e, "index") == 0) engine = kEngineIndex;
     }
-    bool use_partners = true;
-    if (const char* e = std::getenv("XSPMM_CLUSTER_PARTNERS"))
+    // XSPMM_CLUSTER_PARTNERS: off (every seed on the full path) or popcount
+    // (all-pairs lists by VALU popcounts instead of the matrix cores)
+    bool use_partners = true, popcount_partners = false;
+    if (const char* e = std::getenv("XSPMM_CLUSTER_PARTNERS")) {
         use_partners = std::strcmp(e, "off") != 0;
+        popcount_partners = std::strcmp(e, "popcount") == 0;
+    }
     const bool bitmap_partners = W <= 32 && (double)M * (double)M * (double)W <= 6.4e10;
     // row list offsets: their total, sum_b v_b = sum_i |q_i|, bounds the
     // engine estimate: (sum v_b)^2 / Kb <= sum v_b^2 <= sum v_b * min(M, sum v_b)
-    Scratch rb_start((size_t)(M + 1) * sizeof(int64_t), s);
-    device_exclusive_scan(ArrayValue<int32_t>{count.as<int32_t>()}, M, rb_start.as<int64_t>(), s);
-    int64_t nrb = 0;
-    XSPMM_HIP_CHECK(hipMemcpyAsync(&nrb, rb_start.as<int64_t>() + M, sizeof(int64_t),
-                                   hipMemcpyDeviceToHost, s));
-    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    device_exclusive_scan(ArrayValue<int32_t>{count}, M, rb_start, s);
+    int64_t* const status = reinterpret_cast<int64_t*>(base + o_status);
+    hipLaunchKernelGGL(status_kernel, dim3(1), dim3(64), 0, s, rb_start + M, bad, status);
+    XSPMM_LAUNCH_CHECK();
+    // pinned, so that the copy does not hold the host (one buffer per host
+    // thread, kept for the thread's life; a call reads it before returning)
+    thread_local int64_t* h_status = nullptr;
+    if (!h_status) XSPMM_HIP_CHECK(hipHostMalloc((void**)&h_status, 2 * sizeof(int64_t), hipHostMallocDefault));
+    XSPMM_HIP_CHECK(hipMemcpyAsync(h_status, status, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    EventHandle copied;
+    XSPMM_HIP_CHECK(hipEventRecord(copied.get(), s));
+
+    // Partner lists (XSPMM_CLUSTER_PARTNERS=off leaves every seed on the
+    // full path); pn starts at zero.  The all-pairs passes need only the
+    // bitmaps and counts: they are enqueued before the host waits for the
+    // copy of the row list total, so the host decides and enqueues the rest
+    // while they run.  The row-list pass runs after the lists are built.
+    if (use_partners && bitmap_partners) {
+        const int Mi = (int)M, Wi = (int)W;
+        if (bitmap_partners && !popcount_partners) {
+            const int64_t T = (M + kGramTile - 1) / kGramTile;
+            const dim3 g((unsigned)(T * (T + 1) / 2));
+            auto kern = W <= 4 ? partners_gram_kernel<1> : W <= 8 ? partners_gram_kernel<2>
+                      : W <= 16 ? partners_gram_kernel<4> : partners_gram_kernel<8>;
+            hipLaunchKernelGGL(kern, g, dim3(256), 0, s, bits, count, Mi, Wi, (int)T, dist_thresh, pn,
+                               partners);
+        } else {
+            // about 2048 workgroups: the rows j are split over grid.y
+            const int64_t gx = (M + kPairRows - 1) / kPairRows;
+            const int64_t tiles = (M + kPairTile - 1) / kPairTile;
+            const dim3 g((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(tiles, 2048 / gx)));
+            auto kern = W <= 8 ? partners_bitmap_kernel<8> : W <= 16 ? partners_bitmap_kernel<16>
+                                                                      : partners_bitmap_kernel<32>;
+            hipLaunchKernelGGL(kern, g, dim3(256), 0, s, bits, count, Mi, Wi, dist_thresh, pn, partners);
+        }
+        XSPMM_LAUNCH_CHECK();
+    }
+
+    XSPMM_HIP_CHECK(hipEventSynchronize(copied.get()));
+    const int64_t nrb = h_status[0];
+    h_bad = (int)h_status[1];
+    check_bad();
     const double scan_work = 0.5 * (double)M * (double)M * (double)W;
     if (engine == kEngineAuto && Kb > 0) {
         const double sv = (double)nrb;
@@ -882,14 +1208,13 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
         else if (3.0 * sv * std::min(sv, (double)M) < scan_work) engine = kEngineIndex;
     }
     if (engine == kEngineAuto) {
-        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
+        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count, 0, (size_t)nb * sizeof(int32_t), s));
         const int64_t gy = std::max<int64_t>(1, std::min<int64_t>(1024, (M + 255) / 256));
         hipLaunchKernelGGL(block_counts_kernel, dim3((unsigned)((nb + kPrepThreads - 1) / kPrepThreads), (unsigned)gy),
-                           dim3(kPrepThreads), 0, s, bits.as<uint64_t>(), M, W, Kb,
-                           bl_count.as<int32_t>());
+                           dim3(kPrepThreads), 0, s, bits, M, W, Kb, bl_count);
         XSPMM_LAUNCH_CHECK();
         std::vector<int32_t> h_bl((size_t)nb);
-        XSPMM_HIP_CHECK(hipMemcpyAsync(h_bl.data(), bl_count.get(), (size_t)nb * sizeof(int32_t),
+        XSPMM_HIP_CHECK(hipMemcpyAsync(h_bl.data(), bl_count, (size_t)nb * sizeof(int32_t),
                                        hipMemcpyDeviceToHost, s));
         XSPMM_HIP_CHECK(hipStreamSynchronize(s));
         int64_t sq = 0;
@@ -900,67 +1225,41 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     }
     const bool need_lists = engine == kEngineIndex || (use_partners && !bitmap_partners);
 
-    Scratch rb, bl_start, bl_rows;
+    // the per-row block lists and per-block row lists (nrb entries each)
+    Scratch lists;
+    int32_t* rb = nullptr;
+    int64_t* bl_start = nullptr;
+    int32_t* bl_rows = nullptr;
     if (need_lists) {
-        rb = Scratch((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
-        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
-        hipLaunchKernelGGL(row_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, bits.as<uint64_t>(),
-                           M, W, rb_start.as<int64_t>(), rb.as<int32_t>(), bl_count.as<int32_t>());
+        Carve lc;
+        const size_t o_rb = lc.take((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t));
+        const size_t o_bls = lc.take((size_t)(nb + 1) * sizeof(int64_t));
+        const size_t o_blr = lc.take((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t));
+        lists = Scratch(lc.end, s);
+        rb = reinterpret_cast<int32_t*>(lists.as<char>() + o_rb);
+        bl_start = reinterpret_cast<int64_t*>(lists.as<char>() + o_bls);
+        bl_rows = reinterpret_cast<int32_t*>(lists.as<char>() + o_blr);
+        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count, 0, (size_t)nb * sizeof(int32_t), s));
+        hipLaunchKernelGGL(row_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, bits, M, W, rb_start,
+                           rb, bl_count);
         XSPMM_LAUNCH_CHECK();
-        bl_start = Scratch((size_t)(nb + 1) * sizeof(int64_t), s);
-        device_exclusive_scan(ArrayValue<int32_t>{bl_count.as<int32_t>()}, nb, bl_start.as<int64_t>(), s);
-        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count.get(), 0, (size_t)nb * sizeof(int32_t), s));
-        bl_rows = Scratch((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t), s);
-        hipLaunchKernelGGL(block_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, M,
-                           rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
-                           bl_count.as<int32_t>(), bl_rows.as<int32_t>());
+        device_exclusive_scan(ArrayValue<int32_t>{bl_count}, nb, bl_start, s);
+        XSPMM_HIP_CHECK(hipMemsetAsync(bl_count, 0, (size_t)nb * sizeof(int32_t), s));
+        hipLaunchKernelGGL(block_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, M, rb_start, rb,
+                           bl_start, bl_count, bl_rows);
+        XSPMM_LAUNCH_CHECK();
+    }
+    if (use_partners && !bitmap_partners) {
+        hipLaunchKernelGGL(partners_index_kernel, dim3((unsigned)std::min<int64_t>(M, 1024)),
+                           dim3(1024), 0, s, (int)M, rb_start, rb, bl_start, bl_rows, count,
+                           dist_thresh, pn, partners);
         XSPMM_LAUNCH_CHECK();
     }
 
-    Scratch un((size_t)M * sizeof(int32_t), s), pos((size_t)M * sizeof(int32_t), s);
-    Scratch cnt((size_t)M * sizeof(int32_t), s), logb((size_t)M * sizeof(int32_t), s);
-    Scratch ca((size_t)M * sizeof(int32_t), s), cb((size_t)M * sizeof(int32_t), s);
-    Scratch plist((size_t)nb * sizeof(int32_t), s);
-    XSPMM_HIP_CHECK(hipMemsetAsync(cnt.get(), 0, (size_t)M * sizeof(int32_t), s));
-
-    // partner lists (XSPMM_CLUSTER_PARTNERS=off leaves every seed on the full path)
-    Scratch pn((size_t)M * sizeof(int32_t), s);
-    Scratch partners((size_t)M * kPartnerCap * sizeof(int32_t), s);
-    if (use_partners) {
-        const int Mi = (int)M, Wi = (int)W;
-        if (bitmap_partners) {
-            XSPMM_HIP_CHECK(hipMemsetAsync(pn.get(), 0, (size_t)M * sizeof(int32_t), s));
-            // about 2048 workgroups: the rows j are split over grid.y
-            const int64_t gx = (M + kPairRows - 1) / kPairRows;
-            const int64_t tiles = (M + kPairTile - 1) / kPairTile;
-            const dim3 g((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(tiles, 2048 / gx)));
-            if (W <= 8)
-                hipLaunchKernelGGL(partners_bitmap_kernel<8>, g, dim3(256), 0, s, bits.as<uint64_t>(),
-                                   count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
-                                   partners.as<int32_t>());
-            else if (W <= 16)
-                hipLaunchKernelGGL(partners_bitmap_kernel<16>, g, dim3(256), 0, s, bits.as<uint64_t>(),
-                                   count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
-                                   partners.as<int32_t>());
-            else
-                hipLaunchKernelGGL(partners_bitmap_kernel<32>, g, dim3(256), 0, s, bits.as<uint64_t>(),
-                                   count.as<int32_t>(), Mi, Wi, dist_thresh, pn.as<int32_t>(),
-                                   partners.as<int32_t>());
-        } else {
-            hipLaunchKernelGGL(partners_index_kernel, dim3((unsigned)std::min<int64_t>(M, 1024)),
-                               dim3(1024), 0, s, Mi, rb_start.as<int64_t>(), rb.as<int32_t>(),
-                               bl_start.as<int64_t>(), bl_rows.as<int32_t>(), count.as<int32_t>(),
-                               dist_thresh, pn.as<int32_t>(), partners.as<int32_t>());
-        }
-        XSPMM_LAUNCH_CHECK();
-    }
-
-    ClusterArgs args{M, W, Kb, dist_thresh, engine, bits.as<uint64_t>(), count.as<int32_t>(),
-                     rb_start.as<int64_t>(), rb.as<int32_t>(), bl_start.as<int64_t>(),
-                     bl_rows.as<int32_t>(), un.as<int32_t>(), pos.as<int32_t>(),
-                     cnt.as<int32_t>(), logb.as<int32_t>(), ca.as<int32_t>(), cb.as<int32_t>(),
-                     plist.as<int32_t>(), use_partners ? pn.as<int32_t>() : nullptr,
-                     partners.as<int32_t>(), bad + 1};
+    auto at = [&](size_t o) { return reinterpret_cast<int32_t*>(base + o); };
+    ClusterArgs args{M, W, Kb, dist_thresh, engine, bits, count, rb_start, rb, bl_start, bl_rows,
+                     at(o_un), at(o_pos), at(o_cnt), at(o_logb), at(o_ca), at(o_cb), at(o_plist),
+                     use_partners ? pn : nullptr, partners, bad + 1};
     hipLaunchKernelGGL(cluster_kernel<I>, dim3(1), dim3(kClThreads), 0, s, args, perm);
     XSPMM_LAUNCH_CHECK();
     if (engine_used) {

@@ -26,6 +26,12 @@
 namespace xspmm {
 namespace detail {
 
+// Keeps freed stream-ordered memory in the device pool instead of returning
+// it to the driver at every synchronization (the default pool's release
+// threshold; set once per device, before its first stream-ordered
+// allocation).
+void init_device_pool(int device);
+
 // Stream-ordered device scratch: allocated with hipMallocAsync on `s` and
 // released with hipFreeAsync on `s` when it goes out of scope, so it may be
 // dropped right after the kernels that use it are enqueued.
@@ -33,7 +39,12 @@ class Scratch {
 public:
     Scratch() = default;
     Scratch(size_t bytes, hipStream_t s) : s_(s) {
-        if (bytes) XSPMM_HIP_CHECK(hipMallocAsync(&p_, bytes, s));
+        if (bytes) {
+            int dev = 0;
+            XSPMM_HIP_CHECK(hipGetDevice(&dev));
+            init_device_pool(dev);
+            XSPMM_HIP_CHECK(hipMallocAsync(&p_, bytes, s));
+        }
     }
     ~Scratch() {
         if (p_) (void)hipFreeAsync(p_, s_);
@@ -57,6 +68,21 @@ public:
 private:
     void* p_ = nullptr;
     hipStream_t s_ = nullptr;
+};
+
+// A HIP event without timing, destroyed with its scope.
+class EventHandle {
+public:
+    EventHandle() { XSPMM_HIP_CHECK(hipEventCreateWithFlags(&e_, hipEventDisableTiming)); }
+    ~EventHandle() {
+        if (e_) (void)hipEventDestroy(e_);
+    }
+    EventHandle(const EventHandle&) = delete;
+    EventHandle& operator=(const EventHandle&) = delete;
+    hipEvent_t get() const { return e_; }
+
+private:
+    hipEvent_t e_ = nullptr;
 };
 
 // Device memory for a launcher's temporaries.  Without a region it makes
@@ -136,9 +162,6 @@ private:
     hipEvent_t a_ = nullptr, b_ = nullptr;
 };
 
-// Keeps freed stream-ordered memory in the device pool instead of returning
-// it to the driver at every synchronization (called once per device).
-void init_device_pool(int device);
 
 // ---------------------------------------------------------------------------
 // Kernel launchers (all enqueue on `s`; none synchronizes unless stated).
