@@ -168,7 +168,7 @@ int xspmm_jaccard_clustering_host(int itype, int64_t M, int64_t K, const void* r
  * src/cpu/clustering_sylos_labini.cpp:51-120), computed by one workgroup that
  * commits joins in the reference's visiting order.  engine_used (nullable,
  * host) receives 0 (closed form: dist_thresh outside [0, 1)), 1 (scan engine)
- * or 2 (row-list engine).  Synchronizes `stream`.  Limits: M < 2^31, at most
+ * or 2 (row-list engine).  Synchronizes `stream`.  Limits: M < 2^30, at most
  * 524288 column blocks, M * ceil(blocks / 64) * 8 bytes of row bitmaps
  * within 16 GiB; beyond them it returns XSPMM_ERR_INVALID.
  * Replaces xspmm::compute_1d_jaccard_clustering for device matrices

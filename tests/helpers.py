@@ -44,3 +44,20 @@ def dense_from_bcsr(M, K, rb, cb, brp, bci, bvals, dtype=np.float64):
 
 def widen(a):
     return np.asarray(a).astype(np.int64)
+
+
+def nested_csr(rng, M, K, n_base=5, grow=0.1):
+    """CSR rows that are random subsets of a few base patterns (a join leaves
+    the clustering pattern as it is), a fraction `grow` of them with one or
+    two columns of their own (a join grows it)."""
+    base = [rng.choice(K, size=int(rng.integers(20, 60)), replace=False) for _ in range(n_base)]
+    rows = []
+    for _ in range(M):
+        b = base[int(rng.integers(0, n_base))]
+        r = b[rng.random(len(b)) < rng.uniform(0.6, 1.0)]
+        if rng.random() < grow:
+            r = np.concatenate([r, rng.integers(0, K, size=int(rng.integers(1, 3)))])
+        rows.append(r)
+    rp = np.zeros(M + 1, np.int64)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    return rp, np.concatenate(rows).astype(np.int64)

@@ -12,7 +12,7 @@ import pytest
 
 import oracle
 import xspmm_amd as X
-from tests.helpers import golden_cases, widen
+from tests.helpers import golden_cases, nested_csr, widen
 from xspmm_amd import synth
 
 ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
@@ -195,6 +195,29 @@ def test_product_clustering_index_partner_lists(n_templates, keep, monkeypatch):
     for nthreads in (1, 5):
         got = X.compute_1d_jaccard_clustering(p.M, p.K, p.rp, p.ci, nthreads=nthreads)
         np.testing.assert_array_equal(widen(got), want)
+
+
+@pytest.mark.parametrize("engine", ["scan", "index"])
+def test_product_clustering_joins_inside_the_pattern(engine, monkeypatch):
+    # Runs of joiners whose rows lie inside the pattern are committed in one
+    # step by the scan engine (they leave the pattern as it is); the
+    # permutation must stay the reference's: dense pruned-like rows (every
+    # row joins the first cluster) and nested subsets with some rows that
+    # grow the pattern, one and four threads, both search forms.
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", engine)
+    p = synth.pruned(M=3000, K=1024, N=16, seed=3)
+    cases = [(p.M, p.K, p.rp.astype(np.int64), p.ci.astype(np.int64), 0.5, 16)]
+    rng = np.random.default_rng(77)
+    for thr, bw in ((0.3, 4), (0.5, 8), (0.7, 16)):
+        rp, ci = nested_csr(rng, 2500, 2000)
+        cases.append((2500, 2000, rp, ci, thr, bw))
+    for M, K, rp, ci, thr, bw in cases:
+        want = oracle.jaccard(M, K, rp, ci, thr, bw)
+        for simd in ("scalar", "auto"):
+            monkeypatch.setenv("XSPMM_CLUSTER_SIMD", simd)
+            for nthreads in (1, 4):
+                got = X.compute_1d_jaccard_clustering(M, K, rp, ci, thr, bw, nthreads=nthreads)
+                np.testing.assert_array_equal(widen(got), want)
 
 
 @pytest.mark.parametrize("simd", ["scalar", "auto"])

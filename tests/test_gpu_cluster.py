@@ -11,6 +11,8 @@ The permutation must equal the reference's bit for bit:
     default, or by VALU popcounts with XSPMM_CLUSTER_PARTNERS=popcount) and
     without them (XSPMM_CLUSTER_PARTNERS=off), and with both partner passes
     at row bitmaps of 1 to 32 words;
+  * runs of joins that leave the pattern as it is (committed in one step),
+    and rows with more partners than their lists hold;
   * at the headline size (templates, 16384 rows) against the oracle, and on
     the 131072-row power-law graph against the product's host engine (the
     oracle's scan would take minutes there; the host engine is pinned to the
@@ -26,7 +28,7 @@ import pytest
 
 import oracle
 import xspmm_amd as X
-from tests.helpers import golden_cases, widen
+from tests.helpers import golden_cases, nested_csr, widen
 from xspmm_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -245,6 +247,30 @@ def test_gpu_partner_passes_across_bitmap_widths(torch, W, monkeypatch):
             note(f"bitmap width W={W} thr={thr} partners={partners}")
             got, _ = gpu_perm(torch, M, K, rp, ci, thr, bw)
             np.testing.assert_array_equal(widen(got), want)
+
+
+@pytest.mark.parametrize("partners", ["on", "popcount", "off"])
+def test_gpu_clustering_joins_inside_the_pattern(torch, partners, monkeypatch):
+    # The scan engine commits a run of joiners whose rows lie inside the
+    # pattern in one step (they leave it as it is), and the all-pairs
+    # partner passes stop adding to lists already past their cap: dense
+    # pruned-like rows (every pair close, every row joins the first cluster)
+    # and nested subsets with some rows that grow the pattern, against the
+    # oracle.
+    monkeypatch.setenv("XSPMM_CLUSTER_ENGINE", "scan")
+    monkeypatch.setenv("XSPMM_CLUSTER_PARTNERS", partners)
+    p = synth.pruned(M=3000, K=1024, N=16, seed=3)
+    cases = [(p.M, p.K, p.rp.astype(np.int64), p.ci.astype(np.int64), 0.5, 16)]
+    rng = np.random.default_rng(78)
+    for thr, bw in ((0.3, 4), (0.5, 8), (0.7, 16)):
+        rp, ci = nested_csr(rng, 2500, 2000)
+        cases.append((2500, 2000, rp, ci, thr, bw))
+    for M, K, rp, ci, thr, bw in cases:
+        note(f"inside-pattern joins M={M} thr={thr} bw={bw} partners={partners}")
+        want = oracle.jaccard(M, K, rp, ci, thr, bw)
+        got, used = gpu_perm(torch, M, K, rp, ci, thr, bw)
+        assert used == "scan"
+        np.testing.assert_array_equal(widen(got), want)
 
 
 @pytest.mark.parametrize("itype", [np.int32, np.int64])

@@ -114,8 +114,13 @@ __attribute__((target("avx512f,avx512vpopcntdq"))) inline int64_t and_popcount_a
     return s;
 }
 
+// Joiners whose row lies inside the pattern (|p & q| = |q|) leave it as it
+// is, so the search goes on past them: it returns the highest position whose
+// row joins and grows the pattern, and appends the positions above it whose
+// rows join inside the pattern to `inside` (in visiting order).
 template <bool AVX512, typename JT>
-inline int64_t scan_down(const ScanArgs& a, const JT& jt, int64_t top, int64_t bot)
+inline int64_t scan_down(const ScanArgs& a, const JT& jt, int64_t top, int64_t bot,
+                         std::vector<int64_t>& inside)
 {
     for (int64_t pos = top; pos >= bot; --pos) {
         const int64_t cand = a.un[pos];
@@ -128,7 +133,10 @@ inline int64_t scan_down(const ScanArgs& a, const JT& jt, int64_t top, int64_t b
             inter = and_popcount_avx512(a.p, q, a.W);
         else
             inter = and_popcount(a.p, q, a.W);
-        if (jt.close(inter, a.pc + qc - inter)) return pos;
+        if (jt.close(inter, a.pc + qc - inter)) {
+            if (inter != qc) return pos;
+            inside.push_back(pos);
+        }
     }
     return -1;
 }
@@ -214,18 +222,17 @@ private:
 };
 
 template <typename JT>
-int64_t scan_down_scalar(const ScanArgs& a, const JT& jt, int64_t top, int64_t bot)
+int64_t scan_down_scalar(const ScanArgs& a, const JT& jt, int64_t top, int64_t bot,
+                         std::vector<int64_t>& inside)
 {
-    return scan_down<false>(a, jt, top, bot);
+    return scan_down<false>(a, jt, top, bot, inside);
 }
 
 template <typename JT>
-__attribute__((target("avx512f,avx512vpopcntdq"))) int64_t scan_down_avx512(const ScanArgs& a,
-                                                                            const JT& jt,
-                                                                            int64_t top,
-                                                                            int64_t bot)
+__attribute__((target("avx512f,avx512vpopcntdq"))) int64_t scan_down_avx512(
+    const ScanArgs& a, const JT& jt, int64_t top, int64_t bot, std::vector<int64_t>& inside)
 {
-    return scan_down<true>(a, jt, top, bot);
+    return scan_down<true>(a, jt, top, bot, inside);
 }
 
 // XSPMM_CLUSTER_SIMD=scalar forces the scalar search (for tests and CPUs
@@ -251,6 +258,7 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
     Pool pool(nthreads);
     const int nt = pool.size();
     std::vector<int64_t> found((size_t)nt);
+    std::vector<std::vector<int64_t>> inside((size_t)nt);
     // positions searched per round before the range doubles: about 1024 per
     // thread, so that a round's work outweighs waking the pool
     const int64_t first_stretch = std::max<int64_t>(2048, 1024 * (int64_t)nt);
@@ -263,26 +271,46 @@ void engine_scan(const Patterns& P, float t, I* perm, int nthreads)
         int64_t hi = n_un - 1;  // next position to visit
         int64_t stretch = first_stretch;
         while (hi >= 0) {
-            // First joining position in [lo, hi], scanning downwards.
+            // First joining position in [lo, hi] that grows the pattern,
+            // scanning downwards, and the joiners inside the pattern above it.
             const int64_t lo = hi - stretch + 1 > 0 ? hi - stretch + 1 : 0;
             const ScanArgs sa{P.bits.data(), P.count.data(), un.data(), p.data(), W, pc};
-            auto scan = [&](int64_t top, int64_t bot) {
-                return avx512 ? scan_down_avx512(sa, jt, top, bot) : scan_down_scalar(sa, jt, top, bot);
+            auto scan = [&](int64_t top, int64_t bot, std::vector<int64_t>& in) {
+                return avx512 ? scan_down_avx512(sa, jt, top, bot, in)
+                              : scan_down_scalar(sa, jt, top, bot, in);
             };
             int64_t hit = -1;
             const int64_t len = hi - lo + 1;
+            int used = 1;  // shares whose inside-joiners are kept, from the top
+            for (auto& v : inside) v.clear();
             if (nt == 1 || len < 4 * nt) {
-                hit = scan(hi, lo);
+                hit = scan(hi, lo, inside[0]);
             } else {
                 pool.run([&](int tid) {
                     const int64_t per = (len + nt - 1) / nt;
                     const int64_t top = hi - (int64_t)tid * per;
                     const int64_t bot = top - per + 1 > lo ? top - per + 1 : lo;
-                    found[(size_t)tid] = top >= bot ? scan(top, bot) : -1;
+                    found[(size_t)tid] = top >= bot ? scan(top, bot, inside[(size_t)tid]) : -1;
                 });
+                // the shares run from the top down: the first share that
+                // found a growing joiner ends the stretch
+                used = nt;
                 for (int k = 0; k < nt; ++k)
-                    if (found[(size_t)k] > hit) hit = found[(size_t)k];
+                    if (found[(size_t)k] >= 0) {
+                        hit = found[(size_t)k];
+                        used = k + 1;
+                        break;
+                    }
             }
+            // Joiners inside the pattern above `hit` (or in the whole stretch),
+            // in visiting order, with the reference's swap-removes: each moves
+            // a row from above (already visited) into the freed position.
+            for (int k = 0; k < used; ++k)
+                for (const int64_t pos : inside[(size_t)k]) {
+                    perm[out++] = (I)un[(size_t)pos];
+                    un[(size_t)pos] = un[(size_t)(n_un - 1)];
+                    --n_un;
+                }
             if (hit < 0) {
                 hi = lo - 1;
                 stretch *= 2;

@@ -368,6 +368,22 @@ constexpr int kPairRows = 64;    // bitmap method: rows i per workgroup
 constexpr int kPairTile = 128;   // rows j per LDS tile
 constexpr int kHashSlots = 16384;
 
+// The partner counts of a close pair (i, j) as they stand (relaxed loads,
+// possibly stale), and the appends.  pn[i] counts row i's partners and the
+// first kPartnerCap are listed; a count past the cap only marks the list
+// overflowed, so a row whose count already reads past it is not added to
+// again (stale reads just let an add happen).  Rows with thousands of
+// partners would otherwise serialize on their counters.
+__device__ __forceinline__ int partner_count(const int32_t* pn, int i)
+{
+    return __hip_atomic_load(pn + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void add_partner(int32_t* pn, int32_t* partners, int i, int j)
+{
+    const int k = atomicAdd(&pn[i], 1);
+    if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
+}
+
 // All pairs by bitmap popcounts (row bitmaps of at most MAXW words).
 // 256 threads: 64 rows i, four threads per row splitting each tile; the
 // row tiles j are dealt over gridDim.y workgroups.  Each pair is tested once, as
@@ -421,10 +437,8 @@ __global__ __launch_bounds__(256) void partners_bitmap_kernel(const uint64_t* __
 #pragma unroll
             for (int w = 0; w < MAXW; ++w) inter += __popcll(q[w] & tile[jj * MAXW + w]);
             if (jt.close(inter, qc + qj - inter)) {  // partnership is symmetric
-                const int k = atomicAdd(&pn[i], 1);
-                if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
-                const int k2 = atomicAdd(&pn[j], 1);
-                if (k2 < kPartnerCap) partners[(int64_t)j * kPartnerCap + k2] = i;
+                if (partner_count(pn, i) <= kPartnerCap) add_partner(pn, partners, i, j);
+                if (partner_count(pn, j) <= kPartnerCap) add_partner(pn, partners, j, i);
             }
         }
     }
@@ -579,6 +593,25 @@ __global__ __launch_bounds__(256, 3) void partners_gram_kernel(const uint64_t* _
         chunk.template operator()<3>();
     }
 
+    // no candidate in the whole quarter (the usual case): done
+    bool any = false;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) any |= acc[m][n][r] >= 0;
+    if (!__any(any)) return;
+    // the partner counts of the quarter's rows as the epilogue starts (they
+    // only grow): pairs whose two lists had overflowed by then are skipped
+    // without a read; the others read the count again before an add
+    int pn_i[4][4], pn_j[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pn_i[m][r] = partner_count(pn, min((int)i0 + 16 * m + 4 * g + r, M - 1));
+        pn_j[m] = partner_count(pn, min((int)j0 + 16 * m + li, M - 1));
+    }
     // every pair of the quarter has i < j < M (uniform)
     const bool interior = j0 >= i0 + 64 && j0 + 64 <= M;
 #pragma unroll
@@ -593,12 +626,13 @@ __global__ __launch_bounds__(256, 3) void partners_gram_kernel(const uint64_t* _
                 const int i = (int)i0 + 16 * m + 4 * g + r;
                 const int j = (int)j0 + 16 * n + li;
                 if (!interior && (i >= M || j >= M || j <= i)) continue;
+                // both lists already overflowed: nothing to add
+                const int ni = pn_i[m][r], nj = pn_j[n];
+                if (ni > kPartnerCap && nj > kPartnerCap) continue;
                 const int ci = lcount[il0 + 16 * m + 4 * g + r], cj = lcount[jl0 + 16 * n + li];
                 if (jt.close(inter, ci + cj - inter)) {  // partnership is symmetric
-                    const int k = atomicAdd(&pn[i], 1);
-                    if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
-                    const int k2 = atomicAdd(&pn[j], 1);
-                    if (k2 < kPartnerCap) partners[(int64_t)j * kPartnerCap + k2] = i;
+                    if (ni <= kPartnerCap && partner_count(pn, i) <= kPartnerCap) add_partner(pn, partners, i, j);
+                    if (nj <= kPartnerCap && partner_count(pn, j) <= kPartnerCap) add_partner(pn, partners, j, i);
                 }
             }
 }
@@ -729,6 +763,9 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     __shared__ int32_t s_blk[kClThreads];      // touch: blocks of the current chunk
     __shared__ int64_t s_pre[kClThreads + 1];  // touch: their list offsets
     __shared__ uint8_t s_flag[kClThreads];
+    __shared__ int32_t s_rank[kClThreads];     // commit: visiting rank of each window position
+    __shared__ int32_t s_nxt[kClThreads];      // commit: move chains over the positions past the new end
+    __shared__ int32_t s_val[kClThreads];
 
     const int t = threadIdx.x;
     const int M = (int)a.M;
@@ -808,6 +845,71 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
         return block_max(key, red);
     };
 
+    // Commit the rows at the window positions hi - t with `flag` set, in
+    // visiting order (descending position), with the reference's
+    // swap-removes -- the j-th commit (j = 1, 2, ...) moves the row then at
+    // position n0 - j, the end of `un`, into the freed position -- computed
+    // in parallel.  With k commits the new end is nf = n0 - k, every move
+    // source lies in [nf, n0), and a freed position below nf ends up with
+    // the row its source held at that time: the source's own row if it was
+    // not committed, else (it was freed earlier, as the j'-th commit) the row
+    // that came from n0 - j', and so on up.  Those chains climb [nf, n0),
+    // so pointer jumping over k slots resolves them in log2(k) + 1 rounds.
+    auto commit_flagged = [&](int hi, bool flag) {
+        const int at = hi - t;
+        int64_t total;
+        const int rank = (int)block_exscan64(flag ? 1 : 0, &total, red64);  // t ascending = position descending
+        const int k = (int)total;
+        if (k == 0) return;
+        const int n0 = n_un, nf = n0 - k;
+        int32_t row = -1;
+        if (flag) {
+            row = a.un[at];
+            perm[out + rank] = (I)row;
+            s_rank[t] = rank;
+        }
+        s_flag[t] = flag ? 1 : 0;
+        __syncthreads();
+        if (t < k) {  // slot t: position q = nf + t
+            const int q = nf + t;
+            const int tw = hi - q;  // its window slot, when q <= hi (q >= nf > hi - kClThreads)
+            int nx = -1;
+            if (tw >= 0 && s_flag[tw]) {
+                const int src = n0 - 1 - s_rank[tw];  // the source of q's own commit
+                nx = src == q ? -1 : src - nf;         // src == q: q was the end itself, popped
+            } else {
+                s_val[t] = a.un[q];
+            }
+            s_nxt[t] = nx;
+        }
+        __syncthreads();
+        for (int len = 1; len <= k; len <<= 1) {
+            int nx = -1, v = 0;
+            if (t < k) {
+                nx = s_nxt[t];
+                if (nx >= 0) {
+                    v = s_val[nx];
+                    nx = s_nxt[nx];
+                }
+            }
+            __syncthreads();
+            if (t < k && s_nxt[t] >= 0) {
+                s_val[t] = v;
+                s_nxt[t] = nx;
+            }
+            __syncthreads();
+        }
+        if (flag && at < nf) {
+            const int32_t v = s_val[n0 - 1 - rank - nf];  // from the source of this commit
+            a.un[at] = v;
+            a.pos[v] = at;
+        }
+        if (flag) a.pos[row] = -1;
+        out += k;
+        n_un = nf;
+        phase_sync();
+    };
+
     if (engine == kEngineScan) {
         while (n_un > 0) {
             singleton_runs();
@@ -831,6 +933,8 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
             phase_sync();
             while (hi >= 0) {
                 const int at = hi - t;
+                // joiners: 2 at + 1 when q lies inside the pattern (joining
+                // leaves it unchanged), 2 at when q grows it
                 int key = -1;
                 if (at >= 0) {
                     const int c = a.un[at];
@@ -844,10 +948,21 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
                             inter += __popcll(x & y);
                             uni += __popcll(x | y);
                         }
-                        if (jt.close(inter, uni)) key = at;
+                        if (jt.close(inter, uni)) key = 2 * at + (inter == qc ? 1 : 0);
                     }
                 }
-                const int best = block_max(key, red);
+                const int top = block_max(key, red);
+                int best = top < 0 ? -1 : top >> 1;  // the first joiner in visiting order
+                if (top >= 0 && (top & 1)) {
+                    // Joiners inside the pattern leave it as it is, so every joiner
+                    // down to the first one that grows it (best, or the window's
+                    // end) was tested against the pattern it meets: thread 0
+                    // commits those inside it in visiting order, with the
+                    // reference's swap-removes (a row from above moves into each
+                    // freed position), and best, if any, is committed below.
+                    best = block_max((key >= 0 && !(key & 1)) ? key >> 1 : -1, red);
+                    commit_flagged(hi, key >= 0 && (key & 1) && (key >> 1) > best);
+                }
                 if (best < 0) {
                     hi -= kClThreads;
                     continue;
@@ -931,28 +1046,7 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
             // position i moves in a row from above i, already visited.
             for (int hi = n_un - 1; hi >= 0; hi -= kClThreads) {
                 const int at = hi - t;
-                s_flag[t] = (at >= 0 && a.count[a.un[at]] == 0) ? 1 : 0;
-                __syncthreads();
-                if (t == 0) {
-                    int o = out, n = n_un;
-                    for (int k = 0; k < kClThreads && hi - k >= 0; ++k) {
-                        if (!s_flag[k]) continue;
-                        const int i = hi - k;
-                        const int r = a.un[i];
-                        perm[o++] = (I)r;
-                        a.pos[r] = -1;
-                        const int moved = a.un[n - 1];
-                        a.un[i] = moved;
-                        a.pos[moved] = i;
-                        --n;
-                    }
-                    red[0] = o;
-                    red[1] = n;
-                }
-                phase_sync();
-                out = red[0];
-                n_un = red[1];
-                __syncthreads();
+                commit_flagged(hi, at >= 0 && a.count[a.un[at]] == 0);
             }
             continue;
         }
@@ -1270,7 +1364,8 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
 
 bool clustering_device_supported(int64_t M, int64_t K, int64_t block_width)
 {
-    if (block_width <= 0 || M >= (int64_t)1 << 31) return false;
+    // row positions are doubled in the scan's joiner keys: M < 2^30
+    if (block_width <= 0 || M >= (int64_t)1 << 30) return false;
     const int64_t Kb = (K + block_width - 1) / block_width;
     if (Kb > kMaxGpuBlocks) return false;
     const int64_t W = Kb > 0 ? (Kb + 63) / 64 : 1;
