@@ -366,7 +366,7 @@ __global__ void status_kernel(const int64_t* __restrict__ total, const int* __re
 constexpr int kPartnerCap = 32;
 constexpr int kPairRows = 64;    // bitmap method: rows i per workgroup
 constexpr int kPairTile = 128;   // rows j per LDS tile
-constexpr int kHashSlots = 16384;
+constexpr int kHashSlots = 8192;
 
 // The partner counts of a close pair (i, j) as they stand (relaxed loads,
 // possibly stale), and the appends.  pn[i] counts row i's partners and the
@@ -638,10 +638,12 @@ __global__ __launch_bounds__(256, 3) void partners_gram_kernel(const uint64_t* _
 }
 
 // Pairs through the per-block row lists: one workgroup per row i counts
-// |q_i & q_j| for the rows j it meets in an LDS hash table.  Only rows whose
+// |q_i & q_j| for the rows j it meets in an LDS hash table, each wave
+// walking the row lists of every 16th block of row i.  Only rows whose
 // popcount bound allows a join are inserted; a row whose table would pass
 // half full, and empty rows (their partners are the other empty rows, which
-// share no block), get pn = -1.
+// share no block), get pn = -1.  The filled slots are listed, so a row reads
+// and clears only those.
 __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64_t* __restrict__ rb_start,
                                                              const int32_t* __restrict__ rb,
                                                              const int64_t* __restrict__ bl_start,
@@ -651,21 +653,21 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
 {
     __shared__ int32_t hkey[kHashSlots];
     __shared__ int32_t hval[kHashSlots];
-    __shared__ int32_t s_blk[1024];
-    __shared__ int64_t s_pre[1024];
-    __shared__ int64_t red64[kClWaves];
+    __shared__ uint16_t s_used[kHashSlots / 2];  // the slots a row filled, while it fits
     __shared__ int s_n, s_over, s_np;
     const int t = threadIdx.x;
     const JaccardTest jt(thr);
+    // the table starts empty and each row leaves it empty: through its list
+    // of filled slots, or wholly when the row overflowed
+    for (int h = t; h < kHashSlots; h += 1024) {
+        hkey[h] = -1;
+        hval[h] = 0;
+    }
     for (int i = blockIdx.x; i < M; i += gridDim.x) {
         const int qi = count[i];
         if (qi == 0) {
             if (t == 0) pn[i] = -1;
             continue;
-        }
-        for (int h = t; h < kHashSlots; h += 1024) {
-            hkey[h] = -1;
-            hval[h] = 0;
         }
         if (t == 0) {
             s_n = 0;
@@ -673,28 +675,15 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
             s_np = 0;
         }
         __syncthreads();
+        // each wave takes every 16th block of the row and walks its row list
+        // with its lanes (contiguous reads of bl_rows)
         const int64_t rs = rb_start[i];
-        for (int c0 = 0; c0 < qi; c0 += 1024) {
-            // the row's list entries, 1024 blocks at a time, as one flat range
-            const int nb = qi - c0 < 1024 ? qi - c0 : 1024;
-            int64_t len = 0;
-            if (t < nb) {
-                const int32_t b = rb[rs + c0 + t];
-                s_blk[t] = b;
-                len = bl_start[b + 1] - bl_start[b];
-            }
-            int64_t total;
-            const int64_t ex = block_exscan64(len, &total, red64);
-            if (t < nb) s_pre[t] = ex;
-            __syncthreads();
-            for (int64_t e = t; e < total; e += 1024) {
-                int lo = 0, hi = nb - 1;  // last block with s_pre <= e
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (s_pre[mid] <= e) lo = mid;
-                    else hi = mid - 1;
-                }
-                const int32_t j = bl_rows[bl_start[s_blk[lo]] + (e - s_pre[lo])];
+        const int wave = t >> 6, lane = t & 63;
+        for (int c = wave; c < qi; c += kClWaves) {
+            const int32_t b = rb[rs + c];
+            const int64_t b0 = bl_start[b], b1 = bl_start[b + 1];
+            for (int64_t e = b0 + lane; e < b1; e += 64) {
+                const int32_t j = bl_rows[e];
                 if (j == i || s_over) continue;
                 const int qj = count[j];
                 const int mn = qj < qi ? qj : qi, mx = qj < qi ? qi : qj;
@@ -703,24 +692,35 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
                 for (int probe = 0; probe < kHashSlots; ++probe) {
                     const int32_t old = atomicCAS(&hkey[h], -1, j);
                     if (old == -1 || old == j) {
-                        if (old == -1 && atomicAdd(&s_n, 1) >= kHashSlots / 2) s_over = 1;
+                        if (old == -1) {
+                            const int k = atomicAdd(&s_n, 1);
+                            if (k < kHashSlots / 2) s_used[k] = (uint16_t)h;
+                            else s_over = 1;
+                        }
                         atomicAdd(&hval[h], 1);
                         break;
                     }
                     h = (h + 1) & (kHashSlots - 1);
                 }
             }
-            __syncthreads();
         }
+        __syncthreads();
         if (!s_over) {
-            for (int h = t; h < kHashSlots; h += 1024) {
+            for (int k = t; k < s_n; k += 1024) {
+                const int h = s_used[k];
                 const int32_t j = hkey[h];
-                if (j < 0) continue;
                 const int inter = hval[h];
+                hkey[h] = -1;
+                hval[h] = 0;
                 if (jt.close(inter, qi + count[j] - inter)) {
-                    const int k = atomicAdd(&s_np, 1);
-                    if (k < kPartnerCap) partners[(int64_t)i * kPartnerCap + k] = j;
+                    const int np = atomicAdd(&s_np, 1);
+                    if (np < kPartnerCap) partners[(int64_t)i * kPartnerCap + np] = j;
                 }
+            }
+        } else {
+            for (int h = t; h < kHashSlots; h += 1024) {
+                hkey[h] = -1;
+                hval[h] = 0;
             }
         }
         __syncthreads();
