@@ -1257,8 +1257,9 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     int64_t* const status = reinterpret_cast<int64_t*>(base + o_status);
     hipLaunchKernelGGL(status_kernel, dim3(1), dim3(64), 0, s, rb_start + M, bad, status);
     XSPMM_LAUNCH_CHECK();
-    // pinned, so that the copy does not hold the host (one buffer per host
-    // thread, kept for the thread's life; a call reads it before returning)
+    // pinned, so that the copy does not hold the host: 16 bytes allocated
+    // once per host thread and never freed (a call reads them before it
+    // returns, so calls on one thread never share them)
     thread_local int64_t* h_status = nullptr;
     if (!h_status) XSPMM_HIP_CHECK(hipHostMalloc((void**)&h_status, 2 * sizeof(int64_t), hipHostMallocDefault));
     XSPMM_HIP_CHECK(hipMemcpyAsync(h_status, status, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, s));
