@@ -799,36 +799,51 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
     int n_un = M;  // every thread holds the same loop state
     int out = 0;
 
-    // Clusters of one, up to 1024 at a time.  The next seeds are un[n_un-1],
+    // Clusters of one, up to 4096 at a time.  The next seeds are un[n_un-1],
     // un[n_un-2], ... for as long as each stays alone, and the partner lists
     // decide that up front: the seed at position `at` is alone iff it has a
     // list and none of its partners is unclustered below `at` (partners above
     // `at` are the seeds before it, clustered by its turn).  The longest run
-    // of such seeds is committed at once.
+    // of such seeds is committed at once.  Each thread takes kRunSeeds seeds
+    // per round (offsets t + 1024 u from the end) and reads their rows and
+    // partner counts before any partner list.
+    constexpr int kRunSeeds = 4;
+    constexpr int kRun = kRunSeeds * kClThreads;
     auto singleton_runs = [&]() {
         if (!a.pn) return;
         while (n_un > 0) {
-            const int at = n_un - 1 - t;
-            int s = -1;
-            bool alone = false;
-            if (at >= 0) {
-                s = a.un[at];
-                const int np = a.pn[s];
-                alone = np >= 0 && np <= kPartnerCap;
-                for (int e = 0; alone && e < np; ++e) {
-                    const int pr = a.pos[a.partners[(int64_t)s * kPartnerCap + e]];
+            int s[kRunSeeds], np[kRunSeeds];
+#pragma unroll
+            for (int u = 0; u < kRunSeeds; ++u) {
+                const int at = n_un - 1 - (t + kClThreads * u);
+                s[u] = at >= 0 ? a.un[at] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kRunSeeds; ++u) np[u] = s[u] >= 0 ? a.pn[s[u]] : -1;
+            int first = kRun;  // this thread's first offset whose seed is not alone
+#pragma unroll
+            for (int u = 0; u < kRunSeeds; ++u) {
+                const int k = t + kClThreads * u, at = n_un - 1 - k;
+                bool alone = s[u] >= 0 && np[u] >= 0 && np[u] <= kPartnerCap;
+                for (int e = 0; alone && e < np[u]; ++e) {
+                    const int pr = a.pos[a.partners[(int64_t)s[u] * kPartnerCap + e]];
                     if (pr >= 0 && pr < at) alone = false;
                 }
+                if (!alone && k < first) first = k;
             }
-            const int run = -block_max(alone ? -kClThreads : -t, red);  // first seed not alone
-            if (t < run) {
-                perm[out + t] = (I)s;
-                a.pos[s] = -1;
+            const int run = -block_max(-first, red);  // the first seed not alone
+#pragma unroll
+            for (int u = 0; u < kRunSeeds; ++u) {
+                const int k = t + kClThreads * u;
+                if (k < run) {
+                    perm[out + k] = (I)s[u];
+                    a.pos[s[u]] = -1;
+                }
             }
             out += run;
             n_un -= run;
             phase_sync();
-            if (run < kClThreads) return;
+            if (run < kRun) return;
         }
     };
 
