@@ -1154,17 +1154,6 @@ __global__ __launch_bounds__(kClThreads) void cluster_kernel(ClusterArgs a, I* _
 
 }  // namespace
 
-// Offsets of 256-byte aligned pieces of one allocation
-struct Carve {
-    size_t end = 0;
-    size_t take(size_t bytes)
-    {
-        const size_t at = (end + 255) & ~size_t(255);
-        end = at + bytes;
-        return at;
-    }
-};
-
 template <typename I>
 void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
                                float dist_thresh, int64_t block_width, I* perm, hipStream_t s,

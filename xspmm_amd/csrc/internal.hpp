@@ -70,6 +70,25 @@ private:
     hipStream_t s_ = nullptr;
 };
 
+// Offsets of 256-byte aligned pieces of one allocation (one stream-ordered
+// allocation costs less host time than several).
+struct Carve {
+    size_t end = 0;
+    size_t take(size_t bytes)
+    {
+        const size_t at = (end + 255) & ~size_t(255);
+        end = at + bytes;
+        return at;
+    }
+};
+
+// A piece of such an allocation
+struct Piece {
+    char* p;
+    template <typename U>
+    U* as() const { return reinterpret_cast<U*>(p); }
+};
+
 // A HIP event without timing, destroyed with its scope.
 class EventHandle {
 public:
@@ -126,42 +145,60 @@ private:
     std::vector<Scratch> owned_;
 };
 
-// Elapsed time of a stage bracketed by HIP events on stream s; stop() waits
-// for the stage and writes milliseconds.  A disabled timer does nothing.
+// Elapsed times of stages bracketed by HIP events on stream s.  start() and
+// stop() only record the events, so the host goes on to the next stage
+// while the GPU runs this one; finish() waits for the last stop and writes
+// each stage's milliseconds.  Host work inside a bracket still counts: the
+// stop event is recorded after it, and the stream idles meanwhile.  A
+// disabled timer does nothing.
 class StageTimer {
 public:
-    StageTimer(bool on, hipStream_t s) : on_(on), s_(s) {
-        if (on_) {
-            XSPMM_HIP_CHECK(hipEventCreate(&a_));
-            XSPMM_HIP_CHECK(hipEventCreate(&b_));
-        }
-    }
+    StageTimer(bool on, hipStream_t s) : on_(on), s_(s) {}
     ~StageTimer() {
-        if (on_) {
-            (void)hipEventDestroy(a_);
-            (void)hipEventDestroy(b_);
+        for (auto& st : stages_) {
+            (void)hipEventDestroy(st.a);
+            (void)hipEventDestroy(st.b);
         }
     }
     StageTimer(const StageTimer&) = delete;
     StageTimer& operator=(const StageTimer&) = delete;
     void start() {
-        if (on_) XSPMM_HIP_CHECK(hipEventRecord(a_, s_));
+        if (!on_) return;
+        Stage st;
+        XSPMM_HIP_CHECK(hipEventCreate(&st.a));
+        if (hipEventCreate(&st.b) != hipSuccess) {
+            (void)hipEventDestroy(st.a);
+            XSPMM_HIP_CHECK(hipGetLastError());
+            throw std::runtime_error("HIP Error: hipEventCreate failed");
+        }
+        stages_.push_back(st);
+        XSPMM_HIP_CHECK(hipEventRecord(st.a, s_));
     }
     void stop(double* out) {
-        if (!on_) return;
-        XSPMM_HIP_CHECK(hipEventRecord(b_, s_));
-        XSPMM_HIP_CHECK(hipEventSynchronize(b_));
-        float ms = 0.f;
-        XSPMM_HIP_CHECK(hipEventElapsedTime(&ms, a_, b_));
-        *out = (double)ms;
+        if (!on_ || stages_.empty()) return;
+        Stage& st = stages_.back();
+        XSPMM_HIP_CHECK(hipEventRecord(st.b, s_));
+        st.out = out;
+    }
+    void finish() {
+        for (auto& st : stages_) {
+            if (!st.out) continue;
+            XSPMM_HIP_CHECK(hipEventSynchronize(st.b));
+            float ms = 0.f;
+            XSPMM_HIP_CHECK(hipEventElapsedTime(&ms, st.a, st.b));
+            *st.out = (double)ms;
+        }
     }
 
 private:
+    struct Stage {
+        hipEvent_t a = nullptr, b = nullptr;
+        double* out = nullptr;
+    };
     bool on_;
     hipStream_t s_;
-    hipEvent_t a_ = nullptr, b_ = nullptr;
+    std::vector<Stage> stages_;
 };
-
 
 // ---------------------------------------------------------------------------
 // Kernel launchers (all enqueue on `s`; none synchronizes unless stated).

@@ -10,11 +10,12 @@
 // greedy on copies of row_ptr/col_ind, as the reference does; with
 // XSPMM_CLUSTER_DEVICE=gpu it runs the GPU engine instead (the same
 // permutation), within that engine's shape limits.  Each timed stage is
-// bracketed by HIP events on the pipeline stream and waited for, so host work
-// inside a bracket counts too (the reference's HipTimer does the same).
+// bracketed by HIP events on the pipeline stream, so host work inside a
+// bracket counts too (the reference's HipTimer does the same); the events
+// are read once the pipeline has drained instead of after each stage.
 // Differences from the reference, with identical results: C / C_temp are not
-// memset first (the SpMM overwrites every element), temporaries come from the
-// stream-ordered pool instead of hipMalloc/hipFree and are all taken before
+// memset first (the SpMM overwrites every element), temporaries come from one
+// stream-ordered allocation instead of hipMalloc/hipFree pairs, taken before
 // the first stage (the BCSR arrays sized from the bound min(nnz, Mb * Kb), so
 // the conversion needs no host round trip between its count and its fill),
 // and permuted row_ptr[M] is the sum of the gathered lengths (equal to nnz
@@ -84,18 +85,25 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     // the conversion's count and fill run back to back and nnzb is read once,
     // after the fill.
     const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(nnz, Mb * Kb));
-    Scratch d_perm, nrp, nci, nvals, c_tmp;
+    // all in one allocation
+    Carve cv;
+    size_t o_perm = 0, o_nrp = 0, o_nci = 0, o_nvals = 0, o_ctmp = 0;
     if (optimize_pattern) {
-        d_perm = Scratch((size_t)(M > 0 ? M : 1) * sizeof(I), s);
-        nrp = Scratch((size_t)(M + 1) * sizeof(I), s);
-        nci = Scratch((size_t)(nnz > 0 ? nnz : 1) * sizeof(I), s);
-        nvals = Scratch((size_t)(nnz > 0 ? nnz : 1) * sizeof(T), s);
-        c_tmp = Scratch((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float), s);
+        o_perm = cv.take((size_t)(M > 0 ? M : 1) * sizeof(I));
+        o_nrp = cv.take((size_t)(M + 1) * sizeof(I));
+        o_nci = cv.take((size_t)(nnz > 0 ? nnz : 1) * sizeof(I));
+        o_nvals = cv.take((size_t)(nnz > 0 ? nnz : 1) * sizeof(T));
+        o_ctmp = cv.take((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float));
     }
-    Scratch brp((size_t)(Mb + 1) * sizeof(I), s);
-    Scratch bci((size_t)cap * sizeof(I), s);
-    Scratch bvals((size_t)cap * 256 * sizeof(T), s);
-    Scratch err(sizeof(int), s);
+    const size_t o_brp = cv.take((size_t)(Mb + 1) * sizeof(I));
+    const size_t o_bci = cv.take((size_t)cap * sizeof(I));
+    const size_t o_bvals = cv.take((size_t)cap * 256 * sizeof(T));
+    const size_t o_err = cv.take(sizeof(int));
+    Scratch tmp(cv.end, s);
+    char* const base = tmp.as<char>();
+    const Piece d_perm{base + o_perm}, nrp{base + o_nrp}, nci{base + o_nci}, nvals{base + o_nvals},
+        c_tmp{base + o_ctmp}, brp{base + o_brp}, bci{base + o_bci}, bvals{base + o_bvals},
+        err{base + o_err};
 
     // the stage's CSR: the caller's, or the permuted copy
     const I* crp = rp;
@@ -143,6 +151,8 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     }
     if (timed) total.stop(&tm[5]);
     XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    step.finish();
+    total.finish();
 }
 
 #define XSPMM_INST_PIPE(T, I)                                                                 \

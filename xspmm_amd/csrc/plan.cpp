@@ -119,6 +119,8 @@ public:
         if (tm) step.stop(&tm[2]);
         if (tm) total.stop(&tm[5]);
         XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+        step.finish();
+        total.finish();
     }
 
     // Packed column batches: the batch kernel's batches, formed once.  Kept
