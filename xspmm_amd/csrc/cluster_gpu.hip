@@ -317,19 +317,24 @@ __global__ __launch_bounds__(kPrepThreads) void block_counts_kernel(const uint64
 }
 
 // Row lists per block: bl_rows[bl_start[b] ...] (order within a list is free).
+// Per-block row lists, each entry with its row's block count beside it
+// (bl_cnt), so that a walk over a list reads both contiguously.
 __global__ __launch_bounds__(kPrepThreads) void block_lists_kernel(int64_t M,
                                                                    const int64_t* __restrict__ rb_start,
                                                                    const int32_t* __restrict__ rb,
                                                                    const int64_t* __restrict__ bl_start,
-                                                                   int32_t* bl_fill, int32_t* bl_rows)
+                                                                   int32_t* bl_fill, int32_t* bl_rows,
+                                                                   int32_t* bl_cnt)
 {
     const int lane = threadIdx.x & 63;
     const int64_t nw = (int64_t)gridDim.x * (kPrepThreads / 64);
     for (int64_t r = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) >> 6; r < M; r += nw) {
-        for (int64_t k = rb_start[r] + lane; k < rb_start[r + 1]; k += 64) {
+        const int64_t r0 = rb_start[r], r1 = rb_start[r + 1];
+        for (int64_t k = r0 + lane; k < r1; k += 64) {
             const int32_t b = rb[k];
             const int32_t at = atomicAdd(&bl_fill[b], 1);
             bl_rows[bl_start[b] + at] = (int32_t)r;
+            bl_cnt[bl_start[b] + at] = (int32_t)(r1 - r0);
         }
     }
 }
@@ -648,6 +653,7 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
                                                              const int32_t* __restrict__ rb,
                                                              const int64_t* __restrict__ bl_start,
                                                              const int32_t* __restrict__ bl_rows,
+                                                             const int32_t* __restrict__ bl_cnt,
                                                              const int32_t* __restrict__ count,
                                                              float thr, int32_t* pn, int32_t* partners)
 {
@@ -684,8 +690,8 @@ __global__ __launch_bounds__(1024) void partners_index_kernel(int M, const int64
             const int64_t b0 = bl_start[b], b1 = bl_start[b + 1];
             for (int64_t e = b0 + lane; e < b1; e += 64) {
                 const int32_t j = bl_rows[e];
+                const int qj = bl_cnt[e];
                 if (j == i || s_over) continue;
-                const int qj = count[j];
                 const int mn = qj < qi ? qj : qi, mx = qj < qi ? qi : qj;
                 if (!jt.may_close(mn, mx)) continue;
                 uint32_t h = ((uint32_t)j * 2654435761u) & (kHashSlots - 1);
@@ -1329,12 +1335,15 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
     int32_t* rb = nullptr;
     int64_t* bl_start = nullptr;
     int32_t* bl_rows = nullptr;
+    int32_t* bl_cnt = nullptr;
     if (need_lists) {
         Carve lc;
         const size_t o_rb = lc.take((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t));
         const size_t o_bls = lc.take((size_t)(nb + 1) * sizeof(int64_t));
         const size_t o_blr = lc.take((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t));
+        const size_t o_blc2 = lc.take((size_t)(nrb > 0 ? nrb : 1) * sizeof(int32_t));
         lists = Scratch(lc.end, s);
+        bl_cnt = reinterpret_cast<int32_t*>(lists.as<char>() + o_blc2);
         rb = reinterpret_cast<int32_t*>(lists.as<char>() + o_rb);
         bl_start = reinterpret_cast<int64_t*>(lists.as<char>() + o_bls);
         bl_rows = reinterpret_cast<int32_t*>(lists.as<char>() + o_blr);
@@ -1345,12 +1354,12 @@ void jaccard_clustering_device(int64_t M, int64_t K, int64_t nnz, const I* rp, c
         device_exclusive_scan(ArrayValue<int32_t>{bl_count}, nb, bl_start, s);
         XSPMM_HIP_CHECK(hipMemsetAsync(bl_count, 0, (size_t)nb * sizeof(int32_t), s));
         hipLaunchKernelGGL(block_lists_kernel, dim3(grid), dim3(kPrepThreads), 0, s, M, rb_start, rb,
-                           bl_start, bl_count, bl_rows);
+                           bl_start, bl_count, bl_rows, bl_cnt);
         XSPMM_LAUNCH_CHECK();
     }
     if (use_partners && !bitmap_partners) {
         hipLaunchKernelGGL(partners_index_kernel, dim3((unsigned)std::min<int64_t>(M, 1024)),
-                           dim3(1024), 0, s, (int)M, rb_start, rb, bl_start, bl_rows, count,
+                           dim3(1024), 0, s, (int)M, rb_start, rb, bl_start, bl_rows, bl_cnt, count,
                            dist_thresh, pn, partners);
         XSPMM_LAUNCH_CHECK();
     }
