@@ -16,7 +16,8 @@
 // below it -- the candidates above it were tested against the right pattern.
 // All threads keep the loop state (counts, positions) in registers as
 // identical copies: every decision comes out of a block reduction.  Thread 0
-// alone writes the shared arrays (permutation, positions).
+// writes a single commit to the shared arrays (permutation, positions); a
+// run of commits is written by all threads, each its own entries.
 //
 // Two engines, picked from the pattern statistics (or XSPMM_CLUSTER_ENGINE):
 //  * scan:  each step tests 1024 consecutive positions below the last commit
