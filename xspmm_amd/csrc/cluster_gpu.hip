@@ -21,7 +21,9 @@
 //
 // Two engines, picked from the pattern statistics (or XSPMM_CLUSTER_ENGINE):
 //  * scan:  each step tests 1024 consecutive positions below the last commit
-//           with popcounts of the row bitmaps (a popcount bound first);
+//           with popcounts of the row bitmaps (a popcount bound first), and
+//           commits every joiner down to the first one that grows the
+//           pattern (joiners whose rows lie inside it leave it unchanged);
 //  * index: only rows that share a block with the pattern can join (d = 1
 //           otherwise, and dist_thresh < 1), so the workgroup keeps
 //           |p & q_r| per row, raised through per-block row lists whenever a
@@ -30,10 +32,11 @@
 // Every loop of the clustering kernel ends: each commit removes a row and
 // lowers the scan limit, and each step without a commit lowers it by 1024.
 //
-// Preparation (all rows in parallel): row bitmaps by atomic OR, their
-// popcounts, each row's block list, the per-block row lists (counts,
-// exclusive scan, scatter) and each row's partners -- the rows close enough
-// to join it while the pattern is still its own.  A seed whose partners are
+// Preparation (all rows in parallel): row bitmaps by atomic OR (in LDS up to
+// 64 words per row), their popcounts, each row's block list, the per-block
+// row lists (counts, exclusive scan, scatter) and each row's partners --
+// the rows close enough to join it while the pattern is still its own, by
+// all pairs on the int8 matrix cores or through the row lists.  A seed whose partners are
 // all clustered forms a cluster of one without a scan, and any other seed
 // starts its scan at its highest-positioned partner.
 #include <cstdlib>
