@@ -17,8 +17,9 @@
 //
 //  * scan:  the reference loop with the candidate tests of a stretch of
 //           positions evaluated in parallel against the current pattern; the
-//           highest joining position is committed and the scan resumes below
-//           it.  A popcount bound (d >= 1 - min(|p|,|q|)/max(|p|,|q|), which is
+//           joiners down to the first one that grows the pattern are
+//           committed (those above it lie inside the pattern and leave it
+//           unchanged) and the scan resumes below it.  A popcount bound (d >= 1 - min(|p|,|q|)/max(|p|,|q|), which is
 //           monotone under float rounding) skips most bitmap work.
 //  * index: for 0 <= dist_thresh < 1 a row can only join a cluster whose
 //           pattern shares a block with it (d = 1 otherwise), or an empty
