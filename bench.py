@@ -49,6 +49,9 @@ WORKLOADS = {
 for _d in ("90", "50", "5", "0.5", "0.1"):
     WORKLOADS[f"banded{_d}"] = (f"examples/05 density sweep: banded 16384^2 at {_d}% "
                                 "(bandwidth density*K/2), fp16, B = ones, N=128, Tier-1")
+    WORKLOADS[f"banded{_d}_f32"] = (f"examples/05 density sweep as the reference runs it: banded "
+                                    f"16384^2 at {_d}% (bandwidth density*K/2), fp32, B = ones, "
+                                    "N=128, Tier-1")
 
 
 def host_threads() -> int:
@@ -105,8 +108,15 @@ def tier1_kernel(value_bytes, K, N, nnzb, Mb):
     xspmm_amd/csrc/spmm.hip: fp16 takes the GEMM-tiled kernel when every block
     is present, else the column-batch kernel when N % 8 == 0 and B and the
     block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL selects
-    another one)."""
+    another one; fp32 takes its column-batch kernel when N % 4 == 0 and B
+    fits 32-bit offsets and the grid has at least 512 workgroups of 128
+    columns, unless XSPMM_F32_KERNEL=tile or =batch forces one)."""
     if value_bytes == 4:
+        Kb = (K + 15) // 16
+        choice = os.environ.get("XSPMM_F32_KERNEL", "")
+        if (N % 4 == 0 and K * N * 4 <= 1 << 31 and Kb < 1 << 21 and choice != "tile"
+                and (choice == "batch" or Mb * ((N + 127) // 128) >= 512)):
+            return "spmm_f32_batch_kernel"
         return "spmm_f32_kernel"
     Kb = (K + 15) // 16
     if (nnzb == Mb * Kb and N % 8 == 0 and Mb * Kb * 512 < 1 << 31 and K * N * 2 < 1 << 31
@@ -121,22 +131,34 @@ def tier1_kernel(value_bytes, K, N, nnzb, Mb):
     return "pack_b_panels + spmm_f16_kernel"
 
 
+def _profile_json(name):
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
 def load_traffic(config):
     """HBM bytes per SpMM launch from the committed rocprofv3 counter runs
     (profiles/spmm_traffic.json): FETCH_SIZE and WRITE_SIZE in KiB per
     dispatch, each scaled by what the same counter reads for a plain copy of
     known size (`bench.py --calibrate-copy`).  None when not profiled."""
-    path = os.path.join(ROOT, "profiles", "spmm_traffic.json")
-    try:
-        with open(path) as f:
-            d = json.load(f)
-    except (OSError, ValueError):
-        return None
+    d = _profile_json("spmm_traffic.json")
     e = d.get("configs", {}).get(config)
     cal = d.get("calibration")
     if not e or not cal:
         return None
     return (e["fetch_kib"] * cal["fetch_scale"] + e["write_kib"] * cal["write_scale"]) * 1024.0
+
+
+def load_mfma_busy(config):
+    """Share of cycles the SpMM kernel's matrix cores were busy, from the
+    committed rocprofv3 counter run (profiles/spmm_mfma_busy.json:
+    SQ_VALU_MFMA_BUSY_CYCLES over the SIMD-cycles of the dispatch).  None when
+    not profiled."""
+    e = _profile_json("spmm_mfma_busy.json").get("configs", {}).get(config)
+    return e.get("mfma_busy") if e else None
 
 
 def calibrate_copy():
@@ -204,6 +226,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cluster", choices=("config", "on", "off"), default="config",
                     help="override the workload's clustering setting")
+    ap.add_argument("--dtype", choices=("config", "f16", "f32"), default="config",
+                    help="value type of A and B (default: the workload's own; the same "
+                         "draws rounded to the other type)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-pipeline", action="store_true")
     ap.add_argument("--no-vendor", action="store_true",
@@ -232,7 +257,10 @@ def main():
     X.load()
 
     print(f"[bench] generating {args.config}", file=sys.stderr, flush=True)
-    p = synth.CONFIGS[args.config](**({"N": args.n} if args.n else {}))
+    gen_kw = {"N": args.n} if args.n else {}
+    if args.dtype != "config":
+        gen_kw["dtype"] = np.float16 if args.dtype == "f16" else np.float32
+    p = synth.CONFIGS[args.config](**gen_kw)
     if args.cluster != "config":
         p.cluster = args.cluster == "on"
     M, K, N, nnz = p.M, p.K, p.N, p.nnz
@@ -315,7 +343,9 @@ def main():
     else:
         roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": achieved / HBM_PEAK_GBS}
-    traffic_key = args.config if args.n is None else f"{args.config}_n{args.n}"
+    traffic_key = args.config + ("" if args.n is None else f"_n{args.n}")
+    if args.dtype != "config" and not args.config.endswith("_" + args.dtype):
+        traffic_key += "_" + args.dtype
     roofline.update({"traffic": load_traffic(traffic_key), "kernel": tier1_kernel(sT, K, N, nnzb, Mb),
                      "alg_bytes_per_call": alg_bytes,
                      "padded_flops_per_call": 2.0 * nnzb * 256 * N})
@@ -409,7 +439,11 @@ def main():
         "hbm_gbs": achieved,
         "hbm_frac": achieved / HBM_PEAK_GBS,
         "padded_tflops": padded,
-        "mfma_frac": padded / mfma_peak,
+        # padded flops (every block x N) per second over the matrix-core peak;
+        # the column-batch kernels never execute the padded flops, so this is
+        # not a utilisation: mfma_busy is the counter-measured busy share
+        "padded_mfma_frac": padded / mfma_peak,
+        "mfma_busy": load_mfma_busy(traffic_key),
         "wall_s_timed_region": wall,
         "spot_check_rel_frob": spot,
         "prep": prep,

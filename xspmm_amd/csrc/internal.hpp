@@ -262,6 +262,15 @@ bool spmm_f16_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, c
                      const uint32_t* rows, const uint16_t* B, float* C, int64_t N,
                      const int32_t* order, const I* row_map, hipStream_t s);
 
+// Tier-1 fp32 column-batch SpMM (spmm_f32.hip): covers N % 4 == 0 with B and
+// C 16-byte aligned, K * N * 4 <= 2^31 and Kb < 2^21 (XSPMM_F32_KERNEL=tile
+// declines it); order and row_map as for bcsr_spmm_ex.
+bool spmm_f32_batch_covers(int64_t K, int64_t Kb, int64_t N, const void* B, const void* C);
+template <typename I>
+void bcsr_spmm_f32_batch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                         const float* bvals, const float* B, float* C, int64_t N,
+                         const int32_t* order, const I* row_map, hipStream_t s);
+
 // Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb);
 // row_map (null: rows in place) as for bcsr_spmm_ex.  Each tile checks that
 // its block-rows hold the canonical layout (block br * Kb + c has column c)

@@ -1389,6 +1389,18 @@ bool wide_batches(int64_t Mb, int64_t N)
     return Mb * ((N + 255) / 256) >= 1024;
 }
 
+// fp32: the column-batch kernel runs one workgroup per block-row and 128
+// columns; a grid shorter than this takes the tile kernel, which splits each
+// block-row over 8 waves and narrower column tiles.  XSPMM_F32_KERNEL=batch
+// forces the batch kernel (where it covers the shape), =tile the tile kernel.
+constexpr int64_t kF32BatchMinGroups = 512;
+
+bool f32_kernel_forced_batch()
+{
+    const char* e = std::getenv("XSPMM_F32_KERNEL");
+    return e && std::string(e) == "batch";
+}
+
 void check_shape(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, int64_t N)
 {
     if (M < 0 || K < 0 || Mb < 0 || Kb < 0 || nnzb < 0 || N < 0)
@@ -1600,9 +1612,22 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
         }
         XSPMM_LAUNCH_CHECK();
     } else {
-        if (row_map) return false;  // the fp32 kernel stores rows in place
         const float* v = reinterpret_cast<const float*>(bvals);
         const float* b = reinterpret_cast<const float*>(B);
+        // column batches (spmm_f32.hip) unless the grid is too short to keep
+        // the chip busy with one workgroup per block-row
+        if (spmm_f32_batch_covers(K, Kb, N, B, C) &&
+            (f32_kernel_forced_batch() || Mb * ((N + 127) / 128) >= kF32BatchMinGroups)) {
+            const int32_t* order = order_in;
+            if (!order && spmm_order_wanted(Mb)) {
+                int32_t* buf = arena.take_as<int32_t>((size_t)Mb);
+                spmm_dispatch_order<I>(brp, Mb, buf, s);
+                order = buf;
+            }
+            bcsr_spmm_f32_batch<I>(M, K, Mb, Kb, brp, bci, v, b, C, N, order, row_map, s);
+            return true;
+        }
+        if (row_map) return false;  // the fp32 tile kernel stores rows in place
         // 16-column tiles per wave: 4 (fewer B loads per block) unless that
         // leaves fewer than 512 workgroups, when narrower tiles spread the
         // block-rows over more CUs

@@ -1,0 +1,430 @@
+// spmm_f32.hip -- fp32 Tier-1 BCSR SpMM: column batches on v_mfma_f32_16x16x4f32.
+//
+// Semantics follow the reference tile kernel (src/common/spmm_math.hpp:20-146)
+// as instantiated for float (src/xspmm.cpp:102-114, unstructured_mtx_mul.hip:
+// 105-106): C[16 br : +16, :] = sum over the block-row's blocks of
+// A_blk * B[16 col : +16, :], fp32 accumulation, C overwritten, block-rows
+// without blocks give zeros.  Rows >= M are not stored; B rows >= K and
+// columns >= N contribute nothing.
+//
+// A 16x16 block of a sparse matrix usually holds a few non-zero columns (1.7
+// of 16 at the headline pattern), and only the B rows of those columns can
+// change C.  The fp32 matrix-core step v_mfma_f32_16x16x4f32 takes one K
+// index per 16-lane group (lane (i, k) holds A[i][k] and B[k][i]), so its four
+// K slots can be filled with any four non-zero block columns of the
+// block-row, from any blocks: all blocks of a block-row add into the same 16
+// rows of C.  Each wave of a workgroup takes every W-th block of its
+// block-row and
+//   1. streams the blocks (16 bytes per lane: lane (r, g) holds row r,
+//      columns 4g .. 4g+3; non-temporal loads, D blocks in flight) and, one
+//      vector load per ring pass, their block columns;
+//   2. forms the block's column mask from four ballots (one per column of a
+//      lane's quad; a column counts when any of its 16 entries is not +-0,
+//      so NaN and Inf count) and a few scalar operations;
+//   3. writes the block to a 4-block LDS ring (lane l writes bytes
+//      16 l .. 16 l + 15, layout [quad][row][4]) and appends its set columns to
+//      a batch of four K slots: slot k is held by lane group k, which records
+//      the slot's LDS column address and the byte offset of its B row;
+//   4. when four slots are set, closes the batch: multiplies the batch still
+//      in flight, has each lane read its A' entry A[r][col(k)] from the ring
+//      (one ds_read_b32) and issues this batch's B row loads: lane (n, k)
+//      loads B[row(k)][n0 + 64 q + 4 n .. +3] as one 16-byte load per 64
+//      columns, straight into MFMA B operands, so a batch's rows arrive while
+//      the next batch forms;
+//   5. the multiply issues one MFMA per float4 component j: component j of
+//      quad q covers C columns n0 + 64 q + 4 n + j (n = 0 .. 15).
+// A block whose 16 columns are all set is multiplied as it stands (four
+// steps, step s holding columns 4k + s, which lane (r, k) already holds),
+// with its 4 x 16 B rows loaded together.
+// The waves' partial tiles are summed through LDS in wave order and stored as
+// 16-byte rows.  Skipped columns would add exact zeros (products of +-0 and
+// finite B entries), so C equals the full product for finite B; a non-finite
+// B entry meets only columns that hold a non-zero A entry (0 * Inf is not
+// formed), as in the fp16 column-batch kernel.
+// grid = (block-rows, ceil(N / (64 NQ))); N % 4 == 0, B 16-byte aligned,
+// K * N * 4 <= 2^31, Kb < 2^21 (32-bit offsets within a row and into B).
+#include <cstdlib>
+#include <string>
+
+#include "internal.hpp"
+
+namespace xspmm {
+namespace detail {
+
+namespace {
+
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+// Buffer resource word 3 for raw (untyped, unswizzled) dword access on gfx9.
+constexpr int kRawBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer-load builtins: non-temporal (nt).
+constexpr int kNonTemporal = 2;
+// Blocks of the per-wave LDS ring.  A batch's slots come from at most four
+// consecutive non-empty blocks and the batch reads them when it closes, which
+// is before the fourth block after the oldest one is written; LDS operations
+// of one wave complete in order.
+constexpr int kRing = 4;
+constexpr int kRingBytes = kRing * 1024;
+// column mask of a block whose 16 columns all hold a non-zero entry
+constexpr uint64_t kAllColumns = 0x000f000f000f000full;
+
+#ifndef XSPMM_F32_PRIO
+#define XSPMM_F32_PRIO 1
+#endif
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             kRawBufferWord3);
+}
+
+__device__ __forceinline__ void set_prio(int level)
+{
+    switch (level) {
+    case 3: __builtin_amdgcn_s_setprio(3); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    default: __builtin_amdgcn_s_setprio(0); break;
+    }
+}
+
+// Column mask of a block from the ballots of "entry != 0" of the four
+// columns 4g + s (s = 0 .. 3) each lane group g holds: bit 16 g + s is set
+// when column 4g + s has a non-zero entry in any of its 16 rows.  Bit 15 of
+// each 16-bit group of ((b & 0x7fff...) + 0x7fff...) | b is the OR of the
+// group's bits (the low 15 bits cannot carry past bit 15).
+__device__ __forceinline__ uint64_t column_mask(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t b3)
+{
+    constexpr uint64_t kLow = 0x7fff7fff7fff7fffull;
+    constexpr uint64_t kTop = 0x8000800080008000ull;
+    auto any = [](uint64_t b) { return (((b & kLow) + kLow) | b) & kTop; };
+    return (any(b0) >> 15) | (any(b1) >> 14) | (any(b2) >> 13) | (any(b3) >> 12);
+}
+
+// Mask bits of the block columns c < lim (lim in 0 .. 16), in the layout of
+// column_mask.
+__device__ __forceinline__ uint64_t columns_below(uint32_t lim)
+{
+    uint64_t m = 0;
+    for (uint32_t g = 0; g < 4; ++g) {
+        const uint32_t c0 = 4 * g;
+        const uint32_t n = lim > c0 ? (lim - c0 < 4 ? lim - c0 : 4) : 0;
+        m |= (uint64_t)((1u << n) - 1u) << (16 * g);
+    }
+    return m;
+}
+
+// NQ: 64-column quads per workgroup (one 16-byte B load per quad and slot);
+// W: waves per workgroup; D: blocks in flight per wave.
+template <typename I, int NQ, int W, int D>
+__global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
+    const I* __restrict__ brp, const I* __restrict__ bci, const float* __restrict__ vals,
+    const float* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
+    int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map)
+{
+    static_assert(NQ == 1 || NQ == 2, "64 or 128 columns per workgroup");
+    static_assert(D >= 2 && D <= 8, "2 .. 8 blocks in flight per wave");
+    static_assert(W * D <= 64 * 8 / (int)sizeof(I), "index window exceeds a wave");
+    constexpr int kRedBytes = 16 * 64 * NQ * 4;  // one wave's partial tile
+    constexpr int kLdsBytes = W * (kRingBytes > kRedBytes ? kRingBytes : kRedBytes);
+    __shared__ __align__(16) unsigned char smem[kLdsBytes];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+
+    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    // a caller-supplied order holds a permutation of the block-rows; an id
+    // outside the grid is skipped rather than read past row_ptr
+    if ((uint64_t)br >= (uint64_t)gridDim.x) return;
+    const int64_t n0 = (int64_t)blockIdx.y * 64 * NQ;
+    const int64_t rs = brp[br];
+    const int64_t re = brp[br + 1];
+    const uint32_t nblk = (uint32_t)(re - rs);
+    // this wave's blocks: wave, wave + W, ... (wave-block q is row block wave + W q)
+    const uint32_t mine = nblk > (uint32_t)wave ? (nblk - (uint32_t)wave + W - 1) / W : 0u;
+
+    // reads past the row's blocks return zeros (an all-zero block is skipped)
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(vals + rs * 256, nblk * 1024u);
+    const __amdgpu_buffer_rsrc_t c_rsrc = make_rsrc(bci + rs, nblk * (uint32_t)sizeof(I));
+    const uint32_t b_bytes = (uint32_t)(K * N * 4);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
+    const uint32_t rowbytes = (uint32_t)(4 * N);
+    const uint32_t kb32 = (uint32_t)Kb;
+
+    unsigned char* const ring = smem + wave * kRingBytes;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
+    // lane l writes bytes 16 l .. 16 l + 15 of a ring block: [quad g][row li][4]
+    const uint32_t a_voff = (uint32_t)(li * 64 + g * 16) + (uint32_t)wave * 1024u;
+    const uint32_t ring_w = (uint32_t)lane * 16u;
+    // B loads: lane (li, g) covers columns n0 + 64 q + 4 li .. +3 of its slot's
+    // row; quads past N read nothing
+    uint32_t b_lane[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int64_t col = n0 + 64 * q + 4 * li;
+        b_lane[q] = col < N ? (uint32_t)(4 * col) : 0xffffffffu;
+    }
+    // index window of a ring pass: lane l holds dword l of the block columns
+    // of wave-blocks p .. p + D - 1 (int64: two dwords per block)
+    constexpr uint32_t kIdxDw = sizeof(I) / 4;
+    const uint32_t cw_off = (uint32_t)wave * (uint32_t)sizeof(I) +
+                            (uint32_t)(lane / kIdxDw) * (uint32_t)(W * sizeof(I)) +
+                            4u * (uint32_t)(lane % kIdxDw);
+
+    float4_t acc[NQ][4];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[q][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // the batch in flight: its A' entry and B operands
+    float ap = 0.f;
+    float4_t bq[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) bq[q] = float4_t{0.f, 0.f, 0.f, 0.f};
+    bool pending = false;  // a batch is in flight (wave-uniform)
+    uint32_t fill = 0;     // slots of the open batch (wave-uniform)
+    uint32_t ridx = 0;     // next ring block (wave-uniform)
+    uint32_t my_a = 0;     // this lane group's slot: LDS byte offset of its column in the ring
+    uint32_t my_b = 0;     // and the byte offset of its B row
+
+    auto multiply = [&](const float a, const float4_t (&b)[NQ]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[q][j], acc[q][j], 0, 0, 0);
+    };
+    // this lane's B operands of the row at byte offset `boff` (zeros when the
+    // slot is unused or the quad lies past N)
+    auto load_b = [&](float4_t (&b)[NQ], uint32_t boff, bool used) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const uint32_t off = (used && b_lane[q] != 0xffffffffu) ? boff + b_lane[q] : b_bytes;
+            b[q] = __builtin_bit_cast(float4_t,
+                                      __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+        }
+    };
+    // close the open batch of `cnt` slots: multiply the batch in flight, then
+    // read this one's A' entry from the ring (A' = 0 in unused slots) and
+    // issue its B row loads
+    auto close = [&](uint32_t cnt) __attribute__((always_inline)) {
+        if (pending) multiply(ap, bq);
+        const bool used = (uint32_t)g < cnt;
+        const float x = *(__attribute__((address_space(3))) const float*)(uintptr_t)(ring_lds + my_a +
+                                                                                     (uint32_t)li * 16u);
+        ap = used ? x : 0.f;
+        load_b(bq, my_b, used);
+        pending = true;
+    };
+
+    auto stage_a = [&](uint32_t q, float4_t& P) __attribute__((always_inline)) {
+        P = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                             a_rsrc, (int)(a_voff + q * (uint32_t)(W * 1024)), 0,
+                                             kNonTemporal));
+    };
+    auto load_cols = [&](uint32_t q) __attribute__((always_inline)) -> uint32_t {
+        return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+            c_rsrc, (int)(cw_off + q * (uint32_t)(W * sizeof(I))), 0, 0);
+    };
+
+    // block j of the ring pass whose index window is `win`
+    auto process = [&](const float4_t& P, uint32_t win, int j) __attribute__((always_inline)) {
+        uint32_t cb;
+        if constexpr (sizeof(I) == 4) {
+            cb = (uint32_t)__builtin_amdgcn_readlane((int)win, j);
+        } else {
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)win, 2 * j);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)win, 2 * j + 1);
+            cb = hi == 0u ? lo : 0xffffffffu;
+        }
+        uint64_t m = column_mask(__builtin_amdgcn_ballot_w64(P[0] != 0.f),
+                                 __builtin_amdgcn_ballot_w64(P[1] != 0.f),
+                                 __builtin_amdgcn_ballot_w64(P[2] != 0.f),
+                                 __builtin_amdgcn_ballot_w64(P[3] != 0.f));
+        // a block column outside the grid (malformed input) contributes
+        // nothing; so do the B rows >= K of a ragged last block column
+        if (cb >= kb32) m = 0;
+        if (m != 0 && (int64_t)cb * 16 + 16 > K) m &= columns_below((uint32_t)(K - (int64_t)cb * 16));
+        if (m == 0) return;
+        const uint32_t row0 = cb * 16u;
+        if (m == kAllColumns) {
+            // every column set: the block is its own four batches, step s
+            // holding columns 4k + s -- lane (r, k)'s own register s -- so it
+            // skips the ring.  The open batch closes first; the four steps'
+            // B rows load together and multiply after the batch in flight.
+            if (fill > 0u) {
+                close(fill);
+                fill = 0;
+            }
+            const uint32_t rb = (row0 + 4u * (uint32_t)g) * rowbytes;
+            float4_t t0[NQ], t1[NQ], t2[NQ], t3[NQ];
+            load_b(t0, rb, true);
+            load_b(t1, rb + rowbytes, true);
+            load_b(t2, rb + 2u * rowbytes, true);
+            load_b(t3, rb + 3u * rowbytes, true);
+            if (pending) multiply(ap, bq);
+            pending = false;
+            multiply(P[0], t0);
+            multiply(P[1], t1);
+            multiply(P[2], t2);
+            multiply(P[3], t3);
+            return;
+        }
+        const uint32_t base = ridx * 1024u;
+        *(__attribute__((address_space(3))) float4_t*)(uintptr_t)(ring_lds + base + ring_w) = P;
+        ridx = (ridx + 1u) & (kRing - 1u);
+        do {
+            const uint32_t p = (uint32_t)__builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t c = 4u * (p >> 4) + (p & 15u);
+            const uint32_t aoff = base + (c >> 2) * 256u + (c & 3u) * 4u;
+            const uint32_t boff = (row0 + c) * rowbytes;
+            if ((uint32_t)g == fill) {
+                my_a = aoff;
+                my_b = boff;
+            }
+            if (++fill == 4u) {
+                close(4u);
+                fill = 0;
+            }
+        } while (m != 0);
+    };
+
+    if (mine > 0) {
+        float4_t P0, P1, P2, P3, P4, P5, P6, P7;
+        uint32_t win = load_cols(0);
+        stage_a(0, P0);
+        stage_a(1, P1);
+        if constexpr (D > 2) stage_a(2, P2);
+        if constexpr (D > 3) stage_a(3, P3);
+        if constexpr (D > 4) stage_a(4, P4);
+        if constexpr (D > 5) stage_a(5, P5);
+        if constexpr (D > 6) stage_a(6, P6);
+        if constexpr (D > 7) stage_a(7, P7);
+        const uint32_t passes = (mine + D - 1) / D;
+        int level = -1;
+        for (uint32_t pass = 0; pass < passes; ++pass) {
+            const uint32_t q = pass * D;
+            if constexpr (XSPMM_F32_PRIO != 0) {
+                // waves furthest from done issue first, so the workgroups
+                // sharing a CU end together
+                const uint32_t rem = passes - pass;
+                const int lv = rem > 16u ? 3 : rem > 8u ? 2 : rem > 2u ? 1 : 0;
+                if (lv != level) {
+                    level = lv;
+                    set_prio(lv);
+                }
+            }
+            const uint32_t nwin = load_cols(q + D);
+            process(P0, win, 0);
+            stage_a(q + D, P0);
+            process(P1, win, 1);
+            stage_a(q + D + 1, P1);
+            if constexpr (D > 2) {
+                process(P2, win, 2);
+                stage_a(q + D + 2, P2);
+            }
+            if constexpr (D > 3) {
+                process(P3, win, 3);
+                stage_a(q + D + 3, P3);
+            }
+            if constexpr (D > 4) {
+                process(P4, win, 4);
+                stage_a(q + D + 4, P4);
+            }
+            if constexpr (D > 5) {
+                process(P5, win, 5);
+                stage_a(q + D + 5, P5);
+            }
+            if constexpr (D > 6) {
+                process(P6, win, 6);
+                stage_a(q + D + 6, P6);
+            }
+            if constexpr (D > 7) {
+                process(P7, win, 7);
+                stage_a(q + D + 7, P7);
+            }
+            win = nwin;
+        }
+        if (fill > 0u) close(fill);
+        if (pending) multiply(ap, bq);
+    }
+
+    // sum the waves' partial tiles in wave order and store C
+    __syncthreads();
+    float* const red = reinterpret_cast<float*>(smem);  // W x [16][64 NQ]
+    constexpr int kCols = 64 * NQ;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<float4_t*>(red + wave * 16 * kCols + (4 * g + i) * kCols + 64 * q + 4 * li) =
+                float4_t{acc[q][0][i], acc[q][1][i], acc[q][2][i], acc[q][3][i]};
+    __syncthreads();
+    for (int t = threadIdx.x; t < 16 * kCols / 4; t += 64 * W) {
+        const int row = t / (kCols / 4);
+        const int c4 = 4 * (t % (kCols / 4));
+        const int64_t grow = br * 16 + row;
+        const int64_t col = n0 + c4;
+        if (grow >= M || col >= N) continue;
+        float4_t v = *reinterpret_cast<const float4_t*>(red + row * kCols + c4);
+#pragma unroll
+        for (int w = 1; w < W; ++w) v += *reinterpret_cast<const float4_t*>(red + w * 16 * kCols + row * kCols + c4);
+        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+        *reinterpret_cast<float4_t*>(C + crow * N + col) = v;
+    }
+}
+
+// Four waves per workgroup (four workgroups per CU); blocks in flight per
+// wave: 6 at 128 columns (the 128-VGPR budget of four waves per SIMD), 8 at 64.
+template <typename I, int NQ>
+void launch_batch(dim3 grid, hipStream_t s, const I* brp, const I* bci, const float* v, const float* b,
+                  float* C, int64_t M, int64_t K, int64_t N, int64_t Kb, const int32_t* order,
+                  const I* row_map)
+{
+    constexpr int kW = 4;
+    constexpr int kD = NQ == 2 ? 6 : 8;
+    hipLaunchKernelGGL((spmm_f32_batch_kernel<I, NQ, kW, kD>), grid, dim3(64 * kW), 0, s, brp, bci, v,
+                       b, C, M, K, N, Kb, order, row_map);
+}
+
+}  // namespace
+
+bool spmm_f32_batch_covers(int64_t K, int64_t Kb, int64_t N, const void* B, const void* C)
+{
+    const char* e = std::getenv("XSPMM_F32_KERNEL");
+    if (e && std::string(e) == "tile") return false;
+    return N % 4 == 0 && N > 0 && K * N * 4 <= (int64_t(1) << 31) && Kb < (int64_t(1) << 21) &&
+           (reinterpret_cast<uintptr_t>(B) & 15) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
+           (N + 127) / 128 <= 65535;
+}
+
+template <typename I>
+void bcsr_spmm_f32_batch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                         const float* bvals, const float* B, float* C, int64_t N,
+                         const int32_t* order, const I* row_map, hipStream_t s)
+{
+    if (N <= 64)
+        launch_batch<I, 1>(dim3((unsigned)Mb, 1), s, brp, bci, bvals, B, C, M, K, N, Kb, order,
+                           row_map);
+    else
+        launch_batch<I, 2>(dim3((unsigned)Mb, (unsigned)((N + 127) / 128)), s, brp, bci, bvals, B, C,
+                           M, K, N, Kb, order, row_map);
+    XSPMM_LAUNCH_CHECK();
+}
+
+template void bcsr_spmm_f32_batch<int32_t>(int64_t, int64_t, int64_t, int64_t, const int32_t*,
+                                           const int32_t*, const float*, const float*, float*,
+                                           int64_t, const int32_t*, const int32_t*, hipStream_t);
+template void bcsr_spmm_f32_batch<int64_t>(int64_t, int64_t, int64_t, int64_t, const int64_t*,
+                                           const int64_t*, const float*, const float*, float*,
+                                           int64_t, const int32_t*, const int64_t*, hipStream_t);
+
+}  // namespace detail
+}  // namespace xspmm

@@ -15,8 +15,12 @@ Shapes follow the benchmark configurations:
 * ``gnn``         131072^2 fp16 power-law adjacency, N=64        (config 3)
 * ``pruned``      14336x4096 fp16, 90 % pruned, N=2048           (config 4)
 
-plus the reference's ``checkers`` test shape (utils/matrix_gen.hpp:185-211)
-and the ``banded`` shape (utils/matrix_gen.hpp:69-90).
+plus the reference's ``checkers`` test shape (utils/matrix_gen.hpp:185-211),
+the ``banded`` shape (utils/matrix_gen.hpp:69-90) and the ``triangular``
+shape of the Tier-2 sweep (utils/matrix_gen.hpp:95-120).
+
+Every generator takes ``dtype``: the same draws rounded to fp16 or fp32
+(the default is the configuration's own type).
 """
 from __future__ import annotations
 
@@ -64,7 +68,7 @@ def _csr_from_coo(M: int, r: np.ndarray, c: np.ndarray):
     return rp.astype(np.int32), c.astype(np.int32), order
 
 
-def cpu_ref(seed: int = 0, N: int = 64) -> Problem:
+def cpu_ref(seed: int = 0, N: int = 64, dtype=np.float32) -> Problem:
     """M=K=1024 fp32.  Each row draws 10 + Bernoulli(0.24) distinct columns
     uniformly without replacement (E[nnz/row] = 10.24, i.e. 1 %); columns
     sorted.  Values U(-1,1).  B is 1024x64 U(-1,1).  No clustering."""
@@ -75,12 +79,13 @@ def cpu_ref(seed: int = 0, N: int = 64) -> Problem:
         k = 10 + int(rng.random() < 0.24)
         rows.append(np.sort(rng.choice(K, size=k, replace=False)))
     rp, ci = _csr_from_rows(M, rows)
-    vals = rng.uniform(-1, 1, size=len(ci)).astype(np.float32)
-    B = rng.uniform(-1, 1, size=(K, N)).astype(np.float32)
+    vals = rng.uniform(-1, 1, size=len(ci)).astype(dtype)
+    B = rng.uniform(-1, 1, size=(K, N)).astype(dtype)
     return Problem("cpu_ref", M, K, N, rp, ci, vals, B, cluster=False)
 
 
-def blocks(seed: int = 0, M: int = 8192, N: int = 256, frac: float = 0.05) -> Problem:
+def blocks(seed: int = 0, M: int = 8192, N: int = 256, frac: float = 0.05,
+           dtype=np.float16) -> Problem:
     """M=K=8192 fp16.  round(frac * Mb * Kb) of the 16x16 blocks are chosen
     uniformly without replacement; each is fully dense with N(0,1) values.
     B is N(0,1).  No clustering (a Tier-1 workload)."""
@@ -94,14 +99,14 @@ def blocks(seed: int = 0, M: int = 8192, N: int = 256, frac: float = 0.05) -> Pr
     ii = (bi[:, None] * 16 + np.repeat(np.arange(16), 16)[None, :]).ravel()
     jj = (bj[:, None] * 16 + np.tile(np.arange(16), 16)[None, :]).ravel()
     rp, ci, order = _csr_from_coo(M, ii, jj)
-    vals = rng.standard_normal(len(ci)).astype(np.float16)
-    B = rng.standard_normal((K, N)).astype(np.float16)
+    vals = rng.standard_normal(len(ci)).astype(dtype)
+    B = rng.standard_normal((K, N)).astype(dtype)
     return Problem("blocks", M, K, N, rp, ci, vals, B, cluster=False,
                    meta=dict(blocks=nb))
 
 
 def templates(seed: int = 0, M: int = 16384, N: int = 128, n_templates: int = 1024,
-              tcols: int = 82, keep: float = 0.7) -> Problem:
+              tcols: int = 82, keep: float = 0.7, dtype=np.float16) -> Problem:
     """M=K=16384 fp16, 0.5 % density.  1024 templates, each tcols=82 distinct
     uniform columns.  Row r uses template r mod 1024: it keeps a uniform
     subset of round(keep*82)=57 template columns and draws the other 25
@@ -127,8 +132,8 @@ def templates(seed: int = 0, M: int = 16384, N: int = 128, n_templates: int = 10
     shuffle = rng.permutation(M)
     rows = [rows[i] for i in shuffle]
     rp, ci = _csr_from_rows(M, rows)
-    vals = rng.uniform(-1, 1, size=len(ci)).astype(np.float16)
-    B = rng.uniform(-1, 1, size=(K, N)).astype(np.float16)
+    vals = rng.uniform(-1, 1, size=len(ci)).astype(dtype)
+    B = rng.uniform(-1, 1, size=(K, N)).astype(dtype)
     return Problem("templates", M, K, N, rp, ci, vals, B, cluster=True,
                    meta=dict(n_templates=n_templates, tcols=tcols, keep=n_keep))
 
@@ -155,7 +160,7 @@ def _powerlaw_degrees(rng, M, alpha, dmax, mean):
 
 
 def gnn(seed: int = 0, M: int = 131072, N: int = 64, alpha: float = 2.1,
-        dmax: int = 4096, mean: float = 16.0) -> Problem:
+        dmax: int = 4096, mean: float = 16.0, dtype=np.float16) -> Problem:
     """M=K=131072 adjacency.  Out-degrees d_i = floor(x_i), x_i from a
     Pareto(2.1) truncated to [x_min, 4097) with x_min bisected so the sample
     mean is 16; neighbours uniform without replacement; values 1/d_i (fp16).
@@ -165,14 +170,14 @@ def gnn(seed: int = 0, M: int = 131072, N: int = 64, alpha: float = 2.1,
     deg = _powerlaw_degrees(rng, M, alpha, dmax, mean)
     rows = [np.sort(rng.choice(K, size=int(d), replace=False)) for d in deg]
     rp, ci = _csr_from_rows(M, rows)
-    vals = np.repeat(1.0 / np.maximum(deg, 1), deg).astype(np.float16)
-    B = rng.standard_normal((K, N)).astype(np.float16)
+    vals = np.repeat(1.0 / np.maximum(deg, 1), deg).astype(dtype)
+    B = rng.standard_normal((K, N)).astype(dtype)
     return Problem("gnn", M, K, N, rp, ci, vals, B, cluster=True,
                    meta=dict(mean_degree=float(deg.mean()), max_degree=int(deg.max())))
 
 
 def pruned(seed: int = 0, M: int = 14336, K: int = 4096, N: int = 2048,
-           keep: float = 0.10, cluster: bool = False) -> Problem:
+           keep: float = 0.10, cluster: bool = False, dtype=np.float16) -> Problem:
     """A = 14336x4096 fp16 with exactly round(0.1*M*K) surviving positions,
     uniform without replacement (magnitude pruning of an N(0,0.02) weight);
     surviving values N(0,0.02).  B = 4096x2048 N(0,1) fp16."""
@@ -184,8 +189,8 @@ def pruned(seed: int = 0, M: int = 14336, K: int = 4096, N: int = 2048,
     counts = np.bincount(r, minlength=M)
     rp = np.zeros(M + 1, np.int64)
     np.cumsum(counts, out=rp[1:])
-    vals = (rng.standard_normal(nnz) * 0.02).astype(np.float16)
-    B = rng.standard_normal((K, N)).astype(np.float16)
+    vals = (rng.standard_normal(nnz) * 0.02).astype(dtype)
+    B = rng.standard_normal((K, N)).astype(dtype)
     return Problem("pruned", M, K, N, rp.astype(np.int32), c.astype(np.int32), vals, B,
                    cluster=cluster)
 
@@ -219,6 +224,31 @@ def banded(M: int = 1024, bandwidth: int = 8, N: int = 32, seed: int = 42,
     vals = rng.uniform(0.1, 1.0, size=len(ci)).astype(dtype)
     B = np.ones((M, N), dtype)
     return Problem("banded", M, M, N, rp, ci, vals, B, cluster=False)
+
+
+def triangular(size: int = 8192, density: float = 0.01, upper: bool = True, N: int | None = None,
+               seed: int = 42, dtype=np.float32) -> Problem:
+    """The triangular shape of the reference's Tier-2 sweep
+    (examples/02_spmm_benchmark.cpp:60-61, :268-269; utils/matrix_gen.hpp:95-120):
+    entry (i, j) of the upper (lower) triangle is present with probability
+    `density`, the diagonal always, values U(0.1, 1); seeded here with numpy,
+    not the reference's mt19937.  N defaults to `size` (examples/02 runs
+    N = M = K); B is U(-1, 1) here (examples/02 uses ones, which would hide a
+    column mix-up).  The sweep runs the Tier-2 pipeline with clustering on."""
+    rng = np.random.default_rng(seed)
+    N = size if N is None else N
+    rows = []
+    for i in range(size):
+        lo, hi = (i, size) if upper else (0, i + 1)
+        j = np.arange(lo, hi)
+        keep = rng.random(hi - lo) < density
+        keep[i - lo] = True
+        rows.append(j[keep])
+    rp, ci = _csr_from_rows(size, rows)
+    vals = rng.uniform(0.1, 1.0, size=len(ci)).astype(dtype)
+    B = rng.uniform(-1, 1, size=(size, N)).astype(dtype)
+    return Problem("triangular", size, size, N, rp, ci, vals, B, cluster=True,
+                   meta=dict(density=density, upper=upper))
 
 
 # the density sweep of examples/05_core_spmm_benchmark.cpp:67-77
@@ -278,3 +308,6 @@ CONFIGS = {
 }
 for _name, _d in SWEEP_DENSITIES.items():
     CONFIGS[f"banded{_name}"] = (lambda d: lambda **kw: banded_sweep(d, **kw))(_d)
+    # the sweep in fp32, the type examples/05 runs it in (ValueType = float, :25)
+    CONFIGS[f"banded{_name}_f32"] = (
+        lambda d: lambda **kw: banded_sweep(d, **{"dtype": np.float32, **kw}))(_d)
