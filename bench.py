@@ -334,9 +334,13 @@ def main():
     eff = 2.0 * nnz * N / t / 1e12
     padded = 2.0 * nnzb * 256 * N / t / 1e12
     mfma_peak = FP16_PEAK_TFLOPS if sT == 2 else FP32_MFMA_PEAK_TFLOPS
-    # bound: padded flops per algorithmic byte against the ridge point
+    kernel = tier1_kernel(sT, K, N, nnzb, Mb)
+    # bound: the column-batch kernels multiply only the non-zero block
+    # columns, so they never execute the padded flops and HBM bounds them;
+    # a kernel that multiplies whole blocks is bound by whichever of its
+    # padded flops and its algorithmic bytes is the larger share of its peak
     ridge = mfma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
-    mfma_bound = 2.0 * nnzb * 256 * N / alg_bytes > ridge
+    mfma_bound = "batch" not in kernel and 2.0 * nnzb * 256 * N / alg_bytes > ridge
     if mfma_bound:
         roofline = {"bound": "mfma", "achieved": padded, "peak": mfma_peak, "unit": "TFLOP/s",
                     "frac": padded / mfma_peak}
@@ -346,7 +350,7 @@ def main():
     traffic_key = args.config + ("" if args.n is None else f"_n{args.n}")
     if args.dtype != "config" and not args.config.endswith("_" + args.dtype):
         traffic_key += "_" + args.dtype
-    roofline.update({"traffic": load_traffic(traffic_key), "kernel": tier1_kernel(sT, K, N, nnzb, Mb),
+    roofline.update({"traffic": load_traffic(traffic_key), "kernel": kernel,
                      "alg_bytes_per_call": alg_bytes,
                      "padded_flops_per_call": 2.0 * nnzb * 256 * N})
 

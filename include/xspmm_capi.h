@@ -197,6 +197,19 @@ int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
                         double* timings, void* stream);
 
 /*
+ * Device bytes of the temporaries that the last xspmm_spmm_pipeline call on
+ * the calling thread took from the device's memory pool (0 before any call):
+ * the permuted CSR, the permuted-order C and the BCSR arrays.  The BCSR
+ * arrays are sized from the bound min(nnz, Mb * Kb) on the block count while
+ * that bound's block values fit 1 GiB, else exactly after the block count is
+ * read.
+ * No counterpart in the reference (whose pipeline makes a hipMalloc per
+ * temporary, src/hip/unstructured_mtx_mul.hip:31-100); it lets a caller see
+ * the pipeline's memory footprint.
+ */
+int xspmm_pipeline_temp_bytes(int64_t* bytes_out);
+
+/*
  * Prepared Tier-2 product ("plan"): the pipeline's clustering, permutation
  * and CSR->BCSR stages run once at creation, on device CSR arrays rp/ci/vals
  * (hw_block_size must be 16; clustering as in xspmm_spmm_pipeline); the plan

@@ -1,0 +1,84 @@
+"""GPU: the Tier-2 pipeline's temporary device memory.
+
+The pipeline sizes its BCSR arrays from the bound min(nnz, Mb * Kb) on the
+block count while that bound's block values fit 1 GiB (the conversion's count
+and fill then run with no host round trip), and exactly, after reading the
+count, above it -- as the reference's conversion does
+(src/core/conversion.cpp:66-73).  A matrix of full 16x16 blocks has
+nnz = 256 * nnzb, so there the bound is 256x the exact size.
+xspmm_pipeline_temp_bytes reports what the last call took.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import xspmm_amd as X
+from xspmm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+FUSED_LIMIT = 1 << 30
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need an MI355X (torch.cuda.is_available() is False)")
+    X.load()
+    return torch
+
+
+def block_diagonal(Mb, N, seed=0, dtype=np.float32):
+    """Mb dense 16x16 blocks on the diagonal, values U(-1, 1); B U(-1, 1)."""
+    rng = np.random.default_rng(seed)
+    M = 16 * Mb
+    blocks = rng.uniform(-1, 1, size=(Mb, 16, 16)).astype(dtype)
+    rp = (np.arange(M + 1, dtype=np.int64) * 16).astype(np.int32)
+    r = np.arange(M)
+    ci = ((r // 16)[:, None] * 16 + np.arange(16)[None, :]).reshape(-1).astype(np.int32)
+    vals = blocks.reshape(-1)
+    B = rng.uniform(-1, 1, size=(M, N)).astype(dtype)
+    return synth.Problem("blockdiag", M, M, N, rp, ci, vals, B, cluster=False), blocks
+
+
+def test_full_blocks_take_exact_bcsr(torch):
+    """131072^2 block-diagonal fp32: the bound's block values would take
+    2 GiB, the exact arrays 8 MiB; the pipeline takes within 1.5x of the
+    exact bytes and C equals the block products."""
+    Mb, N = 8192, 16
+    p, blocks = block_diagonal(Mb, N)
+    sT, sI = 4, 4
+    cap = min(p.nnz, Mb * Mb)
+    assert cap * 256 * sT > FUSED_LIMIT
+    A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
+    B = torch.as_tensor(p.B).cuda()
+    C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
+    torch.cuda.synchronize()
+    used = X.pipeline_temp_bytes()
+    exact = (Mb + 1) * sI + 4 + Mb * sI + Mb * 256 * sT  # row_ptr, flag, col_ind, values
+    print(f"pipeline temporaries {used} B, exact {exact} B, bound {cap * 256 * sT} B", flush=True)
+    assert exact <= used <= 1.5 * exact
+    ref = np.einsum("bij,bjn->bin", blocks.astype(np.float64),
+                    p.B.astype(np.float64).reshape(Mb, 16, N)).reshape(p.M, N)
+    e = oracle.errors(C.cpu().numpy(), ref)
+    assert e["rel_frob"] <= 1e-5, e
+
+
+def test_small_matrix_keeps_fused_bound(torch):
+    """A small matrix keeps the bound-sized arrays (no host round trip): the
+    reported bytes cover min(nnz, Mb * Kb) blocks; C against fp64."""
+    p = synth.random_csr(500, 700, 64, 0.02, seed=4, dtype=np.float16)
+    Mb, Kb = (p.M + 15) // 16, (p.K + 15) // 16
+    cap = min(p.nnz, Mb * Kb)
+    A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
+    B = torch.as_tensor(p.B).cuda()
+    C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
+    torch.cuda.synchronize()
+    used = X.pipeline_temp_bytes()
+    assert used >= cap * 256 * 2 + cap * 4
+    brp, bci, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    ref = oracle.bcsr_spmm_f64(p.M, p.K, p.N, brp, bci, bv, p.B)
+    assert oracle.errors(C.cpu().numpy(), ref)["rel_frob"] <= 2e-3

@@ -102,6 +102,8 @@ def load():
     L.xspmm_mtx_export.argtypes = [p, i32, i32, p, p, p]
     L.xspmm_mtx_free.restype = i32
     L.xspmm_mtx_free.argtypes = [p]
+    L.xspmm_pipeline_temp_bytes.restype = i32
+    L.xspmm_pipeline_temp_bytes.argtypes = [C.POINTER(C.c_int64)]
     L.xspmm_spmm_pipeline.restype = i32
     L.xspmm_spmm_pipeline.argtypes = [i32, i32, i64, i64, i64, p, p, p, p, p, i64, i64, i32,
                                       C.POINTER(C.c_double), p]
@@ -425,6 +427,14 @@ def spmm_pipeline(A: CSRMatrix, B, C_out=None, N: int | None = None, hw_block_si
                                  C.cast(t, C.POINTER(C.c_double)) if t is not None else None,
                                  _stream()))
     return C_out, (dict(zip(TIMING_FIELDS, list(t))) if t is not None else None)
+
+
+def pipeline_temp_bytes() -> int:
+    """Device bytes of the temporaries the last spmm_pipeline call on this
+    thread took (C ABI xspmm_pipeline_temp_bytes)."""
+    out = C.c_int64(0)
+    _check(load().xspmm_pipeline_temp_bytes(C.byref(out)))
+    return int(out.value)
 
 
 class SpMMPlan:

@@ -258,6 +258,14 @@ int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
     });
 }
 
+int xspmm_pipeline_temp_bytes(int64_t* bytes_out)
+{
+    return guarded([&] {
+        require(bytes_out != nullptr, "xspmm_pipeline_temp_bytes: bytes_out is null.");
+        *bytes_out = (int64_t)last_pipeline_temp_bytes();
+    });
+}
+
 int xspmm_plan_create(int vtype, int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
                       const void* ci, const void* vals, int64_t hw_block_size,
                       int optimize_pattern, double* timings, void* stream, xspmm_plan_t* plan_out)

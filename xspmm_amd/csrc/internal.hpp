@@ -372,6 +372,10 @@ struct MtxData {
 };
 MtxData read_matrix_market(const std::string& path);
 
+// Device bytes of the temporaries the last spmm_pipeline call on this thread
+// took (0 before any call).
+size_t last_pipeline_temp_bytes();
+
 // Tier-2 pipeline on raw device pointers.  `timings` may be null; it points
 // at six doubles laid out like SpMMTimings.
 template <typename T, typename I>

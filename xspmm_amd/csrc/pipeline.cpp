@@ -16,10 +16,15 @@
 // Differences from the reference, with identical results: C / C_temp are not
 // memset first (the SpMM overwrites every element), temporaries come from one
 // stream-ordered allocation instead of hipMalloc/hipFree pairs, taken before
-// the first stage (the BCSR arrays sized from the bound min(nnz, Mb * Kb), so
-// the conversion needs no host round trip between its count and its fill),
-// and permuted row_ptr[M] is the sum of the gathered lengths (equal to nnz
-// for a permutation).
+// the first stage, and permuted row_ptr[M] is the sum of the gathered lengths
+// (equal to nnz for a permutation).  The BCSR arrays are part of that
+// allocation, sized from the bound min(nnz, Mb * Kb) on the block count, when
+// the bound's block values take at most kFusedConversionBytes: the
+// conversion's count and fill then run back to back with no host round trip.
+// Above that the bound can exceed the exact size many times over (256x when
+// every block is full), so the conversion reads the count first and takes the
+// arrays at their exact size, as the reference does
+// (src/core/conversion.cpp:66-73).
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -29,6 +34,19 @@
 
 namespace xspmm {
 namespace detail {
+
+namespace {
+
+// Largest bound-sized BCSR value array the fused conversion takes (above it,
+// exact sizing after one host round trip).
+constexpr size_t kFusedConversionBytes = size_t(1) << 30;
+
+// Device bytes of the last pipeline call's temporaries on this thread.
+thread_local size_t g_last_temp_bytes = 0;
+
+}  // namespace
+
+size_t last_pipeline_temp_bytes() { return g_last_temp_bytes; }
 
 
 template <typename I>
@@ -80,11 +98,12 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
 
     // Every temporary is taken before the first stage, so the stage times
-    // hold the stages' own work.  The BCSR arrays are sized from the bound
-    // min(nnz, Mb * Kb) on the block count (each block holds an entry), so
-    // the conversion's count and fill run back to back and nnzb is read once,
-    // after the fill.
+    // hold the stages' own work, except exactly sized BCSR arrays, which the
+    // conversion stage takes once it has read the block count.  The bound
+    // min(nnz, Mb * Kb) on the block count holds since each block holds an
+    // entry.
     const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(nnz, Mb * Kb));
+    const bool fused = (size_t)cap * 256 * sizeof(T) <= kFusedConversionBytes;
     // all in one allocation
     Carve cv;
     size_t o_perm = 0, o_nrp = 0, o_nci = 0, o_nvals = 0, o_ctmp = 0;
@@ -96,14 +115,16 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
         o_ctmp = cv.take((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float));
     }
     const size_t o_brp = cv.take((size_t)(Mb + 1) * sizeof(I));
-    const size_t o_bci = cv.take((size_t)cap * sizeof(I));
-    const size_t o_bvals = cv.take((size_t)cap * 256 * sizeof(T));
     const size_t o_err = cv.take(sizeof(int));
+    const size_t o_bci = fused ? cv.take((size_t)cap * sizeof(I)) : 0;
+    const size_t o_bvals = fused ? cv.take((size_t)cap * 256 * sizeof(T)) : 0;
     Scratch tmp(cv.end, s);
+    g_last_temp_bytes = cv.end;
     char* const base = tmp.as<char>();
     const Piece d_perm{base + o_perm}, nrp{base + o_nrp}, nci{base + o_nci}, nvals{base + o_nvals},
-        c_tmp{base + o_ctmp}, brp{base + o_brp}, bci{base + o_bci}, bvals{base + o_bvals},
-        err{base + o_err};
+        c_tmp{base + o_ctmp}, brp{base + o_brp}, err{base + o_err};
+    Piece bci{base + o_bci}, bvals{base + o_bvals};
+    Scratch blocks;  // exactly sized BCSR arrays (when not fused)
 
     // the stage's CSR: the caller's, or the permuted copy
     const I* crp = rp;
@@ -128,10 +149,21 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     // 3. Conversion (the fill writes nothing if the count finds invalid input).
     step.start();
     csr_to_bcsr_count_async<I>(M, K, nnz, crp, cci, 16, 16, brp.as<I>(), err.as<int>(), s);
+    int64_t nnzb = 0;
+    if (!fused) {
+        nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
+        Carve bc;
+        const size_t o_ci = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I));
+        const size_t o_v = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T));
+        blocks = Scratch(bc.end, s);
+        g_last_temp_bytes += bc.end;
+        bci = Piece{blocks.as<char>() + o_ci};
+        bvals = Piece{blocks.as<char>() + o_v};
+    }
     csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp.as<I>(), bci.as<I>(),
                            bvals.as<T>(), s, err.as<int>());
     if (timed) step.stop(&tm[2]);
-    const int64_t nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
+    if (fused) nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
 
     if (optimize_pattern) {
         // 4. SpMM into the permuted-order temporary.
