@@ -78,6 +78,8 @@ CASES = [
     ("dispatch order int64", (40000, 4096, 128), (33000, 4096, 128), np.float16, np.int64),
     ("panels N % 8 != 0", (3000, 4096, 20), (1000, 512, 12), np.float16, np.int32),
     ("fp32", (5000, 3000, 64), (700, 300, 40), np.float32, np.int32),
+    ("fp32 column batches, dispatch order", (40000, 4096, 128), (36000, 2048, 64), np.float32,
+     np.int32),
 ]
 
 
@@ -116,14 +118,77 @@ def test_noalloc_rejects_products_beyond_its_scratch(torch, lib):
     cap = lib.xspmm_noalloc_scratch_bytes()
     assert cap == 8 << 20
     # a grid of more block-rows than the dispatch order fits: 4 bytes each.
-    # Rejected before any launch, so the (absent) arrays are never read.
+    # Rejected before any launch.  The arrays are real and describe a valid
+    # product of empty block-rows (a launch would stay in bounds and write
+    # zeros), so C still holding its NaNs shows that nothing ran.
     Mb = cap // 4 + 1
-    rc = lib.xspmm_bcsr_spmm_noalloc(X.F16, X.I32, 16 * Mb, 16, Mb, 1, 0, None, None, None, None,
-                                     None, 64, None)
+    M, K, N = 16 * Mb, 16, 8
+    brp = torch.zeros(Mb + 1, dtype=torch.int32, device="cuda")
+    bci = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bvals = torch.zeros(256, dtype=torch.float16, device="cuda")
+    B = torch.zeros((K, N), dtype=torch.float16, device="cuda")
+    Cout = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    vp = lambda t: C.c_void_p(t.data_ptr())
+    rc = lib.xspmm_bcsr_spmm_noalloc(X.F16, X.I32, M, K, Mb, 1, 0, vp(brp), vp(bci), vp(bvals),
+                                     vp(B), vp(Cout), N,
+                                     C.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == X.ERR_INVALID
     assert "scratch" in lib.xspmm_last_error().decode()
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(Cout).all())
+    del Cout
     # the allocation-free path still works afterwards
     A, B = skewed(40000, 1024, 64, seed=5)
     Bm = X.csr_to_bcsr(A)
     C1, C2 = both(lib, Bm, torch.as_tensor(B).cuda(), 64, torch)
     assert torch.equal(C1, C2)
+
+
+HIP_MEMPOOL_USED_MEM_CURRENT = 0x7   # hipMemPoolAttrUsedMemCurrent
+HIP_MEMPOOL_USED_MEM_HIGH = 0x8      # hipMemPoolAttrUsedMemHigh
+
+
+def test_noalloc_takes_nothing_from_the_pool(torch, lib):
+    """The library's temporaries come from the device's default memory pool
+    (hipMallocAsync).  Its high-water mark must not rise during
+    allocation-free calls on paths that use scratch (dispatch order, B panels,
+    fp32 column batches), and must rise during the allocating entry point's
+    call on the same product (the positive control)."""
+    hip = C.CDLL("libamdhip64.so.7")
+    pool = C.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(C.byref(pool), torch.cuda.current_device()) == 0
+
+    def attr(a):
+        v = C.c_uint64(0)
+        assert hip.hipMemPoolGetAttribute(pool, a, C.byref(v)) == 0
+        return v.value
+
+    def reset_high():
+        v = C.c_uint64(0)
+        assert hip.hipMemPoolSetAttribute(pool, HIP_MEMPOOL_USED_MEM_HIGH, C.byref(v)) == 0
+
+    for name, (M, K, N), dtype in (("dispatch order", (48000, 4096, 64), np.float16),
+                                   ("panels N % 8 != 0", (3000, 4096, 20), np.float16),
+                                   ("fp32 dispatch order", (40000, 4096, 128), np.float32)):
+        A, B = skewed(M, K, N, seed=3, dtype=dtype)
+        Bm = X.csr_to_bcsr(A)
+        Bd = torch.as_tensor(B).cuda()
+        C1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        C2 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        base = attr(HIP_MEMPOOL_USED_MEM_CURRENT)
+        reset_high()
+        call(lib, "xspmm_bcsr_spmm_noalloc", Bm, Bd, C2, N, torch)
+        call(lib, "xspmm_bcsr_spmm_noalloc", Bm, Bd, C2, N, torch)
+        torch.cuda.synchronize()
+        high_noalloc = attr(HIP_MEMPOOL_USED_MEM_HIGH)
+        reset_high()
+        call(lib, "xspmm_bcsr_spmm", Bm, Bd, C1, N, torch)
+        torch.cuda.synchronize()
+        high_alloc = attr(HIP_MEMPOOL_USED_MEM_HIGH)
+        print(f"{name}: pool in use {base} B; high water {high_noalloc} B (allocation-free), "
+              f"{high_alloc} B (allocating)", flush=True)
+        assert high_noalloc <= base, name
+        assert high_alloc > base, name
+        assert torch.equal(C1, C2), name
