@@ -105,7 +105,7 @@ public:
 
     std::shared_ptr<const Executor> get_executor() const { return exec_; }
 
-    // Dispatch order of the fp16 Tier-1 kernel (block-row ids, longest rows
+    // Dispatch order of the Tier-1 column-batch kernels (block-row ids, longest rows
     // first; num_block_rows int32 entries on the executor), which csr_to_bcsr
     // computes once for grids with many block-rows so that Tier-1 calls do
     // not order the rows again.  Null: Tier-1 orders them on each call when

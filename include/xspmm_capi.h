@@ -70,7 +70,7 @@ int xspmm_bcsr_spmm(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int6
  * life of the process.  No hipMalloc, hipFree or allocating library call is
  * made (the array's device address is looked up once per device, on the
  * first call there).  A product that needs more scratch than the array holds
- * (e.g. more than 2^21 block-rows on the fp16 column-batch path) is rejected
+ * (e.g. more than 2^21 block-rows on a column-batch path) is rejected
  * with XSPMM_ERR_INVALID before anything is launched.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams,
  * other host threads) race and must be serialized by the caller.
@@ -87,7 +87,8 @@ int xspmm_bcsr_spmm_noalloc(int vtype, int itype, int64_t M, int64_t K, int64_t 
 int64_t xspmm_noalloc_scratch_bytes(void);
 
 /*
- * Dispatch order of the fp16 Tier-1 kernel for a block-row grid: when Tier-1
+ * Dispatch order of the Tier-1 column-batch kernels (fp16 and fp32) for a
+ * block-row grid: when Tier-1
  * would order this grid's rows (more than 2048 block-rows), writes the Mb
  * block-row ids (int32, longest rows first) to `order` and sets
  * *written = 1; otherwise writes nothing and sets *written = 0.

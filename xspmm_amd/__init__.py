@@ -284,7 +284,7 @@ def csr_to_bcsr(A: CSRMatrix, r_block: int = 16, c_block: int = 16) -> BCSRMatri
                                     A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values),
                                     r_block, c_block, _ptr(brp), _ptr(bci), _ptr(bv), _stream()))
     out = BCSRMatrix(Mb, Kb, r_block, c_block, A.num_rows, A.num_cols, brp, bci, bv)
-    if A.values.dtype == torch.float16 and r_block == 16 and c_block == 16:
+    if r_block == 16 and c_block == 16:
         out.dispatch_order()  # once here rather than in every Tier-1 call
     return out
 
@@ -301,7 +301,7 @@ def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
         C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=dev)
     _check_dense(B, "B", A.num_cols, N, A.values.dtype, dev)
     _check_dense(C_out, "C_out", A.num_rows, N, torch.float32, dev)
-    order = A.dispatch_order() if B.dtype == torch.float16 else None
+    order = A.dispatch_order()
     _check(L.xspmm_bcsr_spmm_ordered(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows,
                                      A.num_cols, A.num_block_rows, A.num_block_cols, A.num_blocks,
                                      _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values), _ptr(B),

@@ -282,12 +282,13 @@ BCSRMatrix<ValueType, IndexType> csr_to_bcsr(std::shared_ptr<const Executor> tar
         detail::csr_to_bcsr_fill<dev_t<ValueType>, IndexType>(
             M, K, nnz, src.d_rp, src.d_ci, dev(src.d_vals), r_block, c_block, brp.as<IndexType>(),
             out.get_bcsr_col_ind(), dev(out.get_bcsr_values()), kStream);
-        // the fp16 Tier-1 kernel's dispatch order, once (see BCSRMatrix)
-        if (sizeof(ValueType) == 2 && r_block == 16 && c_block == 16 && detail::spmm_order_wanted(Mb)) {
+        // the column-batch kernels' dispatch order, once (see BCSRMatrix);
+        // owned by `out` from the allocation on, so a failed launch frees it
+        if (r_block == 16 && c_block == 16 && detail::spmm_order_wanted(Mb)) {
             int32_t* order = nullptr;
             target_exec->allocate(reinterpret_cast<void**>(&order), (size_t)Mb * sizeof(int32_t));
-            detail::spmm_dispatch_order<IndexType>(out.get_bcsr_row_ptr(), Mb, order, kStream);
             out.set_dispatch_order(order);
+            detail::spmm_dispatch_order<IndexType>(out.get_bcsr_row_ptr(), Mb, order, kStream);
         }
     } else {
         // GPU-resident input, host target: convert on the GPU, then copy down.
