@@ -335,24 +335,39 @@ def main():
     padded = 2.0 * nnzb * 256 * N / t / 1e12
     mfma_peak = FP16_PEAK_TFLOPS if sT == 2 else FP32_MFMA_PEAK_TFLOPS
     kernel = tier1_kernel(sT, K, N, nnzb, Mb)
-    # bound: the column-batch kernels multiply only the non-zero block
-    # columns, so they never execute the padded flops and HBM bounds them;
-    # a kernel that multiplies whole blocks is bound by whichever of its
-    # padded flops and its algorithmic bytes is the larger share of its peak
-    ridge = mfma_peak * 1e12 / (HBM_PEAK_GBS * 1e9)
-    mfma_bound = "batch" not in kernel and 2.0 * nnzb * 256 * N / alg_bytes > ridge
-    if mfma_bound:
-        roofline = {"bound": "mfma", "achieved": padded, "peak": mfma_peak, "unit": "TFLOP/s",
-                    "frac": padded / mfma_peak}
+    # Matrix-core work the kernel executes: the column-batch kernels multiply
+    # only the block columns that hold a non-zero entry (32 flops per such
+    # column, row and output column: 16 rows x multiply-add), the other
+    # kernels every block whole (the padded flops).  The bound is whichever of
+    # HBM (algorithmic bytes) and the matrix cores (executed flops) the call
+    # uses the larger share of.
+    if "batch" in kernel:
+        vals = Bm.values.view(-1, 16, 16)
+        ncols = 0
+        for i in range(0, vals.shape[0], 1 << 20):  # chunks bound the temporary
+            ncols += int((vals[i:i + (1 << 20)] != 0).any(dim=1).sum())
+        exec_flops = 32.0 * ncols * N
+    else:
+        ncols = None
+        exec_flops = 2.0 * nnzb * 256 * N
+    exec_tflops = exec_flops / t / 1e12
+    hbm_frac = achieved / HBM_PEAK_GBS
+    mfma_frac = exec_tflops / mfma_peak
+    if mfma_frac > hbm_frac:
+        roofline = {"bound": "mfma", "achieved": exec_tflops, "peak": mfma_peak, "unit": "TFLOP/s",
+                    "frac": mfma_frac}
     else:
         roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": achieved / HBM_PEAK_GBS}
+                    "frac": hbm_frac}
     traffic_key = args.config + ("" if args.n is None else f"_n{args.n}")
     if args.dtype != "config" and not args.config.endswith("_" + args.dtype):
         traffic_key += "_" + args.dtype
     roofline.update({"traffic": load_traffic(traffic_key), "kernel": kernel,
                      "alg_bytes_per_call": alg_bytes,
-                     "padded_flops_per_call": 2.0 * nnzb * 256 * N})
+                     "padded_flops_per_call": 2.0 * nnzb * 256 * N,
+                     "executed_mfma_flops_per_call": exec_flops,
+                     "nonzero_block_columns": ncols,
+                     "hbm_frac": hbm_frac, "mfma_frac": mfma_frac})
 
     stages = stages_gpu = None
     # Tier-2 stage times after untimed warm-up calls, as the reference's own

@@ -25,17 +25,18 @@
 //      16 l .. 16 l + 15, layout [quad][row][4]) and appends its set columns to
 //      a batch of four K slots: slot k is held by lane group k, which records
 //      the slot's LDS column address and the byte offset of its B row;
-//   4. when four slots are set, closes the batch: multiplies the batch still
-//      in flight, has each lane read its A' entry A[r][col(k)] from the ring
-//      (one ds_read_b32) and issues this batch's B row loads: lane (n, k)
-//      loads B[row(k)][n0 + 64 q + 4 n .. +3] as one 16-byte load per 64
-//      columns, straight into MFMA B operands, so a batch's rows arrive while
-//      the next batch forms;
-//   5. the multiply issues one MFMA per float4 component j: component j of
-//      quad q covers C columns n0 + 64 q + 4 n + j (n = 0 .. 15).
-// A block whose 16 columns are all set is multiplied as it stands (four
-// steps, step s holding columns 4k + s, which lane (r, k) already holds),
-// with its 4 x 16 B rows loaded together.
+//   4. when four slots are set, closes the batch: each lane reads its A'
+//      entry A[r][col(k)] from the ring (one ds_read_b32), and the batch joins
+//      the list of batches closed in this ring pass;
+//   5. at the end of each ring pass, multiplies the previous pass's batches
+//      and issues the B row loads of this pass's batches: lane (n, k) loads
+//      B[row(k)][n0 + 64 q + 4 n .. +3] as one 16-byte load per 64 columns,
+//      straight into MFMA B operands, so a pass's rows arrive while the next
+//      pass streams its blocks.  The multiply issues one MFMA per float4
+//      component j: component j of quad q covers C columns
+//      n0 + 64 q + 4 n + j (n = 0 .. 15).
+// A block whose 16 columns are all set joins the list as four batches as it
+// stands (batch s holding columns 4k + s, which lane (r, k) already holds).
 // The waves' partial tiles are summed through LDS in wave order and stored as
 // 16-byte rows.  Skipped columns would add exact zeros (products of +-0 and
 // finite B entries), so C equals the full product for finite B; a non-finite
@@ -62,12 +63,13 @@ constexpr int kWave = 64;
 constexpr int kRawBufferWord3 = 0x00020000;
 // Cache-policy operand of the buffer-load builtins: non-temporal (nt).
 constexpr int kNonTemporal = 2;
-// Blocks of the per-wave LDS ring.  A batch's slots come from at most four
-// consecutive non-empty blocks and the batch reads them when it closes, which
-// is before the fourth block after the oldest one is written; LDS operations
-// of one wave complete in order.
-constexpr int kRing = 4;
-constexpr int kRingBytes = kRing * 1024;
+// Columns of the per-wave LDS column queue (a power of two): 64 bytes of A'
+// and 4 bytes of B row offset each.  A pass queues at most 15 columns per
+// block (a block with all 16 set is multiplied directly), and the pass end
+// leaves at most kQueueCols - 15 D queued, so no unread slot is overwritten;
+// LDS operations of one wave complete in order.
+constexpr int kQueueCols = 128;
+constexpr int kQueueBytes = kQueueCols * 68;
 // column mask of a block whose 16 columns all hold a non-zero entry
 constexpr uint64_t kAllColumns = 0x000f000f000f000full;
 
@@ -117,19 +119,25 @@ __device__ __forceinline__ uint64_t columns_below(uint32_t lim)
     return m;
 }
 
-// NQ: 64-column quads per workgroup (one 16-byte B load per quad and slot);
-// W: waves per workgroup; D: blocks in flight per wave.
-template <typename I, int NQ, int W, int D>
-__global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
+// NQ: 64-column quads per workgroup (one 16-byte B load per quad and batch
+// slot); W: waves per workgroup; D: blocks per ring pass (in flight per
+// wave); F: batches taken from the column queue per pass.
+template <typename I, int NQ, int W, int D, int F>
+__global__ __launch_bounds__(64 * W, (W <= 4 ? 16 / W : 1)) void spmm_f32_batch_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const float* __restrict__ vals,
     const float* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
     int64_t Kb, const int32_t* __restrict__ order, const I* __restrict__ row_map)
 {
     static_assert(NQ == 1 || NQ == 2, "64 or 128 columns per workgroup");
-    static_assert(D >= 2 && D <= 8, "2 .. 8 blocks in flight per wave");
-    static_assert(W * D <= 64 * 8 / (int)sizeof(I), "index window exceeds a wave");
+    static_assert(D >= 2 && D <= 8, "2 .. 8 blocks per ring pass");
+    static_assert(F >= 4 && F <= 8, "4 .. 8 batches per pass");
+    // a pass adds at most 15 D columns to a queue the previous pass end left
+    // at most kQueueCols - 15 D long; that bound is at least 4, so a queue
+    // above it always holds a full batch to take
+    static_assert(15 * D + 4 <= kQueueCols, "a pass's sparse columns fit the queue");
+    static_assert(D * (int)sizeof(I) <= 256, "a pass's block columns fit one index window");
     constexpr int kRedBytes = 16 * 64 * NQ * 4;  // one wave's partial tile
-    constexpr int kLdsBytes = W * (kRingBytes > kRedBytes ? kRingBytes : kRedBytes);
+    constexpr int kLdsBytes = W * (kQueueBytes > kRedBytes ? kQueueBytes : kRedBytes);
     __shared__ __align__(16) unsigned char smem[kLdsBytes];
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -155,22 +163,27 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
     const uint32_t rowbytes = (uint32_t)(4 * N);
     const uint32_t kb32 = (uint32_t)Kb;
+    constexpr uint32_t kNone = 0xffffffffu;  // a slot (or quad) that loads nothing
 
-    unsigned char* const ring = smem + wave * kRingBytes;
-    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
-    // lane l writes bytes 16 l .. 16 l + 15 of a ring block: [quad g][row li][4]
+    // this wave's column queue: A' columns [kQueueCols][16] fp32 and the byte
+    // offsets of their B rows [kQueueCols]; slot s at index s mod kQueueCols
+    float* const qa = reinterpret_cast<float*>(smem + wave * kQueueBytes);
+    uint32_t* const qr = reinterpret_cast<uint32_t*>(smem + wave * kQueueBytes + kQueueCols * 64);
+    uint32_t head = 0;  // next slot to take (wave-uniform)
+    uint32_t tail = 0;  // next slot to fill (wave-uniform)
+
+    // lane (li, g) reads row li, columns 4g .. 4g+3 of a block
     const uint32_t a_voff = (uint32_t)(li * 64 + g * 16) + (uint32_t)wave * 1024u;
-    const uint32_t ring_w = (uint32_t)lane * 16u;
     // B loads: lane (li, g) covers columns n0 + 64 q + 4 li .. +3 of its slot's
     // row; quads past N read nothing
     uint32_t b_lane[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         const int64_t col = n0 + 64 * q + 4 * li;
-        b_lane[q] = col < N ? (uint32_t)(4 * col) : 0xffffffffu;
+        b_lane[q] = col < N ? (uint32_t)(4 * col) : kNone;
     }
     // index window of a ring pass: lane l holds dword l of the block columns
-    // of wave-blocks p .. p + D - 1 (int64: two dwords per block)
+    // of wave-blocks p .. p + 63 (int64: two dwords per block)
     constexpr uint32_t kIdxDw = sizeof(I) / 4;
     const uint32_t cw_off = (uint32_t)wave * (uint32_t)sizeof(I) +
                             (uint32_t)(lane / kIdxDw) * (uint32_t)(W * sizeof(I)) +
@@ -182,16 +195,17 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[q][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // the batch in flight: its A' entry and B operands
-    float ap = 0.f;
-    float4_t bq[NQ];
+    // the batches in flight: A' entry (lane (r, k): A'[r][slot k]) and B
+    // operands (lane (n, k): row of slot k, columns n0 + 64 q + 4 n .. +3)
+    float ap[F];
+    float4_t bq[F][NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) bq[q] = float4_t{0.f, 0.f, 0.f, 0.f};
-    bool pending = false;  // a batch is in flight (wave-uniform)
-    uint32_t fill = 0;     // slots of the open batch (wave-uniform)
-    uint32_t ridx = 0;     // next ring block (wave-uniform)
-    uint32_t my_a = 0;     // this lane group's slot: LDS byte offset of its column in the ring
-    uint32_t my_b = 0;     // and the byte offset of its B row
+    for (int f = 0; f < F; ++f) {
+        ap[f] = 0.f;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) bq[f][q] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    uint32_t inflight = 0;  // batches held in ap / bq (wave-uniform)
 
     auto multiply = [&](const float a, const float4_t (&b)[NQ]) __attribute__((always_inline)) {
 #pragma unroll
@@ -200,27 +214,49 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
             for (int j = 0; j < 4; ++j)
                 acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[q][j], acc[q][j], 0, 0, 0);
     };
-    // this lane's B operands of the row at byte offset `boff` (zeros when the
-    // slot is unused or the quad lies past N)
-    auto load_b = [&](float4_t (&b)[NQ], uint32_t boff, bool used) __attribute__((always_inline)) {
+    // multiply the batches in flight (waits for their B rows)
+    auto multiply_inflight = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const uint32_t off = (used && b_lane[q] != 0xffffffffu) ? boff + b_lane[q] : b_bytes;
-            b[q] = __builtin_bit_cast(float4_t,
-                                      __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
-        }
+        for (int f = 0; f < F; ++f)
+            if ((uint32_t)f < inflight) multiply(ap[f], bq[f]);
+        inflight = 0;
     };
-    // close the open batch of `cnt` slots: multiply the batch in flight, then
-    // read this one's A' entry from the ring (A' = 0 in unused slots) and
-    // issue its B row loads
-    auto close = [&](uint32_t cnt) __attribute__((always_inline)) {
-        if (pending) multiply(ap, bq);
-        const bool used = (uint32_t)g < cnt;
-        const float x = *(__attribute__((address_space(3))) const float*)(uintptr_t)(ring_lds + my_a +
-                                                                                     (uint32_t)li * 16u);
-        ap = used ? x : 0.f;
-        load_b(bq, my_b, used);
-        pending = true;
+    // B operands of the rows at byte offsets off[f] (zeros, with no memory
+    // access, for kNone and quads past N): always F * NQ loads, the ones that
+    // read nothing at distinct offsets past B, so that none is merged away
+    auto load_rows = [&](const uint32_t (&off)[F]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                uint32_t o = (off[f] != kNone && b_lane[q] != kNone)
+                                 ? off[f] + b_lane[q]
+                                 : b_bytes + 16u * (uint32_t)(f * NQ + q);
+                // an opaque offset: one load on every path (the compiler would
+                // otherwise split the select into branches, each with a load)
+                asm volatile("" : "+v"(o));
+                bq[f][q] = __builtin_bit_cast(
+                    float4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)o, 0, 0));
+            }
+    };
+    // take up to F batches of four queued columns (the last one partial when
+    // the queue holds fewer) and issue their B loads; the batches in flight
+    // must have been multiplied
+    auto take = [&](uint32_t nbat) __attribute__((always_inline)) {
+        uint32_t off[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            const uint32_t slot = head + 4u * (uint32_t)f + (uint32_t)g;
+            const bool used = (uint32_t)f < nbat && slot < tail;
+            const uint32_t at = slot & (kQueueCols - 1u);
+            const float x = qa[at * 16u + (uint32_t)li];
+            const uint32_t r = qr[at];
+            ap[f] = used ? x : 0.f;
+            off[f] = used ? r : kNone;
+        }
+        load_rows(off);
+        head = head + 4u * nbat < tail ? head + 4u * nbat : tail;
+        inflight = nbat;
     };
 
     auto stage_a = [&](uint32_t q, float4_t& P) __attribute__((always_inline)) {
@@ -241,7 +277,7 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
         } else {
             const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)win, 2 * j);
             const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)win, 2 * j + 1);
-            cb = hi == 0u ? lo : 0xffffffffu;
+            cb = hi == 0u ? lo : kNone;
         }
         uint64_t m = column_mask(__builtin_amdgcn_ballot_w64(P[0] != 0.f),
                                  __builtin_amdgcn_ballot_w64(P[1] != 0.f),
@@ -254,59 +290,77 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
         if (m == 0) return;
         const uint32_t row0 = cb * 16u;
         if (m == kAllColumns) {
-            // every column set: the block is its own four batches, step s
-            // holding columns 4k + s -- lane (r, k)'s own register s -- so it
-            // skips the ring.  The open batch closes first; the four steps'
-            // B rows load together and multiply after the batch in flight.
-            if (fill > 0u) {
-                close(fill);
-                fill = 0;
-            }
+            // every column set: the block is four batches as it stands, batch
+            // s holding columns 4k + s -- lane (r, k)'s own register s -- and
+            // is multiplied here, after the batches in flight
+            multiply_inflight();
+            uint32_t off[F];
             const uint32_t rb = (row0 + 4u * (uint32_t)g) * rowbytes;
-            float4_t t0[NQ], t1[NQ], t2[NQ], t3[NQ];
-            load_b(t0, rb, true);
-            load_b(t1, rb + rowbytes, true);
-            load_b(t2, rb + 2u * rowbytes, true);
-            load_b(t3, rb + 3u * rowbytes, true);
-            if (pending) multiply(ap, bq);
-            pending = false;
-            multiply(P[0], t0);
-            multiply(P[1], t1);
-            multiply(P[2], t2);
-            multiply(P[3], t3);
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                ap[f] = f < 4 ? P[f & 3] : 0.f;
+                off[f] = f < 4 ? rb + (uint32_t)f * rowbytes : kNone;
+            }
+            load_rows(off);
+            inflight = 4;
+            multiply_inflight();
             return;
         }
-        const uint32_t base = ridx * 1024u;
-        *(__attribute__((address_space(3))) float4_t*)(uintptr_t)(ring_lds + base + ring_w) = P;
-        ridx = (ridx + 1u) & (kRing - 1u);
-        do {
-            const uint32_t p = (uint32_t)__builtin_ctzll(m);
-            m &= m - 1;
-            const uint32_t c = 4u * (p >> 4) + (p & 15u);
-            const uint32_t aoff = base + (c >> 2) * 256u + (c & 3u) * 4u;
-            const uint32_t boff = (row0 + c) * rowbytes;
-            if ((uint32_t)g == fill) {
-                my_a = aoff;
-                my_b = boff;
+        // queue the set columns: lane (r, g) writes row r of each of its set
+        // columns 4g + s to the column's slot (columns keep their order)
+        const uint32_t nib = (uint32_t)(m >> (16 * g)) & 0xfu;
+        const uint32_t before = tail + (uint32_t)__builtin_popcountll(m & ((1ull << (16 * g)) - 1ull));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if ((nib >> s) & 1u) {
+                const uint32_t at = (before + (uint32_t)__builtin_popcount(nib & ((1u << s) - 1u))) &
+                                    (kQueueCols - 1u);
+                qa[at * 16u + (uint32_t)li] = P[s];
+                if (li == 0) qr[at] = (row0 + 4u * (uint32_t)g + (uint32_t)s) * rowbytes;
             }
-            if (++fill == 4u) {
-                close(4u);
-                fill = 0;
-            }
-        } while (m != 0);
+        }
+        tail += (uint32_t)__builtin_popcountll(m);
     };
 
+    // One shape per ring pass: one index-window load, D block loads (each
+    // right after its block is processed, for the next pass) and, at the
+    // pass's end, F * NQ B loads (the batches taken from the queue, padded
+    // with loads that read nothing), so every wait counts exactly the loads
+    // it must.  A pass's B rows arrive while the next pass streams its
+    // blocks, and are multiplied at that pass's end.  Only full blocks, and a
+    // pass that leaves too long a queue for the next one, multiply on the
+    // spot.
     if (mine > 0) {
+        // the first pass's loads in the order a pass leaves them: window,
+        // blocks 0 .. D-1, then F * NQ B loads that read nothing (the
+        // scheduling barriers keep the blocks in order), so that the waits
+        // of the first pass and of later ones agree
         float4_t P0, P1, P2, P3, P4, P5, P6, P7;
         uint32_t win = load_cols(0);
+        __builtin_amdgcn_sched_barrier(0);
         stage_a(0, P0);
+        __builtin_amdgcn_sched_barrier(0);
         stage_a(1, P1);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (D > 2) stage_a(2, P2);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (D > 3) stage_a(3, P3);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (D > 4) stage_a(4, P4);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (D > 5) stage_a(5, P5);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (D > 6) stage_a(6, P6);
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (D > 7) stage_a(7, P7);
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            uint32_t none[F];
+#pragma unroll
+            for (int f = 0; f < F; ++f) none[f] = kNone;
+            load_rows(none);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         const uint32_t passes = (mine + D - 1) / D;
         int level = -1;
         for (uint32_t pass = 0; pass < passes; ++pass) {
@@ -350,10 +404,25 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
                 process(P7, win, 7);
                 stage_a(q + D + 7, P7);
             }
+            // pass end: multiply the previous pass's batches, take this
+            // pass's full batches (after the last pass, the partial one too)
+            multiply_inflight();
+            const uint32_t full = (tail - head + (pass + 1 == passes ? 3u : 0u)) >> 2;
+            take(full < (uint32_t)F ? full : (uint32_t)F);
+            // leave room for the next pass's columns
+            while (tail - head > (uint32_t)(kQueueCols - 15 * D)) {
+                multiply_inflight();
+                const uint32_t more = (tail - head) >> 2;
+                take(more < (uint32_t)F ? more : (uint32_t)F);
+            }
             win = nwin;
         }
-        if (fill > 0u) close(fill);
-        if (pending) multiply(ap, bq);
+        multiply_inflight();
+        while (tail != head) {
+            const uint32_t rest = (tail - head + 3u) >> 2;
+            take(rest < (uint32_t)F ? rest : (uint32_t)F);
+            multiply_inflight();
+        }
     }
 
     // sum the waves' partial tiles in wave order and store C
@@ -381,17 +450,26 @@ __global__ __launch_bounds__(64 * W, 16 / W) void spmm_f32_batch_kernel(
     }
 }
 
-// Four waves per workgroup (four workgroups per CU); blocks in flight per
-// wave: 6 at 128 columns (the 128-VGPR budget of four waves per SIMD), 8 at 64.
+// Four waves per workgroup (four workgroups per CU, 128 VGPRs per wave):
+// at 128 columns 6 blocks per pass and 4 batches, at 64 columns 8 and 6.
+// Grids of fewer than 512 workgroups: 16 waves per workgroup (one per CU),
+// 4 blocks per pass, so that short grids still spread each block-row's
+// blocks over many waves.
 template <typename I, int NQ>
 void launch_batch(dim3 grid, hipStream_t s, const I* brp, const I* bci, const float* v, const float* b,
                   float* C, int64_t M, int64_t K, int64_t N, int64_t Kb, const int32_t* order,
                   const I* row_map)
 {
-    constexpr int kW = 4;
-    constexpr int kD = NQ == 2 ? 6 : 8;
-    hipLaunchKernelGGL((spmm_f32_batch_kernel<I, NQ, kW, kD>), grid, dim3(64 * kW), 0, s, brp, bci, v,
-                       b, C, M, K, N, Kb, order, row_map);
+    const bool short_grid = (int64_t)grid.x * grid.y < 512;
+    if (short_grid)
+        hipLaunchKernelGGL((spmm_f32_batch_kernel<I, NQ, 16, 4, 4>), grid, dim3(64 * 16), 0, s, brp,
+                           bci, v, b, C, M, K, N, Kb, order, row_map);
+    else if constexpr (NQ == 2)
+        hipLaunchKernelGGL((spmm_f32_batch_kernel<I, 2, 4, 6, 4>), grid, dim3(64 * 4), 0, s, brp, bci,
+                           v, b, C, M, K, N, Kb, order, row_map);
+    else
+        hipLaunchKernelGGL((spmm_f32_batch_kernel<I, 1, 4, 8, 6>), grid, dim3(64 * 4), 0, s, brp, bci,
+                           v, b, C, M, K, N, Kb, order, row_map);
 }
 
 }  // namespace
