@@ -130,6 +130,10 @@ __global__ __launch_bounds__(64 * W, (W <= 4 ? 16 / W : 1)) void spmm_f32_batch_
 {
     static_assert(NQ == 1 || NQ == 2, "64 or 128 columns per workgroup");
     static_assert(D >= 2 && D <= 8, "2 .. 8 blocks per ring pass");
+    // the block stream of a long grid is read once per call and bypasses the
+    // caches' reuse (non-temporal); a short grid's blocks (the 16-wave
+    // variant) stay cached for the next call
+    constexpr int kAPolicy = W <= 4 ? kNonTemporal : 0;
     static_assert(F >= 4 && F <= 8, "4 .. 8 batches per pass");
     // a pass adds at most 15 D columns to a queue the previous pass end left
     // at most kQueueCols - 15 D long; that bound is at least 4, so a queue
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(64 * W, (W <= 4 ? 16 / W : 1)) void spmm_f32_batch_
     auto stage_a = [&](uint32_t q, float4_t& P) __attribute__((always_inline)) {
         P = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                              a_rsrc, (int)(a_voff + q * (uint32_t)(W * 1024)), 0,
-                                             kNonTemporal));
+                                             kAPolicy));
     };
     auto load_cols = [&](uint32_t q) __attribute__((always_inline)) -> uint32_t {
         return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
