@@ -334,7 +334,34 @@ __global__ __launch_bounds__(64 * W, (W <= 4 ? 16 / W : 1)) void spmm_f32_batch_
     // blocks, and are multiplied at that pass's end.  Only full blocks, and a
     // pass that leaves too long a queue for the next one, multiply on the
     // spot.
-    if (mine > 0) {
+    if (mine > 0 && mine <= (uint32_t)D) {
+        // A single pass (short rows): the blocks it has, then the B rows of
+        // all its batches; no later loads, so no padding is needed.
+        float4_t P0, P1, P2, P3, P4, P5, P6, P7;
+        const uint32_t win = load_cols(0);
+        stage_a(0, P0);
+        if (mine > 1) stage_a(1, P1);
+        if constexpr (D > 2) if (mine > 2) stage_a(2, P2);
+        if constexpr (D > 3) if (mine > 3) stage_a(3, P3);
+        if constexpr (D > 4) if (mine > 4) stage_a(4, P4);
+        if constexpr (D > 5) if (mine > 5) stage_a(5, P5);
+        if constexpr (D > 6) if (mine > 6) stage_a(6, P6);
+        if constexpr (D > 7) if (mine > 7) stage_a(7, P7);
+        process(P0, win, 0);
+        if (mine > 1) process(P1, win, 1);
+        if constexpr (D > 2) if (mine > 2) process(P2, win, 2);
+        if constexpr (D > 3) if (mine > 3) process(P3, win, 3);
+        if constexpr (D > 4) if (mine > 4) process(P4, win, 4);
+        if constexpr (D > 5) if (mine > 5) process(P5, win, 5);
+        if constexpr (D > 6) if (mine > 6) process(P6, win, 6);
+        if constexpr (D > 7) if (mine > 7) process(P7, win, 7);
+        multiply_inflight();
+        while (tail != head) {
+            const uint32_t rest = (tail - head + 3u) >> 2;
+            take(rest < (uint32_t)F ? rest : (uint32_t)F);
+            multiply_inflight();
+        }
+    } else if (mine > 0) {
         // the first pass's loads in the order a pass leaves them: window,
         // blocks 0 .. D-1, then F * NQ B loads that read nothing (the
         // scheduling barriers keep the blocks in order), so that the waits
