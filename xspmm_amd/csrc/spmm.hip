@@ -19,9 +19,15 @@
 //   pack_b_panels + spmm_f16_kernel  any N: B repacked into 16-row panels laid
 //                           out [block_col][n][k16], two blocks per K = 32 operand.
 //
-// fp32 path.  v_mfma_f32_16x16x4f32 takes one k per lane, so B is read
-// row-major directly: lane l loads A[l&15][4g .. 4g+3] (g = l>>4) once per block
-// and issues four MFMAs, step s pairing A[i][4g+s] with B[16*col + 4g + s][n].
+// fp32 kernels.  v_mfma_f32_16x16x4f32 takes one k per lane, so B is read
+// row-major directly:
+//   spmm_f32_batch_kernel   (spmm_f32.hip) default where the grid has at
+//                           least 512 workgroups of 128 columns: the non-zero
+//                           block columns of a block-row packed four to a
+//                           K = 4 batch;
+//   spmm_f32_kernel         short grids: lane l loads A[l&15][4g .. 4g+3]
+//                           (g = l>>4) once per block and issues four MFMAs,
+//                           step s pairing A[i][4g+s] with B[16*col + 4g + s][n].
 //
 // Work split: one workgroup per block-row (grid.x, or the dispatch order of
 // order_rows_kernel), N split over grid.y.

@@ -14,29 +14,31 @@
 // K slots can be filled with any four non-zero block columns of the
 // block-row, from any blocks: all blocks of a block-row add into the same 16
 // rows of C.  Each wave of a workgroup takes every W-th block of its
-// block-row and
+// block-row, D blocks per ring pass, and
 //   1. streams the blocks (16 bytes per lane: lane (r, g) holds row r,
-//      columns 4g .. 4g+3; non-temporal loads, D blocks in flight) and, one
+//      columns 4g .. 4g+3; each block's load issued one pass ahead) and, one
 //      vector load per ring pass, their block columns;
 //   2. forms the block's column mask from four ballots (one per column of a
 //      lane's quad; a column counts when any of its 16 entries is not +-0,
 //      so NaN and Inf count) and a few scalar operations;
-//   3. writes the block to a 4-block LDS ring (lane l writes bytes
-//      16 l .. 16 l + 15, layout [quad][row][4]) and appends its set columns to
-//      a batch of four K slots: slot k is held by lane group k, which records
-//      the slot's LDS column address and the byte offset of its B row;
-//   4. when four slots are set, closes the batch: each lane reads its A'
-//      entry A[r][col(k)] from the ring (one ds_read_b32), and the batch joins
-//      the list of batches closed in this ring pass;
-//   5. at the end of each ring pass, multiplies the previous pass's batches
-//      and issues the B row loads of this pass's batches: lane (n, k) loads
+//   3. queues the set columns in its LDS column queue: lane (r, g) writes
+//      row r of each of its set columns to the column's slot (64 bytes of A'
+//      per column, columns in block and column order), and lane (0, g) the
+//      byte offset of the column's B row;
+//   4. at the end of the pass, multiplies the batches taken at the previous
+//      pass's end and takes up to F batches of four queued columns: lane
+//      (r, k) reads A'[r][slot k] from the queue, and lane (n, k) loads
 //      B[row(k)][n0 + 64 q + 4 n .. +3] as one 16-byte load per 64 columns,
-//      straight into MFMA B operands, so a pass's rows arrive while the next
+//      straight into MFMA B operands.  So a pass's rows arrive while the next
 //      pass streams its blocks.  The multiply issues one MFMA per float4
-//      component j: component j of quad q covers C columns
-//      n0 + 64 q + 4 n + j (n = 0 .. 15).
-// A block whose 16 columns are all set joins the list as four batches as it
-// stands (batch s holding columns 4k + s, which lane (r, k) already holds).
+//      component j: component j of quad q covers C columns n0 + 64 q + 4 n + j.
+// Every pass issues the same loads in the same order (window, D blocks,
+// F * NQ B loads, unused ones at distinct offsets past B that read nothing),
+// so the compiler's waits count exactly the loads they must: a block's wait
+// never drains the blocks behind it or a batch's rows.
+// A block whose 16 columns are all set is multiplied where it is met, after
+// the batches in flight: four batches as it stands (batch s holding columns
+// 4k + s, which lane (r, k) already holds) with their 4 x 16 B rows.
 // The waves' partial tiles are summed through LDS in wave order and stored as
 // 16-byte rows.  Skipped columns would add exact zeros (products of +-0 and
 // finite B entries), so C equals the full product for finite B; a non-finite
@@ -482,7 +484,9 @@ __global__ __launch_bounds__(64 * W, (W <= 4 ? 16 / W : 1)) void spmm_f32_batch_
 }
 
 // Four waves per workgroup (four workgroups per CU, 128 VGPRs per wave):
-// at 128 columns 6 blocks per pass and 4 batches, at 64 columns 8 and 6.
+// 8 blocks per pass, and 4 batches at 128 columns, 6 at 64 (at 128 columns,
+// templates in fp32: 6 blocks per pass 177.7-178.6 us, 8 173.3-174.0 us, 4
+// 183.2-184.2 us).
 // Grids of fewer than 512 workgroups: 16 waves per workgroup (one per CU),
 // 4 blocks per pass, so that short grids still spread each block-row's
 // blocks over many waves.
@@ -496,7 +500,7 @@ void launch_batch(dim3 grid, hipStream_t s, const I* brp, const I* bci, const fl
         hipLaunchKernelGGL((spmm_f32_batch_kernel<I, NQ, 16, 4, 4>), grid, dim3(64 * 16), 0, s, brp,
                            bci, v, b, C, M, K, N, Kb, order, row_map);
     else if constexpr (NQ == 2)
-        hipLaunchKernelGGL((spmm_f32_batch_kernel<I, 2, 4, 6, 4>), grid, dim3(64 * 4), 0, s, brp, bci,
+        hipLaunchKernelGGL((spmm_f32_batch_kernel<I, 2, 4, 8, 4>), grid, dim3(64 * 4), 0, s, brp, bci,
                            v, b, C, M, K, N, Kb, order, row_map);
     else
         hipLaunchKernelGGL((spmm_f32_batch_kernel<I, 1, 4, 8, 6>), grid, dim3(64 * 4), 0, s, brp, bci,
