@@ -199,16 +199,30 @@ int xspmm_spmm_pipeline(int vtype, int itype, int64_t M, int64_t K, int64_t nnz,
 
 /*
  * Device bytes of the temporaries that the last xspmm_spmm_pipeline call on
- * the calling thread took from the device's memory pool (0 before any call):
- * the permuted CSR, the permuted-order C and the BCSR arrays.  The BCSR
- * arrays are sized from the bound min(nnz, Mb * Kb) on the block count while
- * that bound's block values fit 1 GiB, else exactly after the block count is
- * read.
+ * the calling thread held at once from the device's memory pool (0 before
+ * any call): the permuted CSR, the permuted-order C and the BCSR arrays, or
+ * for the packed form (xspmm_pipeline_last_form) the column batches.  The
+ * BCSR arrays are sized from the bound min(nnz, Mb * Kb) on the block count
+ * while that bound's block values fit 1 GiB, else exactly after the block
+ * count is read; the batches from the bound min(2 nnz / 33 + min(4 Mb, nnz),
+ * Mb * ceil(Kb / 2)) at 1152 bytes each, likewise.
  * No counterpart in the reference (whose pipeline makes a hipMalloc per
  * temporary, src/hip/unstructured_mtx_mul.hip:31-100); it lets a caller see
  * the pipeline's memory footprint.
  */
 int xspmm_pipeline_temp_bytes(int64_t* bytes_out);
+
+/*
+ * Sets *packed_out to 1 when the last xspmm_spmm_pipeline call on the calling
+ * thread converted A into packed column batches and multiplied those (fp16,
+ * N % 8 == 0, K <= 167296, strictly increasing columns per row, finite
+ * values, and batches that save at least a quarter of the block bytes), to 0
+ * when it took the BCSR blocks.  C is the same bit for bit either way.
+ * No counterpart in the reference, whose pipeline always converts to BCSR
+ * (src/hip/unstructured_mtx_mul.hip:58-61, :86-89); it lets a caller see
+ * which form ran.
+ */
+int xspmm_pipeline_last_form(int* packed_out);
 
 /*
  * Prepared Tier-2 product ("plan"): the pipeline's clustering, permutation

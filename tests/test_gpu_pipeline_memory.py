@@ -6,7 +6,8 @@ and fill then run with no host round trip), and exactly, after reading the
 count, above it -- as the reference's conversion does
 (src/core/conversion.cpp:66-73).  A matrix of full 16x16 blocks has
 nnz = 256 * nnzb, so there the bound is 256x the exact size.
-xspmm_pipeline_temp_bytes reports what the last call took.
+xspmm_pipeline_temp_bytes reports what the last call took.  fp16 products
+the packed kernel covers take packed column batches instead of BCSR arrays.
 """
 from __future__ import annotations
 
@@ -69,8 +70,9 @@ def test_full_blocks_take_exact_bcsr(torch):
 
 def test_small_matrix_keeps_fused_bound(torch):
     """A small matrix keeps the bound-sized arrays (no host round trip): the
-    reported bytes cover min(nnz, Mb * Kb) blocks; C against fp64."""
-    p = synth.random_csr(500, 700, 64, 0.02, seed=4, dtype=np.float16)
+    reported bytes cover min(nnz, Mb * Kb) blocks; C against fp64.  (fp32:
+    the fp16 pipeline converts to packed column batches instead.)"""
+    p = synth.random_csr(500, 700, 64, 0.02, seed=4, dtype=np.float32)
     Mb, Kb = (p.M + 15) // 16, (p.K + 15) // 16
     cap = min(p.nnz, Mb * Kb)
     A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
@@ -78,7 +80,31 @@ def test_small_matrix_keeps_fused_bound(torch):
     C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
     torch.cuda.synchronize()
     used = X.pipeline_temp_bytes()
-    assert used >= cap * 256 * 2 + cap * 4
+    assert not X.pipeline_last_packed()
+    assert used >= cap * 256 * 4 + cap * 4
     brp, bci, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    ref = oracle.bcsr_spmm_f64(p.M, p.K, p.N, brp, bci, bv, p.B)
+    assert oracle.errors(C.cpu().numpy(), ref)["rel_frob"] <= 1e-5
+
+
+def test_packed_form_takes_no_block_arrays(torch):
+    """The fp16 pipeline's packed form: per block-row and wave a batch count
+    and offset, and 1152 bytes (A' operand and B-row indices) per batch,
+    sized from the bound 2 nnz / 33 + min(Mb * 4, nnz) on the batch count;
+    no padded blocks (which would take 512 bytes per block)."""
+    p = synth.random_csr(2000, 6000, 64, 0.004, seed=5, dtype=np.float16)
+    Mb = (p.M + 15) // 16
+    brp, bci, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    nnzb = len(bci)
+    A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
+    B = torch.as_tensor(p.B).cuda()
+    C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
+    torch.cuda.synchronize()
+    assert X.pipeline_last_packed()
+    used = X.pipeline_temp_bytes()
+    bound = 2 * p.nnz // 33 + min(Mb * 4, p.nnz)
+    print(f"packed form temporaries {used} B; BCSR blocks would take {nnzb * 512} B", flush=True)
+    assert used < nnzb * 512 // 2
+    assert used <= bound * 1152 + Mb * 64 + 16 * 256
     ref = oracle.bcsr_spmm_f64(p.M, p.K, p.N, brp, bci, bv, p.B)
     assert oracle.errors(C.cpu().numpy(), ref)["rel_frob"] <= 2e-3

@@ -102,6 +102,8 @@ def load():
     L.xspmm_mtx_export.argtypes = [p, i32, i32, p, p, p]
     L.xspmm_mtx_free.restype = i32
     L.xspmm_mtx_free.argtypes = [p]
+    L.xspmm_pipeline_last_form.restype = i32
+    L.xspmm_pipeline_last_form.argtypes = [C.POINTER(C.c_int)]
     L.xspmm_pipeline_temp_bytes.restype = i32
     L.xspmm_pipeline_temp_bytes.argtypes = [C.POINTER(C.c_int64)]
     L.xspmm_spmm_pipeline.restype = i32
@@ -435,6 +437,14 @@ def pipeline_temp_bytes() -> int:
     out = C.c_int64(0)
     _check(load().xspmm_pipeline_temp_bytes(C.byref(out)))
     return int(out.value)
+
+
+def pipeline_last_packed() -> bool:
+    """Whether the last spmm_pipeline call on this thread multiplied packed
+    column batches (C ABI xspmm_pipeline_last_form)."""
+    out = C.c_int(0)
+    _check(load().xspmm_pipeline_last_form(C.byref(out)))
+    return bool(out.value)
 
 
 class SpMMPlan:

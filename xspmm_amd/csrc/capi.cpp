@@ -266,6 +266,14 @@ int xspmm_pipeline_temp_bytes(int64_t* bytes_out)
     });
 }
 
+int xspmm_pipeline_last_form(int* packed_out)
+{
+    return guarded([&] {
+        require(packed_out != nullptr, "xspmm_pipeline_last_form: packed_out is null.");
+        *packed_out = last_pipeline_packed() ? 1 : 0;
+    });
+}
+
 int xspmm_plan_create(int vtype, int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
                       const void* ci, const void* vals, int64_t hw_block_size,
                       int optimize_pattern, double* timings, void* stream, xspmm_plan_t* plan_out)

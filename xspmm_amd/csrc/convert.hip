@@ -18,6 +18,8 @@
 //          rows are all strictly increasing in column cannot hold duplicates and
 //          is scattered with all threads; otherwise one thread walks each row in
 //          order so the last duplicate wins.
+#include <algorithm>
+
 #include "internal.hpp"
 #include "scan.hpp"
 
@@ -29,6 +31,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int64_t kMaxStripRows = 1024;
 constexpr size_t kMaxLds = 64 * 1024;
+constexpr int kEntryUnroll = 4;  // CSR entries per thread per loop step
 
 struct StripView {
     int64_t* bounds;  // [nr+1] row starts of the strip (clamped to [0, nnz])
@@ -88,18 +91,31 @@ __device__ void build_strip_bitmap(int64_t M, int64_t K, int64_t nnz, const I* _
     __syncthreads();
     if (*s_bad) return;  // uniform: every thread sees the same flag
 
+    // kEntryUnroll entries per thread in flight; a bit already set is not
+    // set again (in a dense block every bit is met once per row); the row
+    // search runs only where the next column does not increase
     const int64_t e0 = sv.bounds[0];
     const int64_t e1 = sv.bounds[sv.nr];
-    for (int64_t idx = e0 + threadIdx.x; idx < e1; idx += kThreads) {
-        const int64_t c = (int64_t)ci[idx];
-        if (c < 0 || c >= K) {
-            *s_bad = 1;
-            continue;
+    for (int64_t i0 = e0 + threadIdx.x; i0 < e1; i0 += (int64_t)kThreads * kEntryUnroll) {
+        int64_t c[kEntryUnroll], cn[kEntryUnroll];
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            c[u] = idx < e1 ? (int64_t)ci[idx] : 0;
+            cn[u] = idx + 1 < e1 ? (int64_t)ci[idx + 1] : 0;
         }
-        const int64_t bc = c / cb;
-        atomicOr(&bitmap[bc >> 5], 1u << (bc & 31));
-        if (idx + 1 < e1 && !row_starts_at(sv, idx + 1)) {
-            if ((int64_t)ci[idx + 1] <= c) *s_unsorted = 1;
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            if (idx >= e1) continue;
+            if (c[u] < 0 || c[u] >= K) {
+                *s_bad = 1;
+                continue;
+            }
+            const int64_t bc = cb == 16 ? c[u] >> 4 : c[u] / cb;
+            const uint32_t bit = 1u << (bc & 31);
+            if (!(bitmap[bc >> 5] & bit)) atomicOr(&bitmap[bc >> 5], bit);
+            if (idx + 1 < e1 && cn[u] <= c[u] && !row_starts_at(sv, idx + 1)) *s_unsorted = 1;
         }
     }
     __syncthreads();
@@ -239,6 +255,438 @@ ConvGeometry conv_geometry(int64_t M, int64_t K, int64_t nnz, int64_t rb, int64_
     return g;
 }
 
+
+// ---------------------------------------------------------------------------
+// CSR -> packed column batches (the Tier-2 pipeline's fp16 form).
+//
+// The fp16 column-batch SpMM (spmm.hip) turns each block-row's BCSR blocks
+// into column batches, and its pack mode stores them for
+// spmm_f16_packed_kernel: per (block-row, wave) the batches the wave forms,
+// each an A' operand (64 lanes x 16 bytes) and 32 B-row indices.  What the
+// batches hold is fixed by A alone: block-row br's blocks are its distinct
+// column blocks in ascending order, block pair j is blocks (2j, 2j+1), wave
+// w takes pairs w, w + W, ... in order, a pair's set columns (a column is set
+// when any of its 16 entries has non-zero fp16 bits) take slots in the pair
+// mask's bit order, and a pair that does not fit the open batch's 32 slots
+// closes it.  Two kernels form the same batches straight from the CSR
+// strips, one workgroup per strip, with every per-block quantity in LDS:
+//   pack_analyse_kernel  the strip's column-block bitmap and its popcount
+//                        prefix (a block's rank), the pair words (column
+//                        masks of blocks 2j and 2j+1), then per wave the
+//                        batch walk, counting batches;
+//   pack_scan_kernel     (one workgroup) scans the block counts -> brp and
+//                        the batch counts -> offsets, and decides on the
+//                        device whether the packed form is taken;
+//   pack_emit_kernel     the same analysis again, the walk recording each
+//                        pair's batch and first slot, then the strip's A'
+//                        operands and B-row indices: cleared, then every
+//                        used slot's B row and every entry's value stored.
+// The result equals the pack mode's byte for byte when every strip's rows
+// hold strictly increasing columns and every value is finite (the flags
+// below report strips and values outside that, and the caller then keeps
+// the BCSR path): A' then holds each set column's exact values, with +0.0
+// where the pack mode's compaction turns -0.0 into +0.0.
+//
+// Batch count bound.  In one wave's walk with m batches of s_1 .. s_m slots
+// (S in all), batch i closed because the next pair did not fit, so
+// s_i + s_{i+1} >= 33 for i < m; summed, 2 S - s_1 - s_m >= 33 (m - 1), so
+// m <= (2 S - 2) / 33 + 1.  Each slot holds a non-zero entry, so over all
+// walks the batches number at most 2 nnz / 33 plus the walks with a batch
+// (at most min(Mb * W, nnz)), and at most the pair count Mb * ceil(Kb / 2)
+// (a batch holds at least one pair): csr_pack_batch_bound.
+
+constexpr uint32_t kPackFlagUnsorted = 2;   // a strip's row is not strictly increasing
+constexpr uint32_t kPackFlagNonFinite = 4;  // an Inf or NaN value
+constexpr int kPackWalkUnroll = 8;
+
+// the batch kernel's pair-mask bit of pair column pc (0 .. 31): lane group
+// g = pc / 8 holds pair columns 8g .. 8g+7 as halves e; half 2d goes to bit
+// 4g + d, half 2d + 1 to bit 16 + 4g + d
+__device__ __forceinline__ uint32_t pair_bit(uint32_t pc)
+{
+    const uint32_t g = pc >> 3, e = pc & 7u;
+    return 16u * (e & 1u) + 4u * g + (e >> 1);
+}
+
+// the pair column of pair-mask bit b (inverse of pair_bit)
+__device__ __forceinline__ uint32_t bit_pair_col(uint32_t b)
+{
+    const uint32_t hb = b >> 4, g = (b >> 2) & 3u, d = b & 3u;
+    return 8u * g + 2u * d + hb;
+}
+
+// the even bits of x (bit 2i -> bit i)
+__device__ __forceinline__ uint32_t even_bits(uint32_t x)
+{
+    x &= 0x55555555u;
+    x = (x | (x >> 1)) & 0x33333333u;
+    x = (x | (x >> 2)) & 0x0f0f0f0fu;
+    x = (x | (x >> 4)) & 0x00ff00ffu;
+    return (x | (x >> 8)) & 0x0000ffffu;
+}
+
+// pair mask of a pair word m (bit c: column c of block 2j; bit 16 + c:
+// column c of block 2j + 1): pair column pc = 8g + e has pair_bit(pc), which
+// is bit 4g + e/2 of the even-e or the odd-e half.  A bit permutation, so
+// popc(pair_mask(m)) == popc(m).
+__device__ __forceinline__ uint32_t pair_mask(uint32_t m)
+{
+    return even_bits(m) | (even_bits(m >> 1) << 16);
+}
+
+// MFMA K position that carries batch slot s (inverse of the batch kernel's
+// kslot: k = 8 (s' >> 2) + 4 h + (s' & 3), s = 16 h + s')
+__device__ __forceinline__ uint32_t slot_kpos(uint32_t s)
+{
+    const uint32_t h = s >> 4, sp = s & 15u;
+    return 8u * (sp >> 2) + 4u * h + (sp & 3u);
+}
+
+// LDS of the packed-form strip kernels (byte offsets): the strip's row
+// bounds, the column-block bitmap and its per-word popcount prefix, the pair
+// words; pack_emit_kernel adds each pair's batch info, the waves' first
+// batch and each block's column block.
+struct PackLds {
+    uint32_t bitmap, prefix, pw, analyse_bytes, pinfo, ob, bcl, emit_bytes;
+};
+
+__host__ __device__ inline PackLds pack_lds(int64_t Kb, int nw)
+{
+    const uint32_t nwords = (uint32_t)(Kb > 0 ? (Kb + 31) / 32 : 1);
+    const uint32_t npc = (uint32_t)((Kb + 1) / 2 + 1);  // pair capacity
+    PackLds L;
+    L.bitmap = 17 * 8;
+    L.prefix = L.bitmap + 4 * nwords;
+    L.pw = L.prefix + 4 * nwords;
+    L.analyse_bytes = L.pw + 4 * npc;
+    L.pinfo = L.analyse_bytes;
+    L.ob = (L.pinfo + 4 * npc + 7) & ~7u;
+    L.bcl = L.ob + 8 * (uint32_t)(nw + 1);
+    L.emit_bytes = (L.bcl + 2 * (uint32_t)(Kb > 0 ? Kb : 1) + 15) & ~15u;
+    return L;
+}
+
+// One strip's analysis, shared by both kernels: bitmap, prefix, *nb (the
+// strip's block count) and the pair words.  Leaves *s_bad / *s_unsorted set
+// for an invalid or unsorted strip (the pair words are then not formed) and
+// *s_nonfinite for an Inf or NaN value.  Ends with a barrier.
+template <typename I>
+__device__ void pack_strip(int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp,
+                           const I* __restrict__ ci, const uint16_t* __restrict__ vals,
+                           int64_t nwords, unsigned char* smem, const PackLds& L, StripView& sv,
+                           int* s_unsorted, int* s_bad, int* s_nonfinite, int64_t* red, int64_t* nb)
+{
+    uint32_t* bitmap = reinterpret_cast<uint32_t*>(smem + L.bitmap);
+    uint32_t* prefix = reinterpret_cast<uint32_t*>(smem + L.prefix);
+    uint32_t* pw = reinterpret_cast<uint32_t*>(smem + L.pw);
+    sv.bounds = reinterpret_cast<int64_t*>(smem);
+    if (threadIdx.x == 0) *s_nonfinite = 0;
+    build_strip_bitmap(M, K, nnz, rp, ci, 16, 16, nwords, sv, bitmap, s_unsorted, s_bad);
+    *nb = 0;
+    if (*s_bad) return;  // uniform
+    const int64_t per = (nwords + kThreads - 1) / kThreads;
+    const int64_t w0 = (int64_t)threadIdx.x * per;
+    const int64_t w1 = (w0 + per < nwords) ? w0 + per : nwords;
+    int64_t mine = 0;
+    for (int64_t w = w0; w < w1; ++w) mine += __popc(bitmap[w]);
+    int64_t total;
+    int64_t run = block_exclusive_scan(mine, &total, red);
+    for (int64_t w = w0; w < w1; ++w) {
+        prefix[w] = (uint32_t)run;
+        run += __popc(bitmap[w]);
+    }
+    *nb = total;
+    if (*s_unsorted) return;  // uniform (set before build_strip_bitmap's last barrier)
+    const int64_t npairs = (total + 1) >> 1;
+    for (int64_t j = threadIdx.x; j < npairs; j += kThreads) pw[j] = 0u;
+    __syncthreads();  // prefix and cleared pair words before the ORs
+    const int64_t e0 = sv.bounds[0];
+    const int64_t e1 = sv.bounds[sv.nr];
+    bool nonfinite = false;
+    for (int64_t i0 = e0 + threadIdx.x; i0 < e1; i0 += (int64_t)kThreads * kEntryUnroll) {
+        uint32_t v[kEntryUnroll], c[kEntryUnroll];
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            v[u] = idx < e1 ? (uint32_t)vals[idx] : 0u;
+            c[u] = idx < e1 ? (uint32_t)ci[idx] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            if ((v[u] & 0x7c00u) == 0x7c00u) nonfinite = true;
+            if (v[u] == 0u) continue;  // also the entries past the strip
+            const uint32_t bc = c[u] >> 4;
+            const uint32_t w = bc >> 5;
+            const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (bc & 31u)) - 1u));
+            const uint32_t bit = 1u << (16u * (rank & 1u) + (c[u] & 15u));
+            if (!(pw[rank >> 1] & bit)) atomicOr(&pw[rank >> 1], bit);
+        }
+    }
+    if (nonfinite) *s_nonfinite = 1;
+    __syncthreads();
+}
+
+// One wave's batch walk over pairs t, t + nw, ... (< npairs): returns the
+// wave's batch count; with Record, pinfo[j] = (batch << 6) | first slot for
+// every pair with a set column.  The pair words are read kPackWalkUnroll
+// ahead so that the LDS latency is paid once per group.
+template <bool Record>
+__device__ __forceinline__ uint32_t pack_walk(const uint32_t* pw, uint32_t* pinfo, int64_t t, int nw,
+                                              int64_t npairs)
+{
+    uint32_t pending = 0, nbatch = 0;
+    for (int64_t j0 = t; j0 < npairs; j0 += (int64_t)kPackWalkUnroll * nw) {
+        uint32_t cnt[kPackWalkUnroll];
+#pragma unroll
+        for (int u = 0; u < kPackWalkUnroll; ++u) {
+            const int64_t j = j0 + (int64_t)u * nw;
+            cnt[u] = j < npairs ? (uint32_t)__popc(pw[j]) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kPackWalkUnroll; ++u) {
+            if (cnt[u] == 0u) continue;
+            if (pending + cnt[u] > 32u) {
+                ++nbatch;
+                pending = 0;
+            }
+            if (Record) pinfo[j0 + (int64_t)u * nw] = (nbatch << 6) | pending;
+            pending += cnt[u];
+        }
+    }
+    return nbatch + (pending > 0u ? 1u : 0u);
+}
+
+// err: set for an invalid row_ptr or column (as the count pass does);
+// bcounts[br] = the strip's block count; counts[br * nw + w] = wave w's
+// batch count (0 for an unsorted strip); flags as above.
+template <typename I>
+__global__ __launch_bounds__(kThreads) void pack_analyse_kernel(
+    int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp, const I* __restrict__ ci,
+    const uint16_t* __restrict__ vals, int64_t nwords, int64_t Kb, int nw, I* __restrict__ bcounts,
+    int32_t* __restrict__ counts, int* __restrict__ err, unsigned int* __restrict__ flags)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int s_unsorted, s_bad, s_nonfinite;
+    __shared__ int64_t red[kThreads / 64];
+    const PackLds L = pack_lds(Kb, nw);
+    StripView sv;
+    int64_t nb;
+    pack_strip(M, K, nnz, rp, ci, vals, nwords, smem, L, sv, &s_unsorted, &s_bad, &s_nonfinite, red, &nb);
+    const int64_t br = blockIdx.x;
+    if (threadIdx.x == 0) {
+        bcounts[br] = (I)nb;
+        if (s_bad) atomicOr(err, 1);
+        else if (s_unsorted) atomicOr(flags, kPackFlagUnsorted);
+        else if (s_nonfinite) atomicOr(flags, kPackFlagNonFinite);
+    }
+    if (threadIdx.x < nw) {
+        uint32_t n = 0;
+        if (!s_bad && !s_unsorted)
+            n = pack_walk<false>(reinterpret_cast<const uint32_t*>(smem + L.pw), nullptr, threadIdx.x, nw,
+                                 (nb + 1) >> 1);
+        counts[br * nw + threadIdx.x] = (int32_t)n;
+    }
+}
+
+// status[0..4] = {batches, blocks, err, flags, go}: go (the packed form is
+// taken) when the input is valid, sorted and finite, the grid is not fully
+// populated, there is a batch, the batches fit the cap of the arrays they
+// are written to and take at most three quarters of the BCSR blocks' bytes
+// (1152 B per batch against 512 B per block: 3 * batches <= blocks).
+__device__ __forceinline__ void pack_decide(int64_t nbat, int64_t nnzb, int e, unsigned int f, int64_t Mb,
+                                            int64_t Kb, int64_t cap, int64_t* __restrict__ status)
+{
+    const bool go = e == 0 && f == 0u && nbat > 0 && nbat <= cap && nnzb != Mb * Kb && 3 * nbat <= nnzb;
+    status[0] = nbat;
+    status[1] = nnzb;
+    status[2] = (int64_t)e;
+    status[3] = (int64_t)f;
+    status[4] = go ? 1 : 0;
+}
+
+template <typename I>
+__global__ void pack_decide_kernel(const int64_t* __restrict__ off_end, const I* __restrict__ brp_end,
+                                   const int* __restrict__ err, const unsigned int* __restrict__ flags,
+                                   int64_t Mb, int64_t Kb, int64_t cap, int64_t* __restrict__ status)
+{
+    if (threadIdx.x == 0 && blockIdx.x == 0)
+        pack_decide(*off_end, (int64_t)*brp_end, *err, *flags, Mb, Kb, cap, status);
+}
+
+// One workgroup scans both count arrays and decides (one launch instead of
+// two device-wide scans and pack_decide_kernel) while the batch counts
+// number at most kPackScanMax.
+constexpr int kPackScanThreads = 1024;
+constexpr int kPackScanItems = 8;
+constexpr int64_t kPackScanMax = int64_t(1) << 17;
+
+__device__ __forceinline__ int64_t wg_exclusive_scan_1024(int64_t v, int64_t* total, int64_t* red)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t incl = wave_inclusive_scan(v);
+    if (lane == 63) red[wave] = incl;
+    __syncthreads();
+    int64_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kPackScanThreads / 64; ++w) {
+        const int64_t x = red[w];
+        if (w < wave) before += x;
+        all += x;
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - v;
+}
+
+// out[0..n] = exclusive prefix sums of in[0..n), out[n] = total (returned)
+template <typename T, typename O>
+__device__ int64_t wg_scan_array(const T* __restrict__ in, int64_t n, O* __restrict__ out, int64_t* red)
+{
+    int64_t carry = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += (int64_t)kPackScanThreads * kPackScanItems) {
+        const int64_t base = c0 + (int64_t)threadIdx.x * kPackScanItems;
+        int64_t v[kPackScanItems];
+        int64_t sum = 0;
+#pragma unroll
+        for (int e = 0; e < kPackScanItems; ++e) {
+            v[e] = base + e < n ? (int64_t)in[base + e] : 0;
+            sum += v[e];
+        }
+        int64_t tot;
+        int64_t run = carry + wg_exclusive_scan_1024(sum, &tot, red);
+#pragma unroll
+        for (int e = 0; e < kPackScanItems; ++e) {
+            if (base + e < n) out[base + e] = (O)run;
+            run += v[e];
+        }
+        carry += tot;
+    }
+    if (threadIdx.x == 0) out[n] = (O)carry;
+    return carry;
+}
+
+template <typename I>
+__global__ __launch_bounds__(kPackScanThreads) void pack_scan_kernel(
+    const I* __restrict__ bcounts, int64_t Mb, const int32_t* __restrict__ counts, int nw,
+    I* __restrict__ brp, int64_t* __restrict__ offsets, const int* __restrict__ err,
+    const unsigned int* __restrict__ flags, int64_t Kb, int64_t cap, int64_t* __restrict__ status)
+{
+    __shared__ int64_t red[kPackScanThreads / 64];
+    const int64_t nnzb = wg_scan_array(bcounts, Mb, brp, red);
+    const int64_t nbat = wg_scan_array(counts, Mb * nw, offsets, red);
+    if (threadIdx.x == 0) pack_decide(nbat, nnzb, *err, *flags, Mb, Kb, cap, status);
+}
+
+// Writes strip br's batches [offsets[br * nw], offsets[br * nw + nw]) when
+// status[4] (go) is set: A' operands (1 KB each; lane (r, g) holds
+// A'[r][4g .. 4g+3] and A'[r][16 + 4g .. 16 + 4g + 3]) and B-row indices
+// (32 per batch, 0xffffffff for an unused slot).  Batches at or above cap
+// are never written.
+template <typename I>
+__global__ __launch_bounds__(kThreads) void pack_emit_kernel(
+    int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp, const I* __restrict__ ci,
+    const uint16_t* __restrict__ vals, int64_t nwords, int64_t Kb, int nw,
+    const int64_t* __restrict__ offsets, const int64_t* __restrict__ status, int64_t cap,
+    uint16_t* __restrict__ a, uint32_t* __restrict__ rows)
+{
+    if (status[4] == 0) return;  // uniform: before any barrier
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int s_unsorted, s_bad, s_nonfinite;
+    __shared__ int64_t red[kThreads / 64];
+    const PackLds L = pack_lds(Kb, nw);
+    StripView sv;
+    int64_t nb;
+    pack_strip(M, K, nnz, rp, ci, vals, nwords, smem, L, sv, &s_unsorted, &s_bad, &s_nonfinite, red, &nb);
+    if (s_bad || s_unsorted || s_nonfinite) return;  // uniform; excluded by go
+    const uint32_t* bitmap = reinterpret_cast<const uint32_t*>(smem + L.bitmap);
+    const uint32_t* prefix = reinterpret_cast<const uint32_t*>(smem + L.prefix);
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(smem + L.pw);
+    uint32_t* pinfo = reinterpret_cast<uint32_t*>(smem + L.pinfo);
+    int64_t* ob = reinterpret_cast<int64_t*>(smem + L.ob);
+    uint16_t* bcl = reinterpret_cast<uint16_t*>(smem + L.bcl);
+    const int64_t br = blockIdx.x;
+    const int64_t npairs = (nb + 1) >> 1;
+
+    // each block's column block, by rank
+    {
+        const int64_t per = (nwords + kThreads - 1) / kThreads;
+        const int64_t w0 = (int64_t)threadIdx.x * per;
+        const int64_t w1 = (w0 + per < nwords) ? w0 + per : nwords;
+        for (int64_t w = w0; w < w1; ++w) {
+            uint32_t bits = bitmap[w];
+            uint32_t o = prefix[w];
+            while (bits) {
+                bcl[o++] = (uint16_t)(w * 32 + (__ffs(bits) - 1));
+                bits &= bits - 1;
+            }
+        }
+    }
+    if (threadIdx.x <= nw) ob[threadIdx.x] = offsets[br * nw + threadIdx.x];
+    // clear the strip's batches (A' zero, indices unused) while the walk runs
+    {
+        const int64_t q0 = offsets[br * nw];
+        int64_t q1 = offsets[br * nw + nw];
+        if (q1 > cap) q1 = cap;
+        uint4* a4 = reinterpret_cast<uint4*>(a);
+        uint4* r4 = reinterpret_cast<uint4*>(rows);
+        for (int64_t i = q0 * 64 + threadIdx.x; i < q1 * 64; i += kThreads) a4[i] = make_uint4(0, 0, 0, 0);
+        const uint32_t u = 0xffffffffu;
+        for (int64_t i = q0 * 8 + threadIdx.x; i < q1 * 8; i += kThreads) r4[i] = make_uint4(u, u, u, u);
+    }
+    if (threadIdx.x < nw) (void)pack_walk<true>(pw, pinfo, threadIdx.x, nw, npairs);
+    __syncthreads();  // clears complete; bcl, ob and pinfo visible
+
+    // every used slot's B-row index: one thread per pair
+    for (int64_t j = threadIdx.x; j < npairs; j += kThreads) {
+        uint32_t pm = pair_mask(pw[j]);
+        if (pm == 0u) continue;
+        const uint32_t info = pinfo[j];
+        const int64_t bi = ob[j % nw] + (int64_t)(info >> 6);
+        if (bi >= cap) continue;
+        uint32_t slot = info & 63u;
+        while (pm) {
+            const uint32_t b = (uint32_t)(__ffs(pm) - 1);
+            pm &= pm - 1;
+            const uint32_t pc = bit_pair_col(b);
+            const uint32_t row = 16u * (uint32_t)bcl[2 * j + (pc >> 4)] + (pc & 15u);
+            rows[bi * 32 + slot_kpos(slot)] = row;
+            ++slot;
+        }
+    }
+    // every non-zero entry's fp16 bits at its slot; -0.0 leaves the +0.0
+    const int64_t e0 = sv.bounds[0];
+    const int64_t e1 = sv.bounds[sv.nr];
+    for (int64_t i0 = e0 + threadIdx.x; i0 < e1; i0 += (int64_t)kThreads * kEntryUnroll) {
+        uint16_t v[kEntryUnroll];
+        uint32_t c[kEntryUnroll];
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            v[u] = idx < e1 ? vals[idx] : (uint16_t)0;
+            c[u] = idx < e1 ? (uint32_t)ci[idx] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            if ((v[u] & 0x7fffu) == 0u) continue;  // also the entries past the strip
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            const uint32_t bc = c[u] >> 4;
+            const uint32_t w = bc >> 5;
+            const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (bc & 31u)) - 1u));
+            const uint32_t j = rank >> 1;
+            const uint32_t pm = pair_mask(pw[j]);
+            const uint32_t info = pinfo[j];
+            const uint32_t bit = pair_bit(16u * (rank & 1u) + (c[u] & 15u));
+            const uint32_t slot = (info & 63u) + (uint32_t)__popc(pm & ((1u << bit) - 1u));
+            const int64_t bi = ob[j % (uint32_t)nw] + (int64_t)(info >> 6);
+            if (bi >= cap) continue;
+            const int64_t r = row_of(sv, idx);
+            const uint32_t lane = ((slot & 15u) >> 2) * 16u + (uint32_t)r;
+            const uint32_t t = (slot >> 4) * 4u + (slot & 3u);
+            a[(bi * 64 + lane) * 8 + t] = v[u];
+        }
+    }
+}
 }  // namespace
 
 template <typename I>
@@ -311,6 +759,85 @@ XSPMM_INST_FILL(uint16_t, int64_t)
 XSPMM_INST_FILL(float, int32_t)
 XSPMM_INST_FILL(float, int64_t)
 #undef XSPMM_INST_FILL
+
+bool csr_pack_covers(int64_t K)
+{
+    const int64_t Kb = (K + 15) / 16;
+    return Kb > 0 && pack_lds(Kb, spmm_batch_waves()).emit_bytes <= kMaxLds;
+}
+
+int64_t csr_pack_batch_bound(int64_t M, int64_t K, int64_t nnz)
+{
+    const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
+    const int64_t by_slots = 2 * nnz / 33 + std::min<int64_t>(Mb * spmm_batch_waves(), nnz);
+    return std::min<int64_t>(by_slots, Mb * ((Kb + 1) / 2));  // a batch holds a pair
+}
+
+template <typename I>
+void csr_pack_analyse(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                      const uint16_t* vals, I* bcounts, I* brp, int32_t* counts, int64_t* offsets,
+                      int* err, unsigned int* flags, int64_t cap, int64_t* status, hipStream_t s)
+{
+    const ConvGeometry g = conv_geometry(M, K, nnz, 16, 16);
+    if (!csr_pack_covers(K)) throw std::invalid_argument("csr_pack_analyse: K above the packed form's limit.");
+    const int nw = spmm_batch_waves();
+    const PackLds L = pack_lds(g.Kb, nw);
+    hipLaunchKernelGGL(set_value_kernel<int>, dim3(1), dim3(64), 0, s, err, 0);
+    XSPMM_LAUNCH_CHECK();
+    hipLaunchKernelGGL(set_value_kernel<unsigned int>, dim3(1), dim3(64), 0, s, flags, 0u);
+    XSPMM_LAUNCH_CHECK();
+    if (g.Mb > 0) {
+        hipLaunchKernelGGL(pack_analyse_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.analyse_bytes, s,
+                           M, K, nnz, rp, ci, vals, g.nwords, g.Kb, nw, bcounts, counts, err, flags);
+        XSPMM_LAUNCH_CHECK();
+    }
+    if (g.Mb * nw <= kPackScanMax) {
+        hipLaunchKernelGGL(pack_scan_kernel<I>, dim3(1), dim3(kPackScanThreads), 0, s, bcounts, g.Mb, counts,
+                           nw, brp, offsets, err, flags, g.Kb, cap, status);
+        XSPMM_LAUNCH_CHECK();
+        return;
+    }
+    device_exclusive_scan(ArrayValue<I>{bcounts}, g.Mb, brp, s);
+    device_exclusive_scan(ArrayValue<int32_t>{counts}, g.Mb * nw, offsets, s);
+    hipLaunchKernelGGL(pack_decide_kernel<I>, dim3(1), dim3(64), 0, s, offsets + g.Mb * nw, brp + g.Mb,
+                       err, flags, g.Mb, g.Kb, cap, status);
+    XSPMM_LAUNCH_CHECK();
+}
+
+PackStatus csr_pack_status(const int64_t* status, hipStream_t s)
+{
+    int64_t h[5] = {0, 0, 0, 0, 0};
+    XSPMM_HIP_CHECK(hipMemcpyAsync(h, status, sizeof(h), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    return PackStatus{h[0], h[1], (int)h[2], (unsigned)h[3], h[4] != 0};
+}
+
+template <typename I>
+void csr_pack_emit(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const uint16_t* vals,
+                   const int64_t* offsets, const int64_t* status, int64_t cap, void* a, uint32_t* rows,
+                   hipStream_t s)
+{
+    const ConvGeometry g = conv_geometry(M, K, nnz, 16, 16);
+    if (g.Mb == 0 || cap <= 0) return;
+    if (!csr_pack_covers(K)) throw std::invalid_argument("csr_pack_emit: K above the packed form's limit.");
+    const int nw = spmm_batch_waves();
+    const PackLds L = pack_lds(g.Kb, nw);
+    hipLaunchKernelGGL(pack_emit_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.emit_bytes, s, M, K,
+                       nnz, rp, ci, vals, g.nwords, g.Kb, nw, offsets, status, cap,
+                       static_cast<uint16_t*>(a), rows);
+    XSPMM_LAUNCH_CHECK();
+}
+
+#define XSPMM_INST_PACK(I)                                                                        \
+    template void csr_pack_analyse<I>(int64_t, int64_t, int64_t, const I*, const I*,              \
+                                      const uint16_t*, I*, I*, int32_t*, int64_t*, int*,          \
+                                      unsigned int*, int64_t, int64_t*, hipStream_t);             \
+    template void csr_pack_emit<I>(int64_t, int64_t, int64_t, const I*, const I*,                 \
+                                   const uint16_t*, const int64_t*, const int64_t*, int64_t,      \
+                                   void*, uint32_t*, hipStream_t);
+XSPMM_INST_PACK(int32_t)
+XSPMM_INST_PACK(int64_t)
+#undef XSPMM_INST_PACK
 
 }  // namespace detail
 }  // namespace xspmm

@@ -148,9 +148,9 @@ private:
 // Elapsed times of stages bracketed by HIP events on stream s.  start() and
 // stop() only record the events, so the host goes on to the next stage
 // while the GPU runs this one; finish() waits for the last stop and writes
-// each stage's milliseconds.  Host work inside a bracket still counts: the
-// stop event is recorded after it, and the stream idles meanwhile.  A
-// disabled timer does nothing.
+// each stage's milliseconds (brackets stopped into one slot add up).  Host
+// work inside a bracket still counts: the stop event is recorded after it,
+// and the stream idles meanwhile.  A disabled timer does nothing.
 class StageTimer {
 public:
     StageTimer(bool on, hipStream_t s) : on_(on), s_(s) {}
@@ -181,12 +181,14 @@ public:
         st.out = out;
     }
     void finish() {
+        for (auto& st : stages_)
+            if (st.out) *st.out = 0.0;
         for (auto& st : stages_) {
             if (!st.out) continue;
             XSPMM_HIP_CHECK(hipEventSynchronize(st.b));
             float ms = 0.f;
             XSPMM_HIP_CHECK(hipEventElapsedTime(&ms, st.a, st.b));
-            *st.out = (double)ms;
+            *st.out += (double)ms;
         }
     }
 
@@ -372,9 +374,47 @@ struct MtxData {
 };
 MtxData read_matrix_market(const std::string& path);
 
+// CSR -> packed column batches (convert.hip), the fp16 batches that
+// spmm_f16_packed multiplies, formed from the CSR strips without the padded
+// blocks.  csr_pack_analyse: per strip its block count (bcounts[Mb]) and
+// their exclusive scan (brp, Mb + 1 entries: the BCSR row_ptr), per
+// (block-row, wave) its batch count (counts[Mb * spmm_batch_waves()]) and
+// their exclusive scan (offsets, one more entry), err (set for an invalid
+// row_ptr or column), flags (2: a strip's row is not strictly increasing;
+// 4: an Inf or NaN value) and status[5] = {batches, blocks, err, flags, go}:
+// go is decided on the device (valid, sorted and finite input, not a fully
+// populated grid, 1 .. cap batches, 3 * batches <= blocks).  csr_pack_emit
+// writes the A' operands (1 KB per batch) and B-row indices (32 per batch)
+// when go is set and nothing otherwise, so it can be queued before the host
+// reads the status; a, rows hold cap batches.  csr_pack_status copies the
+// status to the host (one synchronization).  csr_pack_covers: the strip
+// kernels' LDS holds ceil(K / 16) column blocks.  csr_pack_batch_bound: an
+// upper bound on the batch count (the smaller of 2 nnz / 33 +
+// min(Mb * waves, nnz) and Mb * ceil(Kb / 2)).
+struct PackStatus {
+    int64_t nbatches, nnzb;
+    int err;
+    unsigned int flags;
+    bool go;
+};
+bool csr_pack_covers(int64_t K);
+int64_t csr_pack_batch_bound(int64_t M, int64_t K, int64_t nnz);
+template <typename I>
+void csr_pack_analyse(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
+                      const uint16_t* vals, I* bcounts, I* brp, int32_t* counts, int64_t* offsets,
+                      int* err, unsigned int* flags, int64_t cap, int64_t* status, hipStream_t s);
+PackStatus csr_pack_status(const int64_t* status, hipStream_t s);
+template <typename I>
+void csr_pack_emit(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const uint16_t* vals,
+                   const int64_t* offsets, const int64_t* status, int64_t cap, void* a, uint32_t* rows,
+                   hipStream_t s);
+
 // Device bytes of the temporaries the last spmm_pipeline call on this thread
 // took (0 before any call).
 size_t last_pipeline_temp_bytes();
+// Whether the last spmm_pipeline call on this thread multiplied packed column
+// batches (else BCSR blocks).
+bool last_pipeline_packed();
 
 // Tier-2 pipeline on raw device pointers.  `timings` may be null; it points
 // at six doubles laid out like SpMMTimings.

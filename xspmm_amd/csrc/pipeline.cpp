@@ -25,9 +25,23 @@
 // every block is full), so the conversion reads the count first and takes the
 // arrays at their exact size, as the reference does
 // (src/core/conversion.cpp:66-73).
+//
+// fp16 products that spmm_f16_packed covers take a third form: the
+// conversion writes the column batches the BCSR column-batch kernel would
+// form (csr_pack_analyse / csr_pack_emit in convert.hip) instead of padded
+// blocks, and the packed product multiplies them, its store writing product
+// row r to C row perm[r] (un-permutation fused; no C_temp).  C is the BCSR
+// form's bit for bit.  The batch arrays are sized from a bound
+// (csr_pack_batch_bound, at most 2 nnz / 33 + Mb * 4 batches of 1152 bytes)
+// so the conversion is queued without a host round trip; the device decides
+// whether the form is taken (sorted, finite input whose batches save a
+// quarter of the block bytes), and when it is not, the host releases the
+// batch arrays and converts to BCSR at the exact size (the count is then
+// known).  XSPMM_PIPELINE_FORMAT=bcsr keeps the BCSR form.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 #include <vector>
 
 #include "internal.hpp"
@@ -41,12 +55,19 @@ namespace {
 // exact sizing after one host round trip).
 constexpr size_t kFusedConversionBytes = size_t(1) << 30;
 
-// Device bytes of the last pipeline call's temporaries on this thread.
+// Bytes of one packed column batch: its A' operand (1 KB) and 32 B-row
+// indices.
+constexpr size_t kPackedBatchBytes = 1024 + 128;
+
+// Device bytes of the last pipeline call's temporaries on this thread, and
+// whether it multiplied packed column batches.
 thread_local size_t g_last_temp_bytes = 0;
+thread_local bool g_last_packed = false;
 
 }  // namespace
 
 size_t last_pipeline_temp_bytes() { return g_last_temp_bytes; }
+bool last_pipeline_packed() { return g_last_packed; }
 
 
 template <typename I>
@@ -83,6 +104,17 @@ template void jaccard_clustering_dispatch<int64_t>(int64_t, int64_t, int64_t, co
                                                    const int64_t*, float, int64_t, int64_t*,
                                                    hipStream_t);
 
+// The fp16 pipeline converts into packed column batches when the packed
+// kernel covers the product (the same rule as spmm_f16_packed's) and
+// XSPMM_PIPELINE_FORMAT is not "bcsr".
+bool packed_pipeline_covers(int64_t K, int64_t Mb, int64_t Kb, int64_t N)
+{
+    if (const char* e = std::getenv("XSPMM_PIPELINE_FORMAT"))
+        if (std::strcmp(e, "bcsr") == 0) return false;
+    return N > 0 && N % 8 == 0 && K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
+           (N + 127) / 128 <= 65535 && spmm_f16_pack_supported(K, Mb, Kb) && csr_pack_covers(K);
+}
+
 template <typename T, typename I>
 void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const T* vals,
                    const T* B, float* C, int64_t N, int64_t hw, bool optimize_pattern,
@@ -96,14 +128,28 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     StageTimer total(timed, s), step(timed, s);
     total.start();
     const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
+    const int nw = spmm_batch_waves();
 
+    // fp16 products the packed kernel covers convert straight into packed
+    // column batches (csr_pack_analyse / csr_pack_emit): no padded blocks are
+    // written or read.  Strips with unsorted or duplicate columns, non-finite
+    // values, fully populated grids and products whose batches would not save
+    // a quarter of the block bytes take the BCSR path; the device decides,
+    // and the host learns the outcome after the conversion's kernels are
+    // queued.
+    const bool try_packed = sizeof(T) == 2 && M > 0 && nnz > 0 && packed_pipeline_covers(K, Mb, Kb, N);
+    // The batch arrays are sized from csr_pack_batch_bound while that takes
+    // at most kFusedConversionBytes (then the whole conversion is queued with
+    // no host round trip), else exactly, after reading the count.
+    const int64_t pbound = try_packed ? std::max<int64_t>(1, csr_pack_batch_bound(M, K, nnz)) : 0;
+    const bool pfused = try_packed && (size_t)pbound * kPackedBatchBytes <= kFusedConversionBytes;
     // Every temporary is taken before the first stage, so the stage times
-    // hold the stages' own work, except exactly sized BCSR arrays, which the
-    // conversion stage takes once it has read the block count.  The bound
-    // min(nnz, Mb * Kb) on the block count holds since each block holds an
-    // entry.
+    // hold the stages' own work, except arrays sized from a count the
+    // conversion stage reads first (exactly sized BCSR arrays or batches).
+    // The bound min(nnz, Mb * Kb) on the block count holds since each block
+    // holds an entry.
     const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(nnz, Mb * Kb));
-    const bool fused = (size_t)cap * 256 * sizeof(T) <= kFusedConversionBytes;
+    const bool fused = !try_packed && (size_t)cap * 256 * sizeof(T) <= kFusedConversionBytes;
     // all in one allocation
     Carve cv;
     size_t o_perm = 0, o_nrp = 0, o_nci = 0, o_nvals = 0, o_ctmp = 0;
@@ -112,19 +158,46 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
         o_nrp = cv.take((size_t)(M + 1) * sizeof(I));
         o_nci = cv.take((size_t)(nnz > 0 ? nnz : 1) * sizeof(I));
         o_nvals = cv.take((size_t)(nnz > 0 ? nnz : 1) * sizeof(T));
-        o_ctmp = cv.take((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float));
+        if (!try_packed)
+            o_ctmp = cv.take((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * sizeof(float));
     }
     const size_t o_brp = cv.take((size_t)(Mb + 1) * sizeof(I));
     const size_t o_err = cv.take(sizeof(int));
     const size_t o_bci = fused ? cv.take((size_t)cap * sizeof(I)) : 0;
     const size_t o_bvals = fused ? cv.take((size_t)cap * 256 * sizeof(T)) : 0;
+    size_t o_bcounts = 0, o_counts = 0, o_offsets = 0, o_flags = 0, o_status = 0, o_order = 0;
+    if (try_packed) {
+        o_bcounts = cv.take((size_t)Mb * sizeof(I));
+        o_counts = cv.take((size_t)Mb * nw * sizeof(int32_t));
+        o_offsets = cv.take((size_t)(Mb * nw + 1) * sizeof(int64_t));
+        o_flags = cv.take(sizeof(unsigned int));
+        o_status = cv.take(5 * sizeof(int64_t));
+        o_order = cv.take((size_t)Mb * sizeof(int32_t));
+    }
+    // Temporaries reported: the most held at once (the bound-sized batches
+    // are released before a BCSR fallback takes its arrays).
+    size_t live = 0;
+    g_last_temp_bytes = 0;
+    g_last_packed = false;
+    auto took = [&](size_t bytes) {
+        live += bytes;
+        g_last_temp_bytes = std::max(g_last_temp_bytes, live);
+    };
     Scratch tmp(cv.end, s);
-    g_last_temp_bytes = cv.end;
+    took(cv.end);
+    // bound-sized batches: A' operands, then B-row indices
+    Scratch pbatch(pfused ? (size_t)pbound * kPackedBatchBytes : 0, s);
+    took(pfused ? (size_t)pbound * kPackedBatchBytes : 0);
     char* const base = tmp.as<char>();
     const Piece d_perm{base + o_perm}, nrp{base + o_nrp}, nci{base + o_nci}, nvals{base + o_nvals},
-        c_tmp{base + o_ctmp}, brp{base + o_brp}, err{base + o_err};
-    Piece bci{base + o_bci}, bvals{base + o_bvals};
-    Scratch blocks;  // exactly sized BCSR arrays (when not fused)
+        brp{base + o_brp}, err{base + o_err};
+    Piece c_tmp{base + o_ctmp}, bci{base + o_bci}, bvals{base + o_bvals};
+    const Piece bcounts{base + o_bcounts}, counts{base + o_counts}, offsets{base + o_offsets},
+        flags{base + o_flags}, status{base + o_status}, order{base + o_order};
+    void* pa = pbatch.get();
+    uint32_t* prows = pfused ? reinterpret_cast<uint32_t*>(pbatch.as<char>() + (size_t)pbound * 1024) : nullptr;
+    Scratch blocks;  // exactly sized BCSR arrays or batches
+    Scratch ctmp_late;
 
     // the stage's CSR: the caller's, or the permuted copy
     const I* crp = rp;
@@ -147,25 +220,92 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     }
 
     // 3. Conversion (the fill writes nothing if the count finds invalid input).
-    step.start();
-    csr_to_bcsr_count_async<I>(M, K, nnz, crp, cci, 16, 16, brp.as<I>(), err.as<int>(), s);
     int64_t nnzb = 0;
-    if (!fused) {
-        nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
-        Carve bc;
-        const size_t o_ci = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I));
-        const size_t o_v = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T));
-        blocks = Scratch(bc.end, s);
-        g_last_temp_bytes += bc.end;
-        bci = Piece{blocks.as<char>() + o_ci};
-        bvals = Piece{blocks.as<char>() + o_v};
+    bool packed = false;
+    step.start();
+    if (try_packed) {
+        const uint16_t* v16 = reinterpret_cast<const uint16_t*>(cvals);
+        csr_pack_analyse<I>(M, K, nnz, crp, cci, v16, bcounts.as<I>(), brp.as<I>(), counts.as<int32_t>(),
+                            offsets.as<int64_t>(), err.as<int>(), flags.as<unsigned int>(),
+                            pfused ? pbound : std::numeric_limits<int64_t>::max() / 2048,
+                            status.as<int64_t>(), s);
+        if (pfused)
+            csr_pack_emit<I>(M, K, nnz, crp, cci, v16, offsets.as<int64_t>(), status.as<int64_t>(), pbound,
+                             pa, prows, s);
+        if (spmm_order_wanted(Mb)) spmm_dispatch_order<I>(brp.as<I>(), Mb, order.as<int32_t>(), s);
+        if (timed) step.stop(&tm[2]);
+        const PackStatus st = csr_pack_status(status.as<int64_t>(), s);
+        if (st.err)
+            throw std::invalid_argument(
+                "csr_to_bcsr: invalid CSR (column index outside [0, K) or bad row_ptr).");
+        nnzb = st.nnzb;
+        packed = st.go;
+        if (packed && !pfused) {
+            // exactly sized batches (the bracket adds to the conversion time)
+            step.start();
+            blocks = Scratch((size_t)st.nbatches * kPackedBatchBytes, s);
+            took((size_t)st.nbatches * kPackedBatchBytes);
+            pa = blocks.get();
+            prows = reinterpret_cast<uint32_t*>(blocks.as<char>() + (size_t)st.nbatches * 1024);
+            csr_pack_emit<I>(M, K, nnz, crp, cci, v16, offsets.as<int64_t>(), status.as<int64_t>(),
+                             st.nbatches, pa, prows, s);
+            if (timed) step.stop(&tm[2]);
+        }
+        if (!packed) {
+            // the BCSR form, exactly sized from the count (the bracket adds
+            // to the conversion time)
+            step.start();
+            if (pfused) {
+                pbatch = Scratch();
+                live -= (size_t)pbound * kPackedBatchBytes;
+            }
+            Carve bc;
+            const size_t o_ci = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I));
+            const size_t o_v = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T));
+            blocks = Scratch(bc.end, s);
+            took(bc.end);
+            bci = Piece{blocks.as<char>() + o_ci};
+            bvals = Piece{blocks.as<char>() + o_v};
+            csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp.as<I>(), bci.as<I>(),
+                                   bvals.as<T>(), s, err.as<int>());
+            if (timed) step.stop(&tm[2]);
+        }
+    } else {
+        csr_to_bcsr_count_async<I>(M, K, nnz, crp, cci, 16, 16, brp.as<I>(), err.as<int>(), s);
+        if (!fused) {
+            nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
+            Carve bc;
+            const size_t o_ci = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I));
+            const size_t o_v = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T));
+            blocks = Scratch(bc.end, s);
+            took(bc.end);
+            bci = Piece{blocks.as<char>() + o_ci};
+            bvals = Piece{blocks.as<char>() + o_v};
+        }
+        csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp.as<I>(), bci.as<I>(),
+                               bvals.as<T>(), s, err.as<int>());
+        if (timed) step.stop(&tm[2]);
+        if (fused) nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
     }
-    csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp.as<I>(), bci.as<I>(),
-                           bvals.as<T>(), s, err.as<int>());
-    if (timed) step.stop(&tm[2]);
-    if (fused) nnzb = csr_to_bcsr_result<I>(brp.as<I>(), Mb, err.as<int>(), s);
 
-    if (optimize_pattern) {
+    g_last_packed = packed;
+    if (packed) {
+        // 4 + 5. The packed product; with clustering its store writes product
+        // row r to C row perm[r] (the un-permutation, fused: that stage's
+        // time is not set).
+        step.start();
+        const bool ok = spmm_f16_packed<I>(
+            M, K, Mb, offsets.as<int64_t>(), pa, prows, reinterpret_cast<const uint16_t*>(B), C, N,
+            spmm_order_wanted(Mb) ? order.as<int32_t>() : nullptr,
+            optimize_pattern ? d_perm.as<I>() : nullptr, s);
+        if (!ok) throw std::runtime_error("xSpMM: the packed product does not cover this shape.");
+        if (timed) step.stop(&tm[3]);
+    } else if (optimize_pattern) {
+        if (try_packed) {
+            ctmp_late = Scratch((size_t)M * (size_t)(N > 0 ? N : 1) * sizeof(float), s);
+            took((size_t)M * (size_t)(N > 0 ? N : 1) * sizeof(float));
+            c_tmp = Piece{ctmp_late.as<char>()};
+        }
         // 4. SpMM into the permuted-order temporary.
         step.start();
         bcsr_spmm<T, I>(M, K, Mb, Kb, nnzb, brp.as<I>(), bci.as<I>(), bvals.as<T>(), B,
