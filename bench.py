@@ -413,7 +413,8 @@ def main():
                      "nonzero_block_columns": ncols,
                      "hbm_frac": hbm_frac, "mfma_frac": mfma_frac})
 
-    stages = stages_gpu = None
+    stages = stages_gpu = stages_bcsr = None
+    pipe_form = None
     # Tier-2 stage times after untimed warm-up calls, as the reference's own
     # pipeline benchmark takes them (examples/02_spmm_benchmark.cpp:64, :122-124:
     # three warm-up calls, then one call with SpMMTimings)
@@ -423,16 +424,27 @@ def main():
             X.spmm_pipeline(A, B, optimize_pattern=p.cluster, timings=False)
         _, stages = X.spmm_pipeline(A, B, optimize_pattern=p.cluster)
         torch.cuda.synchronize()
+        pipe_form = "packed column batches" if X.pipeline_last_packed() else "bcsr"
         if p.cluster:
             # the same pipeline with the clustering stage on the GPU engine
             os.environ["XSPMM_CLUSTER_DEVICE"] = "gpu"
-            try:
+        try:
+            if p.cluster:
                 for _ in range(pipe_warmup):
                     X.spmm_pipeline(A, B, optimize_pattern=True, timings=False)
                 _, stages_gpu = X.spmm_pipeline(A, B, optimize_pattern=True)
                 torch.cuda.synchronize()
-            finally:
-                del os.environ["XSPMM_CLUSTER_DEVICE"]
+            if pipe_form != "bcsr":
+                # the BCSR form of the same pipeline (the reference's stage
+                # sequence: padded blocks, Tier-1 SpMM, un-permutation)
+                os.environ["XSPMM_PIPELINE_FORMAT"] = "bcsr"
+                for _ in range(pipe_warmup):
+                    X.spmm_pipeline(A, B, optimize_pattern=p.cluster, timings=False)
+                _, stages_bcsr = X.spmm_pipeline(A, B, optimize_pattern=p.cluster)
+                torch.cuda.synchronize()
+        finally:
+            os.environ.pop("XSPMM_CLUSTER_DEVICE", None)
+            os.environ.pop("XSPMM_PIPELINE_FORMAT", None)
 
     # prepared product (plan): per-call time of execute(), which is the
     # Tier-1 SpMM with the un-permutation fused and the dispatch order
@@ -516,7 +528,11 @@ def main():
         "spot_check_rel_frob": spot,
         "prep": prep,
         "pipeline_stages_ms": stages,
+        "pipeline_form": pipe_form,
         "pipeline_stages_ms_gpu_clustering": stages_gpu,
+        # the same pipeline in the BCSR form (clustering on the GPU engine
+        # when the workload clusters), when the default form is the packed one
+        "pipeline_stages_ms_bcsr_form": stages_bcsr,
         "pipeline_warmup_calls": pipe_warmup if not args.no_pipeline else 0,
         "plan": plan_info,
         "vendor": vendor,

@@ -35,9 +35,9 @@
 // (csr_pack_batch_bound, at most 2 nnz / 33 + Mb * 4 batches of 1152 bytes)
 // so the conversion is queued without a host round trip; the device decides
 // whether the form is taken (sorted, finite input whose batches save a
-// quarter of the block bytes), and when it is not, the host releases the
-// batch arrays and converts to BCSR at the exact size (the count is then
-// known).  XSPMM_PIPELINE_FORMAT=bcsr keeps the BCSR form.
+// quarter of the block bytes), and when it is not, the host converts to BCSR
+// at the exact size (the count is then known), inside the unused batch
+// arrays when they hold it, else in a new allocation after releasing them.  XSPMM_PIPELINE_FORMAT=bcsr keeps the BCSR form.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -255,17 +255,23 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
             // the BCSR form, exactly sized from the count (the bracket adds
             // to the conversion time)
             step.start();
-            if (pfused) {
-                pbatch = Scratch();
-                live -= (size_t)pbound * kPackedBatchBytes;
-            }
             Carve bc;
             const size_t o_ci = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I));
             const size_t o_v = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T));
-            blocks = Scratch(bc.end, s);
-            took(bc.end);
-            bci = Piece{blocks.as<char>() + o_ci};
-            bvals = Piece{blocks.as<char>() + o_v};
+            char* bb = nullptr;
+            if (pfused && bc.end <= (size_t)pbound * kPackedBatchBytes) {
+                bb = pbatch.as<char>();  // the unused batch arrays hold them
+            } else {
+                if (pfused) {
+                    pbatch = Scratch();
+                    live -= (size_t)pbound * kPackedBatchBytes;
+                }
+                blocks = Scratch(bc.end, s);
+                took(bc.end);
+                bb = blocks.as<char>();
+            }
+            bci = Piece{bb + o_ci};
+            bvals = Piece{bb + o_v};
             csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp.as<I>(), bci.as<I>(),
                                    bvals.as<T>(), s, err.as<int>());
             if (timed) step.stop(&tm[2]);
