@@ -299,8 +299,10 @@ def test_examples02_triangular_tier2_fp32(torch):
 
 def test_templates_fp32_tier1_and_tier2(torch):
     """The headline matrix in fp32 (the reference's type): Tier-1 on the
-    clustered BCSR and the Tier-2 pipeline, sampled rows against fp64; the
-    two must agree exactly (the pipeline multiplies the same BCSR)."""
+    clustered BCSR and the Tier-2 pipeline, sampled rows against fp64.  The
+    pipeline's BCSR form (XSPMM_PIPELINE_FORMAT=bcsr) multiplies the same
+    BCSR and must agree exactly; its default packed fp32 form sums the same
+    products in another order (relative difference <= 1e-6)."""
     p = synth.templates(dtype=np.float32)
     A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
     B = torch.as_tensor(p.B).cuda()
@@ -308,8 +310,18 @@ def test_templates_fp32_tier1_and_tier2(torch):
     Ap = X.apply_permutation(A, torch.as_tensor(perm).cuda())
     Bm = X.csr_to_bcsr(Ap)
     C1 = X.spmm(Bm, B)
-    C2, _ = X.spmm_pipeline(A, B, optimize_pattern=True, timings=False)
+    Cp, _ = X.spmm_pipeline(A, B, optimize_pattern=True, timings=False)
     torch.cuda.synchronize()
+    assert X.pipeline_last_packed()
+    os.environ["XSPMM_PIPELINE_FORMAT"] = "bcsr"
+    try:
+        C2, _ = X.spmm_pipeline(A, B, optimize_pattern=True, timings=False)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["XSPMM_PIPELINE_FORMAT"]
+    d = float((Cp.double() - C2.double()).norm() / C2.double().norm())
+    note(f"templates fp32: packed pipeline against the BCSR form, relative {d:.2e}")
+    assert d <= 1e-6
     note(f"templates fp32: nnzb {Bm.num_blocks}")
     rows = np.random.default_rng(2).choice(p.M, size=512, replace=False)
     # C1 is in the permuted row order: its row r is row perm[r] of A * B

@@ -6,10 +6,13 @@ and fill then run with no host round trip), and exactly, after reading the
 count, above it -- as the reference's conversion does
 (src/core/conversion.cpp:66-73).  A matrix of full 16x16 blocks has
 nnz = 256 * nnzb, so there the bound is 256x the exact size.
-xspmm_pipeline_temp_bytes reports what the last call took.  fp16 products
-the packed kernel covers take packed column batches instead of BCSR arrays.
+xspmm_pipeline_temp_bytes reports the most the last call held at once.
+Products the packed kernels cover take packed column batches instead of BCSR
+arrays, sized from a bound on the batch count while that fits 128 MiB.
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -70,15 +73,23 @@ def test_full_blocks_take_exact_bcsr(torch):
 
 def test_small_matrix_keeps_fused_bound(torch):
     """A small matrix keeps the bound-sized arrays (no host round trip): the
-    reported bytes cover min(nnz, Mb * Kb) blocks; C against fp64.  (fp32:
-    the fp16 pipeline converts to packed column batches instead.)"""
+    reported bytes cover min(nnz, Mb * Kb) blocks; C against fp64.  (The BCSR
+    form is forced: this product would take the packed form.)"""
     p = synth.random_csr(500, 700, 64, 0.02, seed=4, dtype=np.float32)
     Mb, Kb = (p.M + 15) // 16, (p.K + 15) // 16
     cap = min(p.nnz, Mb * Kb)
     A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
     B = torch.as_tensor(p.B).cuda()
-    C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
-    torch.cuda.synchronize()
+    old = os.environ.get("XSPMM_PIPELINE_FORMAT")
+    os.environ["XSPMM_PIPELINE_FORMAT"] = "bcsr"
+    try:
+        C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            del os.environ["XSPMM_PIPELINE_FORMAT"]
+        else:
+            os.environ["XSPMM_PIPELINE_FORMAT"] = old
     used = X.pipeline_temp_bytes()
     assert not X.pipeline_last_packed()
     assert used >= cap * 256 * 4 + cap * 4
@@ -108,3 +119,25 @@ def test_packed_form_takes_no_block_arrays(torch):
     assert used <= bound * 1152 + Mb * 64 + 16 * 256
     ref = oracle.bcsr_spmm_f64(p.M, p.K, p.N, brp, bci, bv, p.B)
     assert oracle.errors(C.cpu().numpy(), ref)["rel_frob"] <= 2e-3
+
+
+def test_fp32_packed_form_takes_no_block_arrays(torch):
+    """The fp32 pipeline's packed form: 272 bytes per batch of four columns
+    (A' operand and B-row indices), sized from the bound nnz / 4 + 4 Mb;
+    no padded blocks (which would take 1024 bytes per block)."""
+    p = synth.random_csr(2000, 6000, 64, 0.004, seed=6, dtype=np.float32)
+    Mb = (p.M + 15) // 16
+    brp, bci, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    nnzb = len(bci)
+    A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
+    B = torch.as_tensor(p.B).cuda()
+    C, _ = X.spmm_pipeline(A, B, optimize_pattern=False, timings=False)
+    torch.cuda.synchronize()
+    assert X.pipeline_last_packed()
+    used = X.pipeline_temp_bytes()
+    bound = p.nnz // 4 + 4 * Mb
+    print(f"fp32 packed form temporaries {used} B; BCSR blocks would take {nnzb * 1024} B", flush=True)
+    assert used < nnzb * 1024 // 2
+    assert used <= bound * 272 + Mb * 32 + 16 * 256
+    ref = oracle.bcsr_spmm_f64(p.M, p.K, p.N, brp, bci, bv, p.B)
+    assert oracle.errors(C.cpu().numpy(), ref)["rel_frob"] <= 1e-5

@@ -347,7 +347,7 @@ __device__ __forceinline__ uint32_t slot_kpos(uint32_t s)
 // words; pack_emit_kernel adds each pair's batch info, the waves' first
 // batch and each block's column block.
 struct PackLds {
-    uint32_t bitmap, prefix, pw, analyse_bytes, pinfo, ob, bcl, emit_bytes;
+    uint32_t bitmap, prefix, pw, analyse_bytes, pinfo, ob, bcl, emit_bytes, sb, emit32_bytes;
 };
 
 __host__ __device__ inline PackLds pack_lds(int64_t Kb, int nw)
@@ -363,16 +363,31 @@ __host__ __device__ inline PackLds pack_lds(int64_t Kb, int nw)
     L.ob = (L.pinfo + 4 * npc + 7) & ~7u;
     L.bcl = L.ob + 8 * (uint32_t)(nw + 1);
     L.emit_bytes = (L.bcl + 2 * (uint32_t)(Kb > 0 ? Kb : 1) + 15) & ~15u;
+    // fp32 emit: each block's first slot (one more entry for an odd count)
+    L.sb = L.analyse_bytes;
+    L.emit32_bytes = (L.sb + 4 * (uint32_t)((Kb > 0 ? Kb : 1) + 2) + 15) & ~15u;
     return L;
 }
 
-// One strip's analysis, shared by both kernels: bitmap, prefix, *nb (the
-// strip's block count) and the pair words.  Leaves *s_bad / *s_unsorted set
-// for an invalid or unsorted strip (the pair words are then not formed) and
-// *s_nonfinite for an Inf or NaN value.  Ends with a barrier.
-template <typename I>
+// Value bits of the packed forms: V = uint16_t (fp16) or uint32_t (fp32).
+// A column of a block is set when one of its entries is: for fp16 when its
+// bits are not 0 (the fp16 batch kernel's rule: -0.0 counts), for fp32 when
+// it is not +-0 (a +-0 entry adds an exact zero to an fp32 sum that starts
+// at +0).  Non-finite values are flagged for fp16 only (the fp16 form must
+// equal the BCSR kernel's compaction bit for bit).
+__device__ __forceinline__ bool pack_set(uint16_t v) { return v != 0u; }
+__device__ __forceinline__ bool pack_set(uint32_t v) { return (v & 0x7fffffffu) != 0u; }
+__device__ __forceinline__ bool pack_nonfinite(uint16_t v) { return (v & 0x7c00u) == 0x7c00u; }
+__device__ __forceinline__ bool pack_nonfinite(uint32_t) { return false; }
+
+// One strip's analysis, shared by the strip kernels: bitmap, prefix, *nb (the
+// strip's block count) and the pair words (column masks of blocks 2j, 2j+1).
+// Leaves *s_bad / *s_unsorted set for an invalid or unsorted strip (the pair
+// words are then not formed) and *s_nonfinite for a flagged value.  Ends with
+// a barrier.
+template <typename I, typename V>
 __device__ void pack_strip(int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp,
-                           const I* __restrict__ ci, const uint16_t* __restrict__ vals,
+                           const I* __restrict__ ci, const V* __restrict__ vals,
                            int64_t nwords, unsigned char* smem, const PackLds& L, StripView& sv,
                            int* s_unsorted, int* s_bad, int* s_nonfinite, int64_t* red, int64_t* nb)
 {
@@ -404,17 +419,18 @@ __device__ void pack_strip(int64_t M, int64_t K, int64_t nnz, const I* __restric
     const int64_t e1 = sv.bounds[sv.nr];
     bool nonfinite = false;
     for (int64_t i0 = e0 + threadIdx.x; i0 < e1; i0 += (int64_t)kThreads * kEntryUnroll) {
-        uint32_t v[kEntryUnroll], c[kEntryUnroll];
+        V v[kEntryUnroll];
+        uint32_t c[kEntryUnroll];
 #pragma unroll
         for (int u = 0; u < kEntryUnroll; ++u) {
             const int64_t idx = i0 + (int64_t)u * kThreads;
-            v[u] = idx < e1 ? (uint32_t)vals[idx] : 0u;
+            v[u] = idx < e1 ? vals[idx] : (V)0;
             c[u] = idx < e1 ? (uint32_t)ci[idx] : 0u;
         }
 #pragma unroll
         for (int u = 0; u < kEntryUnroll; ++u) {
-            if ((v[u] & 0x7c00u) == 0x7c00u) nonfinite = true;
-            if (v[u] == 0u) continue;  // also the entries past the strip
+            if (pack_nonfinite(v[u])) nonfinite = true;
+            if (!pack_set(v[u])) continue;  // also the entries past the strip
             const uint32_t bc = c[u] >> 4;
             const uint32_t w = bc >> 5;
             const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (bc & 31u)) - 1u));
@@ -489,14 +505,18 @@ __global__ __launch_bounds__(kThreads) void pack_analyse_kernel(
 }
 
 // status[0..4] = {batches, blocks, err, flags, go}: go (the packed form is
-// taken) when the input is valid, sorted and finite, the grid is not fully
-// populated, there is a batch, the batches fit the cap of the arrays they
-// are written to and take at most three quarters of the BCSR blocks' bytes
-// (1152 B per batch against 512 B per block: 3 * batches <= blocks).
+// taken) when the input is valid, sorted (and for fp16 finite), the grid is
+// not fully populated, there is a batch, the batches fit the cap of the
+// arrays they are written to and take at most three quarters of the BCSR
+// blocks' bytes: num * batches <= den * blocks (fp16: 1152 B per batch
+// against 512 B per block, num / den = 3 / 1; fp32: 272 B against 1024 B,
+// 17 / 48).
 __device__ __forceinline__ void pack_decide(int64_t nbat, int64_t nnzb, int e, unsigned int f, int64_t Mb,
-                                            int64_t Kb, int64_t cap, int64_t* __restrict__ status)
+                                            int64_t Kb, int64_t cap, int64_t num, int64_t den,
+                                            int64_t* __restrict__ status)
 {
-    const bool go = e == 0 && f == 0u && nbat > 0 && nbat <= cap && nnzb != Mb * Kb && 3 * nbat <= nnzb;
+    const bool go = e == 0 && f == 0u && nbat > 0 && nbat <= cap && nnzb != Mb * Kb &&
+                    num * nbat <= den * nnzb;
     status[0] = nbat;
     status[1] = nnzb;
     status[2] = (int64_t)e;
@@ -507,10 +527,11 @@ __device__ __forceinline__ void pack_decide(int64_t nbat, int64_t nnzb, int e, u
 template <typename I>
 __global__ void pack_decide_kernel(const int64_t* __restrict__ off_end, const I* __restrict__ brp_end,
                                    const int* __restrict__ err, const unsigned int* __restrict__ flags,
-                                   int64_t Mb, int64_t Kb, int64_t cap, int64_t* __restrict__ status)
+                                   int64_t Mb, int64_t Kb, int64_t cap, int64_t num, int64_t den,
+                                   int64_t* __restrict__ status)
 {
     if (threadIdx.x == 0 && blockIdx.x == 0)
-        pack_decide(*off_end, (int64_t)*brp_end, *err, *flags, Mb, Kb, cap, status);
+        pack_decide(*off_end, (int64_t)*brp_end, *err, *flags, Mb, Kb, cap, num, den, status);
 }
 
 // One workgroup scans both count arrays and decides (one launch instead of
@@ -570,12 +591,13 @@ template <typename I>
 __global__ __launch_bounds__(kPackScanThreads) void pack_scan_kernel(
     const I* __restrict__ bcounts, int64_t Mb, const int32_t* __restrict__ counts, int nw,
     I* __restrict__ brp, int64_t* __restrict__ offsets, const int* __restrict__ err,
-    const unsigned int* __restrict__ flags, int64_t Kb, int64_t cap, int64_t* __restrict__ status)
+    const unsigned int* __restrict__ flags, int64_t Kb, int64_t cap, int64_t num, int64_t den,
+    int64_t* __restrict__ status)
 {
     __shared__ int64_t red[kPackScanThreads / 64];
     const int64_t nnzb = wg_scan_array(bcounts, Mb, brp, red);
     const int64_t nbat = wg_scan_array(counts, Mb * nw, offsets, red);
-    if (threadIdx.x == 0) pack_decide(nbat, nnzb, *err, *flags, Mb, Kb, cap, status);
+    if (threadIdx.x == 0) pack_decide(nbat, nnzb, *err, *flags, Mb, Kb, cap, num, den, status);
 }
 
 // Writes strip br's batches [offsets[br * nw], offsets[br * nw + nw]) when
@@ -687,6 +709,146 @@ __global__ __launch_bounds__(kThreads) void pack_emit_kernel(
         }
     }
 }
+// ---------------------------------------------------------------------------
+// CSR -> packed fp32 column batches (the Tier-2 pipeline's fp32 form,
+// multiplied by spmm_f32_packed_kernel).  A strip's slots are its set
+// columns (a column of a block is set when one of its entries is not +-0)
+// in block order (ascending block column), then column order; slot s is
+// K position s % 4 of batch s / 4.  A batch's A' operand is 16 rows x 4
+// slots of fp32 values (zeros where a row has no entry), and its B-row
+// indices are the slots' columns (0xffffffff for a slot past the last).  A
+// strip's batch count is rounded up to a multiple of 4; four consecutive
+// batches form a group, stored so that one 16-byte load per lane reads the
+// group: A' value of batch 4G + c, row i, slot k at float (64 G + 16 k + i)
+// * 4 + c, B row of its slot k at word (4 G + k) * 4 + c.  Per strip:
+//   pack32_analyse_kernel  the strip's block count and batch count (and the
+//                          flags of pack_analyse_kernel);
+//   pack_scan_kernel       as for fp16, one batch count per strip;
+//   pack32_emit_kernel     clears the strip's groups, then stores every set
+//                          entry's value and its column as the slot's B row.
+// Batch count bound: a strip's S slots make at most S / 4 + 4 batches
+// after rounding, so at most nnz / 4 + 4 Mb in all, and at most
+// 4 Kb + 4 per strip.
+
+template <typename I>
+__global__ __launch_bounds__(kThreads) void pack32_analyse_kernel(
+    int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp, const I* __restrict__ ci,
+    const uint32_t* __restrict__ vals, int64_t nwords, int64_t Kb, I* __restrict__ bcounts,
+    int32_t* __restrict__ counts, int* __restrict__ err, unsigned int* __restrict__ flags)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int s_unsorted, s_bad, s_nonfinite;
+    __shared__ int64_t red[kThreads / 64];
+    const PackLds L = pack_lds(Kb, 1);
+    StripView sv;
+    int64_t nb;
+    pack_strip(M, K, nnz, rp, ci, vals, nwords, smem, L, sv, &s_unsorted, &s_bad, &s_nonfinite, red, &nb);
+    const int64_t br = blockIdx.x;
+    if (s_bad || s_unsorted) {  // uniform
+        if (threadIdx.x == 0) {
+            bcounts[br] = (I)nb;
+            counts[br] = 0;
+            if (s_bad) atomicOr(err, 1);
+            else atomicOr(flags, kPackFlagUnsorted);
+        }
+        return;
+    }
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(smem + L.pw);
+    const int64_t npairs = (nb + 1) >> 1;
+    int64_t mine = 0;
+    for (int64_t j = threadIdx.x; j < npairs; j += kThreads) mine += __popc(pw[j]);
+    const int64_t slots = block_sum(mine, red);
+    if (threadIdx.x == 0) {
+        bcounts[br] = (I)nb;
+        counts[br] = (int32_t)((((slots + 3) / 4) + 3) / 4 * 4);
+    }
+}
+
+// Writes strip br's batches [offsets[br], offsets[br + 1]) when status[4]
+// (go) is set; batches at or above cap are never written.
+template <typename I>
+__global__ __launch_bounds__(kThreads) void pack32_emit_kernel(
+    int64_t M, int64_t K, int64_t nnz, const I* __restrict__ rp, const I* __restrict__ ci,
+    const uint32_t* __restrict__ vals, int64_t nwords, int64_t Kb, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ status, int64_t cap, uint32_t* __restrict__ a, uint32_t* __restrict__ rows)
+{
+    if (status[4] == 0) return;  // uniform: before any barrier
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int s_unsorted, s_bad, s_nonfinite;
+    __shared__ int64_t red[kThreads / 64];
+    const PackLds L = pack_lds(Kb, 1);
+    StripView sv;
+    int64_t nb;
+    pack_strip(M, K, nnz, rp, ci, vals, nwords, smem, L, sv, &s_unsorted, &s_bad, &s_nonfinite, red, &nb);
+    if (s_bad || s_unsorted) return;  // uniform; excluded by go
+    const uint32_t* bitmap = reinterpret_cast<const uint32_t*>(smem + L.bitmap);
+    const uint32_t* prefix = reinterpret_cast<const uint32_t*>(smem + L.prefix);
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(smem + L.pw);
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+    const int64_t br = blockIdx.x;
+    const int64_t npairs = (nb + 1) >> 1;
+
+    // each block's first slot: exclusive scan of the column counts by rank
+    {
+        const int64_t per = (npairs + kThreads - 1) / kThreads;
+        const int64_t j0 = (int64_t)threadIdx.x * per;
+        const int64_t j1 = (j0 + per < npairs) ? j0 + per : npairs;
+        int64_t mine = 0;
+        for (int64_t j = j0; j < j1; ++j) mine += __popc(pw[j]);
+        int64_t total;
+        int64_t run = block_exclusive_scan(mine, &total, red);
+        for (int64_t j = j0; j < j1; ++j) {
+            const uint32_t w = pw[j];
+            sb[2 * j] = (uint32_t)run;
+            run += __popc(w & 0xffffu);
+            sb[2 * j + 1] = (uint32_t)run;
+            run += __popc(w >> 16);
+        }
+    }
+    // clear the strip's groups (A' zero, indices unused)
+    const int64_t q0 = offsets[br];
+    int64_t q1 = offsets[br + 1];
+    if (q1 > cap) q1 = cap;
+    {
+        uint4* a4 = reinterpret_cast<uint4*>(a);
+        uint4* r4 = reinterpret_cast<uint4*>(rows);
+        for (int64_t i = q0 * 16 + threadIdx.x; i < q1 * 16; i += kThreads) a4[i] = make_uint4(0, 0, 0, 0);
+        const uint32_t u = 0xffffffffu;
+        for (int64_t i = q0 + threadIdx.x; i < q1; i += kThreads) r4[i] = make_uint4(u, u, u, u);
+    }
+    __syncthreads();  // clears complete; slot bases visible
+
+    const int64_t e0 = sv.bounds[0];
+    const int64_t e1 = sv.bounds[sv.nr];
+    for (int64_t i0 = e0 + threadIdx.x; i0 < e1; i0 += (int64_t)kThreads * kEntryUnroll) {
+        uint32_t v[kEntryUnroll], c[kEntryUnroll];
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            v[u] = idx < e1 ? vals[idx] : 0u;
+            c[u] = idx < e1 ? (uint32_t)ci[idx] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kEntryUnroll; ++u) {
+            if (!pack_set(v[u])) continue;  // also the entries past the strip
+            const int64_t idx = i0 + (int64_t)u * kThreads;
+            const uint32_t bc = c[u] >> 4;
+            const uint32_t w = bc >> 5;
+            const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (bc & 31u)) - 1u));
+            const uint32_t m = (pw[rank >> 1] >> (16u * (rank & 1u))) & 0xffffu;
+            const uint32_t slot = sb[rank] + (uint32_t)__popc(m & ((1u << (c[u] & 15u)) - 1u));
+            const int64_t t = q0 + (int64_t)(slot >> 2);  // the batch (q0 is a multiple of 4)
+            if (t >= cap) continue;
+            const uint32_t k = slot & 3u;
+            const int64_t G = t >> 2;
+            const uint32_t cc = (uint32_t)(t & 3);
+            const int64_t r = row_of(sv, idx);
+            a[((G * 64) + 16 * k + r) * 4 + cc] = v[u];
+            rows[(G * 4 + k) * 4 + cc] = c[u];
+        }
+    }
+}
+
 }  // namespace
 
 template <typename I>
@@ -763,44 +925,53 @@ XSPMM_INST_FILL(float, int64_t)
 bool csr_pack_covers(int64_t K)
 {
     const int64_t Kb = (K + 15) / 16;
-    return Kb > 0 && pack_lds(Kb, spmm_batch_waves()).emit_bytes <= kMaxLds;
+    if (Kb <= 0) return false;
+    const PackLds L16 = pack_lds(Kb, spmm_batch_waves()), L32 = pack_lds(Kb, 1);
+    return L16.emit_bytes <= kMaxLds && L32.emit32_bytes <= kMaxLds;
 }
 
-int64_t csr_pack_batch_bound(int64_t M, int64_t K, int64_t nnz)
+int64_t csr_pack_batch_bound(int64_t M, int64_t K, int64_t nnz, int value_bytes)
 {
     const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
+    if (value_bytes == 4) return std::min<int64_t>(nnz / 4 + 4 * Mb, Mb * (4 * Kb + 4));
     const int64_t by_slots = 2 * nnz / 33 + std::min<int64_t>(Mb * spmm_batch_waves(), nnz);
     return std::min<int64_t>(by_slots, Mb * ((Kb + 1) / 2));  // a batch holds a pair
 }
 
-template <typename I>
-void csr_pack_analyse(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
-                      const uint16_t* vals, I* bcounts, I* brp, int32_t* counts, int64_t* offsets,
-                      int* err, unsigned int* flags, int64_t cap, int64_t* status, hipStream_t s)
+template <typename I, typename V>
+void csr_pack_analyse(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const V* vals,
+                      I* bcounts, I* brp, int32_t* counts, int64_t* offsets, int* err,
+                      unsigned int* flags, int64_t cap, int64_t* status, hipStream_t s)
 {
+    constexpr bool f32 = sizeof(V) == 4;
     const ConvGeometry g = conv_geometry(M, K, nnz, 16, 16);
     if (!csr_pack_covers(K)) throw std::invalid_argument("csr_pack_analyse: K above the packed form's limit.");
-    const int nw = spmm_batch_waves();
+    const int nw = f32 ? 1 : spmm_batch_waves();  // batch counts per strip
     const PackLds L = pack_lds(g.Kb, nw);
+    const int64_t num = f32 ? 17 : 3, den = f32 ? 48 : 1;
     hipLaunchKernelGGL(set_value_kernel<int>, dim3(1), dim3(64), 0, s, err, 0);
     XSPMM_LAUNCH_CHECK();
     hipLaunchKernelGGL(set_value_kernel<unsigned int>, dim3(1), dim3(64), 0, s, flags, 0u);
     XSPMM_LAUNCH_CHECK();
     if (g.Mb > 0) {
-        hipLaunchKernelGGL(pack_analyse_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.analyse_bytes, s,
-                           M, K, nnz, rp, ci, vals, g.nwords, g.Kb, nw, bcounts, counts, err, flags);
+        if constexpr (f32)
+            hipLaunchKernelGGL(pack32_analyse_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.analyse_bytes,
+                               s, M, K, nnz, rp, ci, vals, g.nwords, g.Kb, bcounts, counts, err, flags);
+        else
+            hipLaunchKernelGGL(pack_analyse_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.analyse_bytes,
+                               s, M, K, nnz, rp, ci, vals, g.nwords, g.Kb, nw, bcounts, counts, err, flags);
         XSPMM_LAUNCH_CHECK();
     }
     if (g.Mb * nw <= kPackScanMax) {
         hipLaunchKernelGGL(pack_scan_kernel<I>, dim3(1), dim3(kPackScanThreads), 0, s, bcounts, g.Mb, counts,
-                           nw, brp, offsets, err, flags, g.Kb, cap, status);
+                           nw, brp, offsets, err, flags, g.Kb, cap, num, den, status);
         XSPMM_LAUNCH_CHECK();
         return;
     }
     device_exclusive_scan(ArrayValue<I>{bcounts}, g.Mb, brp, s);
     device_exclusive_scan(ArrayValue<int32_t>{counts}, g.Mb * nw, offsets, s);
     hipLaunchKernelGGL(pack_decide_kernel<I>, dim3(1), dim3(64), 0, s, offsets + g.Mb * nw, brp + g.Mb,
-                       err, flags, g.Mb, g.Kb, cap, status);
+                       err, flags, g.Mb, g.Kb, cap, num, den, status);
     XSPMM_LAUNCH_CHECK();
 }
 
@@ -812,31 +983,41 @@ PackStatus csr_pack_status(const int64_t* status, hipStream_t s)
     return PackStatus{h[0], h[1], (int)h[2], (unsigned)h[3], h[4] != 0};
 }
 
-template <typename I>
-void csr_pack_emit(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const uint16_t* vals,
+template <typename I, typename V>
+void csr_pack_emit(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const V* vals,
                    const int64_t* offsets, const int64_t* status, int64_t cap, void* a, uint32_t* rows,
                    hipStream_t s)
 {
+    constexpr bool f32 = sizeof(V) == 4;
     const ConvGeometry g = conv_geometry(M, K, nnz, 16, 16);
     if (g.Mb == 0 || cap <= 0) return;
     if (!csr_pack_covers(K)) throw std::invalid_argument("csr_pack_emit: K above the packed form's limit.");
-    const int nw = spmm_batch_waves();
-    const PackLds L = pack_lds(g.Kb, nw);
-    hipLaunchKernelGGL(pack_emit_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.emit_bytes, s, M, K,
-                       nnz, rp, ci, vals, g.nwords, g.Kb, nw, offsets, status, cap,
-                       static_cast<uint16_t*>(a), rows);
+    if constexpr (f32) {
+        const PackLds L = pack_lds(g.Kb, 1);
+        hipLaunchKernelGGL(pack32_emit_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.emit32_bytes, s, M,
+                           K, nnz, rp, ci, vals, g.nwords, g.Kb, offsets, status, cap,
+                           static_cast<uint32_t*>(a), rows);
+    } else {
+        const int nw = spmm_batch_waves();
+        const PackLds L = pack_lds(g.Kb, nw);
+        hipLaunchKernelGGL(pack_emit_kernel<I>, dim3((unsigned)g.Mb), dim3(kThreads), L.emit_bytes, s, M, K,
+                           nnz, rp, ci, vals, g.nwords, g.Kb, nw, offsets, status, cap,
+                           static_cast<uint16_t*>(a), rows);
+    }
     XSPMM_LAUNCH_CHECK();
 }
 
-#define XSPMM_INST_PACK(I)                                                                        \
-    template void csr_pack_analyse<I>(int64_t, int64_t, int64_t, const I*, const I*,              \
-                                      const uint16_t*, I*, I*, int32_t*, int64_t*, int*,          \
-                                      unsigned int*, int64_t, int64_t*, hipStream_t);             \
-    template void csr_pack_emit<I>(int64_t, int64_t, int64_t, const I*, const I*,                 \
-                                   const uint16_t*, const int64_t*, const int64_t*, int64_t,      \
-                                   void*, uint32_t*, hipStream_t);
-XSPMM_INST_PACK(int32_t)
-XSPMM_INST_PACK(int64_t)
+#define XSPMM_INST_PACK(I, V)                                                                     \
+    template void csr_pack_analyse<I, V>(int64_t, int64_t, int64_t, const I*, const I*, const V*, \
+                                         I*, I*, int32_t*, int64_t*, int*, unsigned int*,         \
+                                         int64_t, int64_t*, hipStream_t);                         \
+    template void csr_pack_emit<I, V>(int64_t, int64_t, int64_t, const I*, const I*, const V*,    \
+                                      const int64_t*, const int64_t*, int64_t, void*, uint32_t*, \
+                                      hipStream_t);
+XSPMM_INST_PACK(int32_t, uint16_t)
+XSPMM_INST_PACK(int64_t, uint16_t)
+XSPMM_INST_PACK(int32_t, uint32_t)
+XSPMM_INST_PACK(int64_t, uint32_t)
 #undef XSPMM_INST_PACK
 
 }  // namespace detail

@@ -272,6 +272,15 @@ template <typename I>
 void bcsr_spmm_f32_batch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
                          const float* bvals, const float* B, float* C, int64_t N,
                          const int32_t* order, const I* row_map, hipStream_t s);
+// Packed fp32 column batches (csr_pack_emit with V = uint32_t): strip br's
+// batches [offsets[br], offsets[br + 1]) (a multiple of 4), A' in a and row
+// indices in rows; order and row_map as for bcsr_spmm_ex.  Returns false
+// when the shape is not covered (N % 4 != 0, B, C or a not 16-byte aligned,
+// K * N * 4 > 2^31).
+template <typename I>
+bool spmm_f32_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, const void* a,
+                     const uint32_t* rows, const float* B, float* C, int64_t N, const int32_t* order,
+                     const I* row_map, hipStream_t s);
 
 // Tier-1 fp16 SpMM for a fully populated block grid (nnzb == Mb * Kb);
 // row_map (null: rows in place) as for bcsr_spmm_ex.  Each tile checks that
@@ -374,23 +383,27 @@ struct MtxData {
 };
 MtxData read_matrix_market(const std::string& path);
 
-// CSR -> packed column batches (convert.hip), the fp16 batches that
-// spmm_f16_packed multiplies, formed from the CSR strips without the padded
-// blocks.  csr_pack_analyse: per strip its block count (bcounts[Mb]) and
-// their exclusive scan (brp, Mb + 1 entries: the BCSR row_ptr), per
-// (block-row, wave) its batch count (counts[Mb * spmm_batch_waves()]) and
-// their exclusive scan (offsets, one more entry), err (set for an invalid
-// row_ptr or column), flags (2: a strip's row is not strictly increasing;
-// 4: an Inf or NaN value) and status[5] = {batches, blocks, err, flags, go}:
-// go is decided on the device (valid, sorted and finite input, not a fully
-// populated grid, 1 .. cap batches, 3 * batches <= blocks).  csr_pack_emit
-// writes the A' operands (1 KB per batch) and B-row indices (32 per batch)
-// when go is set and nothing otherwise, so it can be queued before the host
-// reads the status; a, rows hold cap batches.  csr_pack_status copies the
-// status to the host (one synchronization).  csr_pack_covers: the strip
-// kernels' LDS holds ceil(K / 16) column blocks.  csr_pack_batch_bound: an
-// upper bound on the batch count (the smaller of 2 nnz / 33 +
-// min(Mb * waves, nnz) and Mb * ceil(Kb / 2)).
+// CSR -> packed column batches (convert.hip), formed from the CSR strips
+// without padded blocks.  V = uint16_t: the fp16 batches that
+// spmm_f16_packed multiplies (per (block-row, wave) chains, 1152 B per
+// batch); V = uint32_t: the fp32 batches that spmm_f32_packed multiplies
+// (one count per strip, a multiple of 4 batches, 272 B per batch).
+// csr_pack_analyse: per strip its block count (bcounts[Mb]) and their
+// exclusive scan (brp, Mb + 1 entries: the BCSR row_ptr), the batch counts
+// (counts: Mb * spmm_batch_waves() for fp16, Mb for fp32) and their exclusive
+// scan (offsets, one more entry), err (set for an invalid row_ptr or
+// column), flags (2: a strip's row is not strictly increasing; 4, fp16 only:
+// an Inf or NaN value) and status[5] = {batches, blocks, err, flags, go}:
+// go is decided on the device (valid and sorted input, fp16 finite, not a
+// fully populated grid, 1 .. cap batches that take at most three quarters of
+// the padded blocks' bytes).  csr_pack_emit writes the batches (A' operands,
+// then B-row indices, in a and rows, each holding cap batches) when go is
+// set and nothing otherwise, so it can be queued before the host reads the
+// status.  csr_pack_status copies the status to the host (one
+// synchronization).  csr_pack_covers: the strip kernels' LDS holds
+// ceil(K / 16) column blocks.  csr_pack_batch_bound: an upper bound on the
+// batch count (fp16: the smaller of 2 nnz / 33 + min(Mb * waves, nnz) and
+// Mb * ceil(Kb / 2); fp32: the smaller of nnz / 4 + 4 Mb and Mb (4 Kb + 4)).
 struct PackStatus {
     int64_t nbatches, nnzb;
     int err;
@@ -398,14 +411,14 @@ struct PackStatus {
     bool go;
 };
 bool csr_pack_covers(int64_t K);
-int64_t csr_pack_batch_bound(int64_t M, int64_t K, int64_t nnz);
-template <typename I>
-void csr_pack_analyse(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci,
-                      const uint16_t* vals, I* bcounts, I* brp, int32_t* counts, int64_t* offsets,
-                      int* err, unsigned int* flags, int64_t cap, int64_t* status, hipStream_t s);
+int64_t csr_pack_batch_bound(int64_t M, int64_t K, int64_t nnz, int value_bytes);
+template <typename I, typename V>
+void csr_pack_analyse(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const V* vals,
+                      I* bcounts, I* brp, int32_t* counts, int64_t* offsets, int* err,
+                      unsigned int* flags, int64_t cap, int64_t* status, hipStream_t s);
 PackStatus csr_pack_status(const int64_t* status, hipStream_t s);
-template <typename I>
-void csr_pack_emit(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const uint16_t* vals,
+template <typename I, typename V>
+void csr_pack_emit(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const V* vals,
                    const int64_t* offsets, const int64_t* status, int64_t cap, void* a, uint32_t* rows,
                    hipStream_t s);
 

@@ -26,22 +26,27 @@
 // arrays at their exact size, as the reference does
 // (src/core/conversion.cpp:66-73).
 //
-// fp16 products that spmm_f16_packed covers take a third form: the
-// conversion writes the column batches the BCSR column-batch kernel would
-// form (csr_pack_analyse / csr_pack_emit in convert.hip) instead of padded
-// blocks, and the packed product multiplies them, its store writing product
-// row r to C row perm[r] (un-permutation fused; no C_temp).  C is the BCSR
-// form's bit for bit.  The batch arrays are sized from a bound
-// (csr_pack_batch_bound, at most 2 nnz / 33 + Mb * 4 batches of 1152 bytes)
-// so the conversion is queued without a host round trip; the device decides
-// whether the form is taken (sorted, finite input whose batches save a
-// quarter of the block bytes), and when it is not, the host converts to BCSR
-// at the exact size (the count is then known), inside the unused batch
-// arrays when they hold it, else in a new allocation after releasing them.  XSPMM_PIPELINE_FORMAT=bcsr keeps the BCSR form.
+// Products that the packed kernels cover take a third form: the conversion
+// writes column batches (csr_pack_analyse / csr_pack_emit in convert.hip)
+// instead of padded blocks, and a packed product multiplies them, its store
+// writing product row r to C row perm[r] (un-permutation fused; no C_temp).
+// fp16: the batches the BCSR column-batch kernel would form, multiplied by
+// spmm_f16_packed, so C is the BCSR form's bit for bit.  fp32: a strip's
+// non-zero columns four at a time, multiplied by spmm_f32_packed (the same
+// products summed in another order).  The batch arrays are sized from a
+// bound (csr_pack_batch_bound) so the conversion is queued without a host
+// round trip; the device decides whether the form is taken (sorted input,
+// for fp16 finite, whose batches save a quarter of the block bytes), and when
+// it is not, the host converts to BCSR at the exact size (the count is then
+// known), inside the unused batch arrays when they hold it, else in a new
+// allocation after releasing them.  Bound-sized batch arrays above 128 MiB
+// are not taken: the host reads the status first and sizes the batches (or
+// the BCSR arrays) exactly.  XSPMM_PIPELINE_FORMAT=bcsr keeps the BCSR form.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <type_traits>
 #include <vector>
 
 #include "internal.hpp"
@@ -55,9 +60,16 @@ namespace {
 // exact sizing after one host round trip).
 constexpr size_t kFusedConversionBytes = size_t(1) << 30;
 
-// Bytes of one packed column batch: its A' operand (1 KB) and 32 B-row
-// indices.
+// Largest bound-sized batch arrays the packed conversion takes (above it,
+// exact sizing after one host round trip): the bound can exceed the exact
+// size many times over for dense blocks (17x for fp32 full blocks), and
+// what the pipeline holds stays reserved in the device pool.
+constexpr size_t kPackedFusedBytes = size_t(128) << 20;
+
+// Bytes of one packed column batch: fp16, its A' operand (1 KB) and 32 B-row
+// indices; fp32, its A' operand (16 rows x 4 slots) and 4 B-row indices.
 constexpr size_t kPackedBatchBytes = 1024 + 128;
+constexpr size_t kPacked32BatchBytes = 256 + 16;
 
 // Device bytes of the last pipeline call's temporaries on this thread, and
 // whether it multiplied packed column batches.
@@ -104,15 +116,22 @@ template void jaccard_clustering_dispatch<int64_t>(int64_t, int64_t, int64_t, co
                                                    const int64_t*, float, int64_t, int64_t*,
                                                    hipStream_t);
 
-// The fp16 pipeline converts into packed column batches when the packed
-// kernel covers the product (the same rule as spmm_f16_packed's) and
+// The pipeline converts into packed column batches when the packed kernel
+// covers the product (the same rules as spmm_f16_packed's and
+// spmm_f32_packed's), the strip kernels' LDS holds the column blocks, and
 // XSPMM_PIPELINE_FORMAT is not "bcsr".
-bool packed_pipeline_covers(int64_t K, int64_t Mb, int64_t Kb, int64_t N)
+template <typename T>
+bool packed_pipeline_covers(int64_t K, int64_t Mb, int64_t Kb, int64_t N, const void* B, const void* C)
 {
     if (const char* e = std::getenv("XSPMM_PIPELINE_FORMAT"))
         if (std::strcmp(e, "bcsr") == 0) return false;
-    return N > 0 && N % 8 == 0 && K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
-           (N + 127) / 128 <= 65535 && spmm_f16_pack_supported(K, Mb, Kb) && csr_pack_covers(K);
+    if (N <= 0 || (N + 127) / 128 > 65535 || !csr_pack_covers(K)) return false;
+    if constexpr (sizeof(T) == 2)
+        return N % 8 == 0 && K * N * 2 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
+               spmm_f16_pack_supported(K, Mb, Kb);
+    else
+        return N % 4 == 0 && K * N * 4 <= (int64_t(1) << 31) && Mb <= 0x7fffffffLL &&
+               (reinterpret_cast<uintptr_t>(B) & 15) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
 }
 
 template <typename T, typename I>
@@ -130,19 +149,24 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     const int64_t Mb = (M + 15) / 16, Kb = (K + 15) / 16;
     const int nw = spmm_batch_waves();
 
-    // fp16 products the packed kernel covers convert straight into packed
-    // column batches (csr_pack_analyse / csr_pack_emit): no padded blocks are
-    // written or read.  Strips with unsorted or duplicate columns, non-finite
+    // Products the packed kernels cover convert straight into packed column
+    // batches (csr_pack_analyse / csr_pack_emit): no padded blocks are written
+    // or read.  Strips with unsorted or duplicate columns, fp16 non-finite
     // values, fully populated grids and products whose batches would not save
     // a quarter of the block bytes take the BCSR path; the device decides,
     // and the host learns the outcome after the conversion's kernels are
     // queued.
-    const bool try_packed = sizeof(T) == 2 && M > 0 && nnz > 0 && packed_pipeline_covers(K, Mb, Kb, N);
+    using V = std::conditional_t<sizeof(T) == 2, uint16_t, uint32_t>;  // value bits
+    constexpr size_t kBatchBytes = sizeof(T) == 2 ? kPackedBatchBytes : kPacked32BatchBytes;
+    constexpr size_t kBatchABytes = sizeof(T) == 2 ? 1024 : 256;  // A' operand of a batch
+    const int pnw = sizeof(T) == 2 ? nw : 1;                         // batch counts per strip
+    const bool try_packed = M > 0 && nnz > 0 && packed_pipeline_covers<T>(K, Mb, Kb, N, B, C);
     // The batch arrays are sized from csr_pack_batch_bound while that takes
-    // at most kFusedConversionBytes (then the whole conversion is queued with
-    // no host round trip), else exactly, after reading the count.
-    const int64_t pbound = try_packed ? std::max<int64_t>(1, csr_pack_batch_bound(M, K, nnz)) : 0;
-    const bool pfused = try_packed && (size_t)pbound * kPackedBatchBytes <= kFusedConversionBytes;
+    // at most kPackedFusedBytes (then the whole conversion is queued with no
+    // host round trip), else exactly, after reading the count.
+    const int64_t pbound =
+        try_packed ? std::max<int64_t>(1, csr_pack_batch_bound(M, K, nnz, (int)sizeof(T))) : 0;
+    const bool pfused = try_packed && (size_t)pbound * kBatchBytes <= kPackedFusedBytes;
     // Every temporary is taken before the first stage, so the stage times
     // hold the stages' own work, except arrays sized from a count the
     // conversion stage reads first (exactly sized BCSR arrays or batches).
@@ -168,8 +192,8 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     size_t o_bcounts = 0, o_counts = 0, o_offsets = 0, o_flags = 0, o_status = 0, o_order = 0;
     if (try_packed) {
         o_bcounts = cv.take((size_t)Mb * sizeof(I));
-        o_counts = cv.take((size_t)Mb * nw * sizeof(int32_t));
-        o_offsets = cv.take((size_t)(Mb * nw + 1) * sizeof(int64_t));
+        o_counts = cv.take((size_t)Mb * pnw * sizeof(int32_t));
+        o_offsets = cv.take((size_t)(Mb * pnw + 1) * sizeof(int64_t));
         o_flags = cv.take(sizeof(unsigned int));
         o_status = cv.take(5 * sizeof(int64_t));
         o_order = cv.take((size_t)Mb * sizeof(int32_t));
@@ -186,8 +210,8 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     Scratch tmp(cv.end, s);
     took(cv.end);
     // bound-sized batches: A' operands, then B-row indices
-    Scratch pbatch(pfused ? (size_t)pbound * kPackedBatchBytes : 0, s);
-    took(pfused ? (size_t)pbound * kPackedBatchBytes : 0);
+    Scratch pbatch(pfused ? (size_t)pbound * kBatchBytes : 0, s);
+    took(pfused ? (size_t)pbound * kBatchBytes : 0);
     char* const base = tmp.as<char>();
     const Piece d_perm{base + o_perm}, nrp{base + o_nrp}, nci{base + o_nci}, nvals{base + o_nvals},
         brp{base + o_brp}, err{base + o_err};
@@ -195,7 +219,8 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     const Piece bcounts{base + o_bcounts}, counts{base + o_counts}, offsets{base + o_offsets},
         flags{base + o_flags}, status{base + o_status}, order{base + o_order};
     void* pa = pbatch.get();
-    uint32_t* prows = pfused ? reinterpret_cast<uint32_t*>(pbatch.as<char>() + (size_t)pbound * 1024) : nullptr;
+    uint32_t* prows =
+        pfused ? reinterpret_cast<uint32_t*>(pbatch.as<char>() + (size_t)pbound * kBatchABytes) : nullptr;
     Scratch blocks;  // exactly sized BCSR arrays or batches
     Scratch ctmp_late;
 
@@ -224,14 +249,14 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
     bool packed = false;
     step.start();
     if (try_packed) {
-        const uint16_t* v16 = reinterpret_cast<const uint16_t*>(cvals);
-        csr_pack_analyse<I>(M, K, nnz, crp, cci, v16, bcounts.as<I>(), brp.as<I>(), counts.as<int32_t>(),
+        const V* vb = reinterpret_cast<const V*>(cvals);
+        csr_pack_analyse<I, V>(M, K, nnz, crp, cci, vb, bcounts.as<I>(), brp.as<I>(), counts.as<int32_t>(),
                             offsets.as<int64_t>(), err.as<int>(), flags.as<unsigned int>(),
                             pfused ? pbound : std::numeric_limits<int64_t>::max() / 2048,
                             status.as<int64_t>(), s);
         if (pfused)
-            csr_pack_emit<I>(M, K, nnz, crp, cci, v16, offsets.as<int64_t>(), status.as<int64_t>(), pbound,
-                             pa, prows, s);
+            csr_pack_emit<I, V>(M, K, nnz, crp, cci, vb, offsets.as<int64_t>(), status.as<int64_t>(),
+                                pbound, pa, prows, s);
         if (spmm_order_wanted(Mb)) spmm_dispatch_order<I>(brp.as<I>(), Mb, order.as<int32_t>(), s);
         if (timed) step.stop(&tm[2]);
         const PackStatus st = csr_pack_status(status.as<int64_t>(), s);
@@ -243,12 +268,12 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
         if (packed && !pfused) {
             // exactly sized batches (the bracket adds to the conversion time)
             step.start();
-            blocks = Scratch((size_t)st.nbatches * kPackedBatchBytes, s);
-            took((size_t)st.nbatches * kPackedBatchBytes);
+            blocks = Scratch((size_t)st.nbatches * kBatchBytes, s);
+            took((size_t)st.nbatches * kBatchBytes);
             pa = blocks.get();
-            prows = reinterpret_cast<uint32_t*>(blocks.as<char>() + (size_t)st.nbatches * 1024);
-            csr_pack_emit<I>(M, K, nnz, crp, cci, v16, offsets.as<int64_t>(), status.as<int64_t>(),
-                             st.nbatches, pa, prows, s);
+            prows = reinterpret_cast<uint32_t*>(blocks.as<char>() + (size_t)st.nbatches * kBatchABytes);
+            csr_pack_emit<I, V>(M, K, nnz, crp, cci, vb, offsets.as<int64_t>(), status.as<int64_t>(),
+                                st.nbatches, pa, prows, s);
             if (timed) step.stop(&tm[2]);
         }
         if (!packed) {
@@ -259,12 +284,12 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
             const size_t o_ci = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(I));
             const size_t o_v = bc.take((size_t)(nnzb > 0 ? nnzb : 1) * 256 * sizeof(T));
             char* bb = nullptr;
-            if (pfused && bc.end <= (size_t)pbound * kPackedBatchBytes) {
+            if (pfused && bc.end <= (size_t)pbound * kBatchBytes) {
                 bb = pbatch.as<char>();  // the unused batch arrays hold them
             } else {
                 if (pfused) {
                     pbatch = Scratch();
-                    live -= (size_t)pbound * kPackedBatchBytes;
+                    live -= (size_t)pbound * kBatchBytes;
                 }
                 blocks = Scratch(bc.end, s);
                 took(bc.end);
@@ -300,10 +325,15 @@ void spmm_pipeline(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, 
         // row r to C row perm[r] (the un-permutation, fused: that stage's
         // time is not set).
         step.start();
-        const bool ok = spmm_f16_packed<I>(
-            M, K, Mb, offsets.as<int64_t>(), pa, prows, reinterpret_cast<const uint16_t*>(B), C, N,
-            spmm_order_wanted(Mb) ? order.as<int32_t>() : nullptr,
-            optimize_pattern ? d_perm.as<I>() : nullptr, s);
+        const int32_t* ord = spmm_order_wanted(Mb) ? order.as<int32_t>() : nullptr;
+        const I* rmap = optimize_pattern ? d_perm.as<I>() : nullptr;
+        bool ok;
+        if constexpr (sizeof(T) == 2)
+            ok = spmm_f16_packed<I>(M, K, Mb, offsets.as<int64_t>(), pa, prows,
+                                    reinterpret_cast<const uint16_t*>(B), C, N, ord, rmap, s);
+        else
+            ok = spmm_f32_packed<I>(M, K, Mb, offsets.as<int64_t>(), pa, prows,
+                                    reinterpret_cast<const float*>(B), C, N, ord, rmap, s);
         if (!ok) throw std::runtime_error("xSpMM: the packed product does not cover this shape.");
         if (timed) step.stop(&tm[3]);
     } else if (optimize_pattern) {

@@ -9,6 +9,11 @@
 //   * fp16, N % 8 == 0, on the batch kernel: its store writes product row r
 //     straight into C row perm[r] -- the un-permutation of the pipeline fused
 //     into the SpMM, one launch, no temporary;
+//   * packed column batches, when they take at most 3/4 of the BCSR values'
+//     bytes: fp16, the batch kernel's batches (spmm_f16_packed); fp32, the
+//     pipeline's packed fp32 batches formed from the permuted CSR
+//     (csr_pack_analyse / csr_pack_emit, spmm_f32_packed); both with the
+//     fused store;
 //   * a fully populated block grid takes the GEMM-tiled kernel, as in the
 //     pipeline, with the same fused store;
 //   * otherwise (fp32, other N) the product goes to a workspace kept by the
@@ -19,6 +24,7 @@
 // Calls on one plan must not overlap (they share the workspace).
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 #include <vector>
 
 #include "internal.hpp"
@@ -111,11 +117,14 @@ public:
         bvals_.reset((size_t)(nnzb_ > 0 ? nnzb_ : 1) * 256 * sizeof(T));
         csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp_.as<I>(), bci_.as<I>(),
                                bvals_.as<T>(), s);
-        if (sizeof(T) == 2 && spmm_order_wanted(Mb_)) {
+        if (spmm_order_wanted(Mb_)) {
             order_.reset((size_t)Mb_ * sizeof(int32_t));
             spmm_dispatch_order<I>(brp_.as<I>(), Mb_, order_.as<int32_t>(), s);
         }
-        if constexpr (sizeof(T) == 2) pack(s);
+        if constexpr (sizeof(T) == 2)
+            pack(s);
+        else
+            pack32(M, K, nnz, crp, cci, reinterpret_cast<const uint32_t*>(cvals), s);
         if (tm) step.stop(&tm[2]);
         if (tm) total.stop(&tm[5]);
         XSPMM_HIP_CHECK(hipStreamSynchronize(s));
@@ -148,6 +157,43 @@ public:
         packed_ = true;
     }
 
+    // Packed fp32 column batches from the (permuted) CSR, as the pipeline
+    // forms them; kept when the device's decision takes them (sorted input,
+    // batches at most 3/4 of the BCSR values' bytes).
+    void pack32(int64_t M, int64_t K, int64_t nnz, const I* rp, const I* ci, const uint32_t* v,
+                hipStream_t s)
+    {
+        if (M == 0 || nnz == 0 || !csr_pack_covers(K)) return;
+        if (const char* e = std::getenv("XSPMM_PLAN_PACK"))
+            if (std::strcmp(e, "off") == 0) return;
+        Carve cv;
+        const size_t o_bc = cv.take((size_t)Mb_ * sizeof(I));
+        const size_t o_brp = cv.take((size_t)(Mb_ + 1) * sizeof(I));
+        const size_t o_cnt = cv.take((size_t)Mb_ * sizeof(int32_t));
+        const size_t o_err = cv.take(sizeof(int));
+        const size_t o_flags = cv.take(sizeof(unsigned int));
+        const size_t o_st = cv.take(5 * sizeof(int64_t));
+        Scratch tmp(cv.end, s);
+        char* b = tmp.as<char>();
+        DeviceBuffer offsets((size_t)(Mb_ + 1) * sizeof(int64_t));
+        csr_pack_analyse<I, uint32_t>(M, K, nnz, rp, ci, v, reinterpret_cast<I*>(b + o_bc),
+                                      reinterpret_cast<I*>(b + o_brp), reinterpret_cast<int32_t*>(b + o_cnt),
+                                      offsets.as<int64_t>(), reinterpret_cast<int*>(b + o_err),
+                                      reinterpret_cast<unsigned int*>(b + o_flags),
+                                      std::numeric_limits<int64_t>::max() / 2048,
+                                      reinterpret_cast<int64_t*>(b + o_st), s);
+        const PackStatus st = csr_pack_status(reinterpret_cast<const int64_t*>(b + o_st), s);
+        if (!st.go) return;
+        pa_.reset((size_t)st.nbatches * 256);
+        prow_.reset((size_t)st.nbatches * 16);
+        csr_pack_emit<I, uint32_t>(M, K, nnz, rp, ci, v, offsets.as<int64_t>(),
+                                   reinterpret_cast<const int64_t*>(b + o_st), st.nbatches, pa_.as<void>(),
+                                   prow_.as<uint32_t>(), s);
+        poff_ = std::move(offsets);
+        nbatches_ = st.nbatches;
+        packed_ = true;
+    }
+
     void execute(const void* Bv, float* C, int64_t N, hipStream_t s) override
     {
         if (N < 0) throw std::invalid_argument("xSpMM: negative N.");
@@ -159,6 +205,11 @@ public:
                                               prow_.as<uint32_t>(),
                                               reinterpret_cast<const uint16_t*>(B), C, N, order,
                                               clustered_ ? perm_.as<I>() : nullptr, s))
+                return;
+        } else {
+            if (packed_ && spmm_f32_packed<I>(M_, K_, Mb_, poff_.as<int64_t>(), pa_.as<void>(),
+                                              prow_.as<uint32_t>(), reinterpret_cast<const float*>(B), C,
+                                              N, order, clustered_ ? perm_.as<I>() : nullptr, s))
                 return;
         }
         if (!clustered_) {

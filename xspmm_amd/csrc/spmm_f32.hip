@@ -46,6 +46,10 @@
 // formed), as in the fp16 column-batch kernel.
 // grid = (block-rows, ceil(N / (64 NQ))); N % 4 == 0, B 16-byte aligned,
 // K * N * 4 <= 2^31, Kb < 2^21 (32-bit offsets within a row and into B).
+//
+// spmm_f32_packed_kernel (below) multiplies the same kind of batches stored
+// once, from the Tier-2 pipeline's CSR conversion, instead of forming them
+// from the blocks.
 #include <cstdlib>
 #include <string>
 
@@ -507,6 +511,144 @@ void launch_batch(dim3 grid, hipStream_t s, const I* brp, const I* bci, const fl
                            v, b, C, M, K, N, Kb, order, row_map);
 }
 
+// ---------------------------------------------------------------------------
+// Packed fp32 column batches (the Tier-2 pipeline's fp32 form, written by
+// csr_pack_emit in convert.hip): strip br's batches [offsets[br],
+// offsets[br + 1]) hold its set columns four at a time (batch t: slots
+// 4t .. 4t+3, one per MFMA K position), in groups of four batches.  Group G
+// is one 16-byte load per lane of A' (lane (i, k): A'[i][k] of batches 4G ..
+// 4G+3) and one of row indices (lane (n, k): B row of slot k of the four
+// batches).  Wave w of the workgroup of block-row br multiplies the strip's
+// groups w, w + 4, ... in order: per batch and 64-column quad, the B rows of
+// its four slots as one 16-byte load per lane, straight into MFMA B operands
+// (as spmm_f32_batch_kernel does), then one v_mfma_f32_16x16x4f32 per float4
+// component.  Row indices arrive two groups ahead and B rows and A' one group
+// ahead; every iteration issues the same loads (the ones past the wave's
+// groups read nothing or are not multiplied), so each wait counts exactly
+// the loads it must.  The waves' partial tiles are summed through LDS in wave
+// order; product row r goes to C row row_map[r] when row_map is given.
+// grid = (block-rows, ceil(N / (64 NQ))); N % 4 == 0, B and C 16-byte
+// aligned, K * N * 4 <= 2^31.
+template <typename I, int NQ>
+__global__ __launch_bounds__(256, 4) void spmm_f32_packed_kernel(
+    const int64_t* __restrict__ offsets, const float* __restrict__ pa, const uint32_t* __restrict__ prow,
+    const float* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
+    const int32_t* __restrict__ order, const I* __restrict__ row_map)
+{
+    static_assert(NQ == 1 || NQ == 2, "64 or 128 columns per workgroup");
+    constexpr int W = 4;
+    constexpr int kCols = 64 * NQ;
+    __shared__ __align__(16) float red[W * 16 * kCols];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+
+    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    // a caller-supplied order holds a permutation of the block-rows; an id
+    // outside the grid is skipped rather than read past the offsets
+    if ((uint64_t)br >= (uint64_t)gridDim.x) return;
+    const int64_t n0 = (int64_t)blockIdx.y * kCols;
+    const int64_t G0 = offsets[br] >> 2;
+    const int64_t ng = (offsets[br + 1] >> 2) - G0;
+    // this wave's groups: G0 + wave + W i, i < n
+    const int64_t n = ng > wave ? (ng - wave + W - 1) / W : 0;
+
+    // reads past the strip's groups return zeros
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(pa + G0 * 256, (uint32_t)(ng * 1024));
+    const __amdgpu_buffer_rsrc_t r_rsrc = make_rsrc(prow + G0 * 16, (uint32_t)(ng * 64));
+    const uint32_t b_bytes = (uint32_t)(K * N * 4);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(B, b_bytes);
+    const uint32_t rowbytes = (uint32_t)(4 * N);
+    const uint32_t k32 = (uint32_t)K;
+    constexpr uint32_t kNone = 0xffffffffu;
+    uint32_t b_lane[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int64_t col = n0 + 64 * q + 4 * li;
+        b_lane[q] = col < N ? (uint32_t)(4 * col) : kNone;
+    }
+    // byte offsets of group i of this wave in the strip's A' and index arrays
+    const uint32_t a_off0 = (uint32_t)wave * 1024u + 16u * (uint32_t)lane;
+    const uint32_t r_off0 = (uint32_t)wave * 64u + 16u * (uint32_t)g;
+
+    float4_t acc[NQ][4];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[q][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto load_rows = [&](int64_t i) __attribute__((always_inline)) -> u32x4_t {
+        return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               r_rsrc, (int)(r_off0 + (uint32_t)i * (64u * W)), 0, 0));
+    };
+    // group i's A' and B rows (rows r: slot k of its four batches)
+    auto load_group = [&](int64_t i, const u32x4_t& r, float4_t& a, float4_t (&bq)[4][NQ])
+        __attribute__((always_inline)) {
+        a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                             a_rsrc, (int)(a_off0 + (uint32_t)i * (1024u * W)), 0,
+                                             kNonTemporal));
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const uint32_t row = r[c];
+                const uint32_t off =
+                    (row < k32 && b_lane[q] != kNone) ? __umul24(row, rowbytes) + b_lane[q] : b_bytes;
+                bq[c][q] = __builtin_bit_cast(float4_t,
+                                              __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)off, 0, 0));
+            }
+    };
+    auto multiply = [&](const float4_t& a, const float4_t (&bq)[4][NQ]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], bq[c][q][j], acc[q][j], 0, 0, 0);
+    };
+
+    if (n > 0) {
+        float4_t a0, a1;
+        float4_t b0[4][NQ], b1[4][NQ];
+        u32x4_t r0 = load_rows(0);
+        u32x4_t r1 = load_rows(1);
+        load_group(0, r0, a0, b0);
+        for (int64_t i = 0; i < n; i += 2) {
+            // group i in a0 / b0, rows of group i + 1 in r1
+            r0 = load_rows(i + 2);
+            load_group(i + 1, r1, a1, b1);
+            multiply(a0, b0);
+            // group i + 1 in a1 / b1, rows of group i + 2 in r0
+            r1 = load_rows(i + 3);
+            load_group(i + 2, r0, a0, b0);
+            if (i + 1 < n) multiply(a1, b1);
+        }
+    }
+
+    // sum the waves' partial tiles in wave order and store C
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<float4_t*>(red + wave * 16 * kCols + (4 * g + i) * kCols + 64 * q + 4 * li) =
+                float4_t{acc[q][0][i], acc[q][1][i], acc[q][2][i], acc[q][3][i]};
+    __syncthreads();
+    for (int t = threadIdx.x; t < 16 * kCols / 4; t += 64 * W) {
+        const int row = t / (kCols / 4);
+        const int c4 = 4 * (t % (kCols / 4));
+        const int64_t grow = br * 16 + row;
+        const int64_t col = n0 + c4;
+        if (grow >= M || col >= N) continue;
+        float4_t v = *reinterpret_cast<const float4_t*>(red + row * kCols + c4);
+#pragma unroll
+        for (int w = 1; w < W; ++w) v += *reinterpret_cast<const float4_t*>(red + w * 16 * kCols + row * kCols + c4);
+        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+        *reinterpret_cast<float4_t*>(C + crow * N + col) = v;
+    }
+}
+
 }  // namespace
 
 bool spmm_f32_batch_covers(int64_t K, int64_t Kb, int64_t N, const void* B, const void* C)
@@ -538,6 +680,34 @@ template void bcsr_spmm_f32_batch<int32_t>(int64_t, int64_t, int64_t, int64_t, c
 template void bcsr_spmm_f32_batch<int64_t>(int64_t, int64_t, int64_t, int64_t, const int64_t*,
                                            const int64_t*, const float*, const float*, float*,
                                            int64_t, const int32_t*, const int64_t*, hipStream_t);
+
+template <typename I>
+bool spmm_f32_packed(int64_t M, int64_t K, int64_t Mb, const int64_t* offsets, const void* a,
+                     const uint32_t* rows, const float* B, float* C, int64_t N, const int32_t* order,
+                     const I* row_map, hipStream_t s)
+{
+    if (M == 0 || N == 0 || Mb == 0) return true;
+    if (N % 4 != 0 || K * N * 4 > (int64_t(1) << 31) || (reinterpret_cast<uintptr_t>(B) & 15) != 0 ||
+        (reinterpret_cast<uintptr_t>(C) & 15) != 0 || (reinterpret_cast<uintptr_t>(a) & 15) != 0 ||
+        (N + 127) / 128 > 65535 || Mb > 0x7fffffffLL)
+        return false;
+    const float* pa = static_cast<const float*>(a);
+    if (N <= 64)
+        hipLaunchKernelGGL((spmm_f32_packed_kernel<I, 1>), dim3((unsigned)Mb, 1), dim3(256), 0, s, offsets, pa,
+                           rows, B, C, M, K, N, order, row_map);
+    else
+        hipLaunchKernelGGL((spmm_f32_packed_kernel<I, 2>), dim3((unsigned)Mb, (unsigned)((N + 127) / 128)),
+                           dim3(256), 0, s, offsets, pa, rows, B, C, M, K, N, order, row_map);
+    XSPMM_LAUNCH_CHECK();
+    return true;
+}
+
+template bool spmm_f32_packed<int32_t>(int64_t, int64_t, int64_t, const int64_t*, const void*,
+                                       const uint32_t*, const float*, float*, int64_t, const int32_t*,
+                                       const int32_t*, hipStream_t);
+template bool spmm_f32_packed<int64_t>(int64_t, int64_t, int64_t, const int64_t*, const void*,
+                                       const uint32_t*, const float*, float*, int64_t, const int32_t*,
+                                       const int64_t*, hipStream_t);
 
 }  // namespace detail
 }  // namespace xspmm
