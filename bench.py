@@ -471,11 +471,22 @@ def main():
                      "packed_batches": plan.packed_batches,
                      "effective_tflops": 2.0 * nnz * N / (ex_ms * 1e-3) / 1e12}
         if plan.packed_batches > 0:
-            # streamed per call: packed A' (1 KB) + indices (128 B) per batch,
-            # 4 offsets per block-row, B once, C once, the permutation once
-            pb = (plan.packed_batches * 1152 + (4 * Mb + 1) * 8 + K * N * p.vals.dtype.itemsize
-                  + M * N * 4 + M * p.rp.dtype.itemsize)
-            plan_info.update(bytes_per_call=pb, achieved_gbs=pb / (ex_ms * 1e-3) / 1e9)
+            # streamed per call: per batch the packed A' and B-row indices
+            # (fp16: 1 KB + 128 B, offsets for 4 waves per block-row; fp32:
+            # 256 B + 16 B, one offset per block-row), B once, C once, the
+            # permutation once
+            f16 = p.vals.dtype.itemsize == 2
+            per_batch, per_row = (1152, 4) if f16 else (272, 1)
+            pb = (plan.packed_batches * per_batch + (per_row * Mb + 1) * 8
+                  + K * N * p.vals.dtype.itemsize + M * N * 4 + M * p.rp.dtype.itemsize)
+            plan_info.update(bytes_per_call=pb, achieved_gbs=pb / (ex_ms * 1e-3) / 1e9,
+                             hbm_frac=pb / (ex_ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+            if not f16:
+                # executed matrix-core work: per batch and 64 columns, four
+                # v_mfma_f32_16x16x4f32 (16 x 16 x 4 multiply-adds each)
+                fl = plan.packed_batches * ((N + 63) // 64) * 4 * 2 * 16 * 16 * 4
+                plan_info.update(executed_mfma_tflops=fl / (ex_ms * 1e-3) / 1e12,
+                                 mfma_frac=fl / (ex_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS)
         if stages:
             plan_info["pipeline_spmm_plus_unpermute_ms"] = stages["spmm_ms"] + stages["unpermutation_ms"]
         plan.close()

@@ -105,11 +105,13 @@ public:
 
     std::shared_ptr<const Executor> get_executor() const { return exec_; }
 
-    // Dispatch order of the Tier-1 column-batch kernels (block-row ids, longest rows
-    // first; num_block_rows int32 entries on the executor), which csr_to_bcsr
-    // computes once for grids with many block-rows so that Tier-1 calls do
-    // not order the rows again.  Null: Tier-1 orders them on each call when
-    // it needs to.  set_dispatch_order takes ownership of an array allocated
+    // Dispatch order of the Tier-1 column-batch kernels (block-row ids; at
+    // least num_block_rows int32 entries on the executor), which csr_to_bcsr
+    // computes once per matrix so that Tier-1 calls do not order the rows
+    // again: above 2048 block-rows the longest rows first, from 256 a
+    // contiguous range of block-rows per XCD when the rows are short and
+    // neighbouring rows alike.  Null: Tier-1 orders the rows on each call
+    // when it needs to (above 2048 block-rows).  set_dispatch_order takes ownership of an array allocated
     // with this matrix's executor; copy_from_host drops it (the row lengths
     // may change).
     const int32_t* get_dispatch_order() const { return dispatch_order_; }

@@ -88,10 +88,13 @@ int64_t xspmm_noalloc_scratch_bytes(void);
 
 /*
  * Dispatch order of the Tier-1 column-batch kernels (fp16 and fp32) for a
- * block-row grid: when Tier-1
- * would order this grid's rows (more than 2048 block-rows), writes the Mb
- * block-row ids (int32, longest rows first) to `order` and sets
- * *written = 1; otherwise writes nothing and sets *written = 0.
+ * block-row grid: when Tier-1 would order this grid's rows (at least 256
+ * block-rows), writes the Mb block-row ids (int32) to `order` and sets
+ * *written = 1; otherwise writes nothing and sets *written = 0.  Above 2048
+ * block-rows the longest rows come first; up to 2048 each of the 8 XCDs
+ * takes a contiguous range of block-rows (workgroup i runs block-row
+ * start[i % 8] + i / 8), so neighbouring rows' shared B rows stay in one
+ * XCD's L2.
  * Asynchronous on `stream`.
  * No counterpart in the reference: Tier-1 computes this order on every call
  * on long grids; a caller that multiplies one matrix many times computes it
@@ -100,6 +103,26 @@ int64_t xspmm_noalloc_scratch_bytes(void);
  */
 int xspmm_bcsr_dispatch_order(int itype, int64_t Mb, const void* brp, int32_t* order,
                               int* written, void* stream);
+
+/*
+ * The dispatch order that csr_to_bcsr keeps on a C++ BCSRMatrix, computed
+ * once per matrix from its row_ptr and col_ind (bci), into `order` (Mb + 1
+ * int32; the last entry is scratch).  Above 2048 block-rows: the longest rows
+ * first (as xspmm_bcsr_dispatch_order), *written = 1, asynchronous on
+ * `stream`.  From 256 to 2048 block-rows, when the block-rows hold at most 128
+ * blocks on average and neighbouring block-rows are alike (the middle block
+ * columns of at least half of 256 sampled neighbour pairs differ by at most
+ * max(2, length / 8)): each of the 8 XCDs takes a contiguous range of
+ * block-rows (workgroup i runs block-row start[i % 8] + i / 8), so the B rows
+ * neighbours share stay in one XCD's L2, *written = 1; otherwise *written =
+ * 0 (the identity: pass no order).  This range synchronizes `stream`.  Below
+ * 256 block-rows nothing is written (*written = 0).  C is the same bit for
+ * bit with any order.
+ * No counterpart in the reference (whose kernel takes block-rows in grid
+ * order, src/common/spmm_math.hpp:20-30).
+ */
+int xspmm_bcsr_dispatch_order_cols(int itype, int64_t Mb, const void* brp, const void* bci,
+                                   int32_t* order, int* written, void* stream);
 
 /*
  * xspmm_bcsr_spmm with a dispatch order from xspmm_bcsr_dispatch_order

@@ -245,6 +245,56 @@ def test_spmm_many_skewed_block_rows(torch, N):
     check_c(host(C), ref, np.float16)
 
 
+def xcd_ranges(Mb):
+    """Workgroup i -> block-row start[i % 8] + i / 8 (XCD x: a contiguous range)."""
+    counts = np.array([(Mb - x + 7) // 8 for x in range(8)])
+    start = np.concatenate([[0], np.cumsum(counts)])[:-1]
+    i = np.arange(Mb)
+    return start[i % 8] + i // 8
+
+
+@pytest.mark.parametrize("case", ["band", "random_blocks", "long_rows", "short_grid"])
+def test_spmm_locality_order(torch, case):
+    """Grids of 256 .. 2048 block-rows: csr_to_bcsr keeps an order computed
+    from the block columns -- contiguous block-row ranges per XCD for short,
+    alike neighbouring rows (a narrow band) -- and none for unrelated
+    neighbours (random dense blocks), long rows (a wide band) or fewer than
+    256 block-rows.  C equals the unordered entry point's bit for bit."""
+    import ctypes as C
+    if case == "band":
+        p = synth.banded_sweep(0.01, M=8192, N=64)          # 512 block-rows, ~6 blocks each
+        expect = "xcd"
+    elif case == "random_blocks":
+        p = synth.blocks(M=8192, N=64)                      # 512 block-rows of random blocks
+        expect = "identity"
+    elif case == "long_rows":
+        p = synth.banded_sweep(0.5, M=8192, N=64)           # ~256 blocks per block-row
+        expect = "identity"
+    else:
+        p = synth.banded_sweep(0.01, M=2048, N=64)          # 128 block-rows
+        expect = None
+    A = X.CSRMatrix.from_host(p.M, p.K, p.rp, p.ci, p.vals)
+    Bm = X.csr_to_bcsr(A)
+    Mb = Bm.num_block_rows
+    order = Bm.dispatch_order()
+    if expect == "xcd":
+        o = host(order).astype(np.int64)
+        assert np.array_equal(o, xcd_ranges(Mb)), (case, o[:16])
+    else:
+        assert order is None  # the identity (or a short grid): no order passed
+    B = dev(torch, np.random.default_rng(3).uniform(-1, 1, (p.K, p.N)).astype(p.vals.dtype))
+    C1 = X.spmm(Bm, B)
+    L = X.load()
+    ptr = lambda t: C.c_void_p(t.data_ptr())
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    C2 = torch.full((p.M, p.N), float("nan"), dtype=torch.float32, device="cuda")
+    assert L.xspmm_bcsr_spmm(X.vcode(Bm.values.dtype), X.icode(Bm.row_ptr.dtype), Bm.num_rows,
+                             Bm.num_cols, Mb, Bm.num_block_cols, Bm.num_blocks, ptr(Bm.row_ptr),
+                             ptr(Bm.col_ind), ptr(Bm.values), ptr(B), ptr(C2), p.N, stream) == X.OK
+    torch.cuda.synchronize()
+    assert torch.equal(C1, C2)
+
+
 @pytest.mark.parametrize("itype", [np.int32, np.int64])
 def test_spmm_cached_dispatch_order(torch, itype):
     # Mb = 3000 > 2048: csr_to_bcsr keeps the longest-first dispatch order and

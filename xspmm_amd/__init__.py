@@ -67,6 +67,8 @@ def load():
                                           p, p]
     L.xspmm_bcsr_dispatch_order.restype = i32
     L.xspmm_bcsr_dispatch_order.argtypes = [i32, i64, p, p, C.POINTER(C.c_int), p]
+    L.xspmm_bcsr_dispatch_order_cols.restype = i32
+    L.xspmm_bcsr_dispatch_order_cols.argtypes = [i32, i64, p, p, p, C.POINTER(C.c_int), p]
     L.xspmm_csr_to_bcsr_count.restype = i32
     L.xspmm_csr_to_bcsr_count.argtypes = [i32, i64, i64, i64, p, p, i64, i64, p,
                                           C.POINTER(C.c_int64), p]
@@ -233,10 +235,12 @@ class BCSRMatrix:
     row_ptr: object   # [Mb+1]
     col_ind: object   # [nnzb]
     values: object    # [nnzb * r * c]
-    # The fp16 Tier-1 kernel's dispatch order (block-row ids, longest rows
-    # first), computed once for grids with more than 2048 block-rows and kept
-    # with the row_ptr tensor it came from (its identity and version): Tier-1
-    # would otherwise order the rows on every call.
+    # The Tier-1 column-batch kernels' dispatch order (block-row ids: longest
+    # rows first above 2048 block-rows, else a contiguous range of block-rows
+    # per XCD for short, alike neighbouring rows, or the identity; see
+    # xspmm_bcsr_dispatch_order_cols), computed once for grids of at least
+    # 256 block-rows and kept with the row_ptr and col_ind tensors it came
+    # from (their identities and versions).
     _order: object = field(default=None, repr=False, compare=False)
     _order_key: object = field(default=None, repr=False, compare=False)
 
@@ -248,16 +252,18 @@ class BCSRMatrix:
         """The cached dispatch order for the current row_ptr (computed on
         first use), or None when Tier-1 does not order this grid."""
         key = (id(self.row_ptr), self.row_ptr.data_ptr(), self.row_ptr._version,
+               id(self.col_ind), self.col_ind.data_ptr(), self.col_ind._version,
                int(self.num_block_rows))
         if self._order_key != key:
             torch = _torch()
-            order = torch.empty(max(int(self.num_block_rows), 1), dtype=torch.int32,
+            order = torch.empty(int(self.num_block_rows) + 1, dtype=torch.int32,
                                 device=self.row_ptr.device)
             written = C.c_int(0)
-            _check(load().xspmm_bcsr_dispatch_order(icode(self.row_ptr.dtype),
-                                                    int(self.num_block_rows), _ptr(self.row_ptr),
-                                                    _ptr(order), C.byref(written), _stream()))
-            self._order = order if written.value else None
+            _check(load().xspmm_bcsr_dispatch_order_cols(icode(self.row_ptr.dtype),
+                                                         int(self.num_block_rows), _ptr(self.row_ptr),
+                                                         _ptr(self.col_ind), _ptr(order),
+                                                         C.byref(written), _stream()))
+            self._order = order[:int(self.num_block_rows)] if written.value else None
             self._order_key = key
         return self._order
 

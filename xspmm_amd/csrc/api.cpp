@@ -284,11 +284,13 @@ BCSRMatrix<ValueType, IndexType> csr_to_bcsr(std::shared_ptr<const Executor> tar
             out.get_bcsr_col_ind(), dev(out.get_bcsr_values()), kStream);
         // the column-batch kernels' dispatch order, once (see BCSRMatrix);
         // owned by `out` from the allocation on, so a failed launch frees it
-        if (r_block == 16 && c_block == 16 && detail::spmm_order_wanted(Mb)) {
+        if (r_block == 16 && c_block == 16 && detail::spmm_order_cols_wanted(Mb)) {
             int32_t* order = nullptr;
-            target_exec->allocate(reinterpret_cast<void**>(&order), (size_t)Mb * sizeof(int32_t));
+            target_exec->allocate(reinterpret_cast<void**>(&order), (size_t)(Mb + 1) * sizeof(int32_t));
             out.set_dispatch_order(order);
-            detail::spmm_dispatch_order<IndexType>(out.get_bcsr_row_ptr(), Mb, order, kStream);
+            if (!detail::spmm_dispatch_order_cols<IndexType>(out.get_bcsr_row_ptr(), out.get_bcsr_col_ind(),
+                                                             Mb, order, kStream))
+                out.set_dispatch_order(nullptr);  // the identity: not worth a load per workgroup
         }
     } else {
         // GPU-resident input, host target: convert on the GPU, then copy down.

@@ -137,6 +137,26 @@ int xspmm_bcsr_dispatch_order(int itype, int64_t Mb, const void* brp, int32_t* o
     });
 }
 
+int xspmm_bcsr_dispatch_order_cols(int itype, int64_t Mb, const void* brp, const void* bci,
+                                   int32_t* order, int* written, void* stream)
+{
+    return guarded([&] {
+        if (Mb < 0) throw std::invalid_argument("xSpMM: negative number of block-rows.");
+        if (!written) throw std::invalid_argument("xSpMM: written must not be NULL.");
+        *written = 0;
+        if (!spmm_order_cols_wanted(Mb)) return;
+        if (!brp || !bci || !order)
+            throw std::invalid_argument("xSpMM: brp, bci and order must not be NULL.");
+        bool used = false;
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            used = spmm_dispatch_order_cols<I>(static_cast<const I*>(brp), static_cast<const I*>(bci), Mb,
+                                               order, as_stream(stream));
+        });
+        *written = used ? 1 : 0;
+    });
+}
+
 int xspmm_bcsr_spmm_ordered(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
                             int64_t nnzb, const void* brp, const void* bci, const void* bvals,
                             const void* B, float* C, int64_t N, const int32_t* order, void* stream)

@@ -230,11 +230,23 @@ template <typename T, typename I>
 void bcsr_spmm_noalloc(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
                        const I* bci, const T* bvals, const T* B, float* C, int64_t N,
                        hipStream_t s);
-// Longest-block-row-first dispatch order of the fp16 batch kernel: whether
-// the grid is long enough to use one, and the kernel that writes it (Mb ids).
+// Dispatch order of the column-batch kernels (fp16 and fp32), Mb block-row
+// ids.  spmm_order_wanted: a grid long enough (more than 2048 block-rows)
+// that Tier-1 orders it on every call that is given no order;
+// spmm_dispatch_order writes that order (longest rows first).
+// spmm_order_cols_wanted: a grid for which an order computed once per
+// matrix may pay (at least 256 block-rows); spmm_dispatch_order_cols writes
+// it into order[0 .. Mb] (Mb + 1 entries) and returns whether to use it:
+// longest rows first above 2048 block-rows (true, asynchronous), else, from
+// the block columns, a contiguous range of block-rows per XCD when the rows
+// are short and neighbouring rows alike (true) or the identity (false,
+// order not worth passing); below 2048 block-rows it synchronizes s.
 bool spmm_order_wanted(int64_t Mb);
+bool spmm_order_cols_wanted(int64_t Mb);
 template <typename I>
 void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s);
+template <typename I>
+bool spmm_dispatch_order_cols(const I* brp, const I* bci, int64_t Mb, int32_t* order, hipStream_t s);
 
 // Packed column batches (fp16): the batches the Tier-1 batch kernel forms
 // for each (block-row, wave) -- their A' operands (1 KB each) and B-row

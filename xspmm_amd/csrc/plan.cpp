@@ -117,9 +117,10 @@ public:
         bvals_.reset((size_t)(nnzb_ > 0 ? nnzb_ : 1) * 256 * sizeof(T));
         csr_to_bcsr_fill<T, I>(M, K, nnz, crp, cci, cvals, 16, 16, brp_.as<I>(), bci_.as<I>(),
                                bvals_.as<T>(), s);
-        if (spmm_order_wanted(Mb_)) {
-            order_.reset((size_t)Mb_ * sizeof(int32_t));
-            spmm_dispatch_order<I>(brp_.as<I>(), Mb_, order_.as<int32_t>(), s);
+        if (spmm_order_cols_wanted(Mb_)) {
+            order_.reset((size_t)(Mb_ + 1) * sizeof(int32_t));
+            if (!spmm_dispatch_order_cols<I>(brp_.as<I>(), bci_.as<I>(), Mb_, order_.as<int32_t>(), s))
+                order_.reset(0);  // the identity: not worth a load per workgroup
         }
         if constexpr (sizeof(T) == 2)
             pack(s);

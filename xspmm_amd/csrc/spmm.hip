@@ -30,7 +30,7 @@
 //                           step s pairing A[i][4g+s] with B[16*col + 4g + s][n].
 //
 // Work split: one workgroup per block-row (grid.x, or the dispatch order of
-// order_rows_kernel), N split over grid.y.
+// order_rows_kernel / xcd_rows_kernel), N split over grid.y.
 #include <cstdlib>
 #include <mutex>
 #include <string>
@@ -1204,17 +1204,33 @@ __global__ __launch_bounds__(64 * kBW, XSPMM_BATCH_MIN_WAVES) void spmm_f16_pack
 }
 
 // ---------------------------------------------------------------------------
-// Dispatch order for skewed block-rows: one 1024-thread workgroup buckets the
-// block-rows by the bit length of their block count (longest bucket first) and
-// writes the row ids in that order.  Workgroups are dispatched in id order, so
-// long rows start first instead of trailing the grid.  Only scheduling
-// changes: each row's result is computed exactly as before.
+// Dispatch orders of the column-batch kernels (block-row ids by workgroup id).
+// Only scheduling changes: each row's result is computed exactly as before.
+//   * more than kOrderMinRows block-rows (skewed rows trail a long grid): one
+//     1024-thread workgroup buckets the block-rows by the bit length of their
+//     block count and writes the row ids longest bucket first; workgroups are
+//     dispatched in id order, so long rows start first;
+//   * kXcdOrderMinRows .. kOrderMinRows block-rows, for an order computed
+//     once per matrix (spmm_dispatch_order_cols): when the block-rows are
+//     short (at most kXcdOrderMaxAvg blocks on average) and neighbouring
+//     block-rows are alike (their middle block columns differ by at most
+//     max(2, length / 8) for at least half of 256 sampled pairs), each XCD
+//     takes a contiguous range of block-rows: workgroups go to the 8 XCDs
+//     round-robin by id, so workgroup i takes row start[i % 8] + i / 8,
+//     where XCD x's range starts at start[x].  The B rows the neighbours
+//     share then stay in one XCD's L2 instead of being fetched by all eight
+//     (banded matrices at 0.5-5 %: 6-25 % faster).  Otherwise the order is
+//     the identity: long rows (a 90 % band ran 18 % slower with the XCD
+//     ranges) and unrelated neighbours (random dense blocks) gain nothing.
 // ---------------------------------------------------------------------------
 constexpr int kOrderThreads = 1024;
 #ifndef XSPMM_ORDER_MIN_ROWS
 #define XSPMM_ORDER_MIN_ROWS 2048
 #endif
 constexpr int64_t kOrderMinRows = XSPMM_ORDER_MIN_ROWS;
+constexpr int64_t kXcdOrderMinRows = 256;
+constexpr int64_t kXcdOrderMaxAvg = 128;
+constexpr int kXcds = 8;
 constexpr int kOrderBuckets = 33;
 
 template <typename I>
@@ -1247,6 +1263,43 @@ __global__ __launch_bounds__(kOrderThreads) void order_rows_kernel(const I* __re
         const uint32_t pos = atomicAdd(&next[bucket(r)], 1u);
         order[pos] = (int32_t)r;
     }
+}
+
+// one 256-thread workgroup: the decision above, then order[i] for i < Mb,
+// and order[Mb] = 1 for the XCD ranges, 0 for the identity
+template <typename I>
+__global__ __launch_bounds__(256) void order_local_kernel(const I* __restrict__ brp, const I* __restrict__ bci,
+                                                          int64_t Mb, int32_t* __restrict__ order)
+{
+    __shared__ int s_alike;
+    const int t = threadIdx.x;
+    if (t == 0) s_alike = 0;
+    __syncthreads();
+    const int64_t nnzb = (int64_t)brp[Mb] - (int64_t)brp[0];
+    if (Mb > 1 && nnzb <= kXcdOrderMaxAvg * Mb) {
+        const int64_t r = (int64_t)t * (Mb - 1) / 256;  // pair (r, r + 1)
+        const int64_t a0 = brp[r], a1 = brp[r + 1], a2 = brp[r + 2];
+        const int64_t l0 = a1 - a0, l1 = a2 - a1;
+        if (l0 > 0 && l1 > 0) {
+            const int64_t m0 = (int64_t)bci[a0 + l0 / 2], m1 = (int64_t)bci[a1 + l1 / 2];
+            const int64_t d = m1 > m0 ? m1 - m0 : m0 - m1;
+            const int64_t lim = l0 / 8 > 2 ? l0 / 8 : 2;
+            if (d <= lim) atomicAdd(&s_alike, 1);
+        }
+    }
+    __syncthreads();
+    const bool xcd = s_alike >= 128;
+    for (int64_t i = t; i < Mb; i += 256) {
+        int64_t br = i;
+        if (xcd) {
+            const int64_t x = i % kXcds;
+            int64_t start = 0;
+            for (int64_t y = 0; y < x; ++y) start += (Mb - y + kXcds - 1) / kXcds;
+            br = start + i / kXcds;
+        }
+        order[i] = (int32_t)br;
+    }
+    if (t == 0) order[Mb] = xcd ? 1 : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1432,6 +1485,8 @@ void check_alignment(const void* bvals, const void* B, bool b_vector)
 
 bool spmm_order_wanted(int64_t Mb) { return Mb > kOrderMinRows && Mb <= 0x7fffffffLL; }
 
+bool spmm_order_cols_wanted(int64_t Mb) { return Mb >= kXcdOrderMinRows && Mb <= 0x7fffffffLL; }
+
 int spmm_batch_waves() { return kBW; }
 
 bool spmm_f16_pack_supported(int64_t K, int64_t Mb, int64_t Kb)
@@ -1520,6 +1575,24 @@ void spmm_dispatch_order(const I* brp, int64_t Mb, int32_t* order, hipStream_t s
 }
 template void spmm_dispatch_order<int32_t>(const int32_t*, int64_t, int32_t*, hipStream_t);
 template void spmm_dispatch_order<int64_t>(const int64_t*, int64_t, int32_t*, hipStream_t);
+
+template <typename I>
+bool spmm_dispatch_order_cols(const I* brp, const I* bci, int64_t Mb, int32_t* order, hipStream_t s)
+{
+    if (Mb > kOrderMinRows) {
+        hipLaunchKernelGGL((order_rows_kernel<I>), dim3(1), dim3(kOrderThreads), 0, s, brp, Mb, order);
+        XSPMM_LAUNCH_CHECK();
+        return true;
+    }
+    hipLaunchKernelGGL((order_local_kernel<I>), dim3(1), dim3(256), 0, s, brp, bci, Mb, order);
+    XSPMM_LAUNCH_CHECK();
+    int32_t used = 0;
+    XSPMM_HIP_CHECK(hipMemcpyAsync(&used, order + Mb, sizeof(used), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    return used != 0;
+}
+template bool spmm_dispatch_order_cols<int32_t>(const int32_t*, const int32_t*, int64_t, int32_t*, hipStream_t);
+template bool spmm_dispatch_order_cols<int64_t>(const int64_t*, const int64_t*, int64_t, int32_t*, hipStream_t);
 
 namespace {
 
