@@ -1308,14 +1308,18 @@ __global__ __launch_bounds__(256) void order_local_kernel(const I* __restrict__ 
 // A workgroup of kF32Waves waves owns one block-row and NTW 16-column tiles
 // (up to 64 columns; the launcher narrows NTW when the grid would have fewer
 // than 512 workgroups).  The waves split the row's blocks (wave w: blocks
-// w, w + kF32Waves, ...), kF32Unroll blocks per step with all their loads
-// issued before the MFMAs (v_mfma_f32_16x16x4_f32, four per block and tile),
-// and their partial tiles are summed through LDS in wave order.  Splitting
-// the row keeps short rows' dependent load chains short: a small matrix has
-// few block-rows, and one wave per row would leave the chip idle.
+// w, w + kF32Waves, ...), f32_unroll(NTW) blocks per step with all their
+// loads issued before the MFMAs (v_mfma_f32_16x16x4_f32, four per block and
+// tile; a step past the row's end loads the row's last block again and does
+// not multiply it, so a wave's last blocks need no step of their own), and
+// their partial tiles are summed through LDS in wave order.  Splitting the
+// row keeps short rows' dependent load chains short: a small matrix has few
+// block-rows, and one wave per row would leave the chip idle.
 // ---------------------------------------------------------------------------
 constexpr int kF32Waves = 8;
-constexpr int kF32Unroll = 4;  // blocks per wave whose loads are in flight together
+// blocks per wave whose loads are in flight together: 8 at one tile (64
+// VGPRs of operands), fewer at wider tiles
+constexpr int f32_unroll(int ntw) { return ntw == 1 ? 8 : (ntw == 2 ? 4 : 2); }
 
 template <typename I, int NTW>
 __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __restrict__ brp,
@@ -1359,26 +1363,24 @@ __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __res
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bv[j][s], acc[j], 0, 0, 0);
     };
 
-    // the wave's blocks rs + wave + 8 i in ascending order, kF32Unroll at a
-    // time: all their loads first, then their MFMAs
-    int64_t blk = rs + wave;
-    for (; blk + (kF32Unroll - 1) * kF32Waves < re; blk += kF32Unroll * kF32Waves) {
-        float4_t a[kF32Unroll];
-        float bv[kF32Unroll][NTW][4];
+    // the wave's blocks rs + wave + 8 i in ascending order, U at a time:
+    // all their loads first, then their MFMAs (blocks past the row's end
+    // load the last block and are not multiplied: the order of the MFMAs
+    // is the blocks' order)
+    constexpr int U = f32_unroll(NTW);
+    for (int64_t blk = rs + wave; blk < re; blk += (int64_t)U * kF32Waves) {
+        float4_t a[U];
+        float bv[U][NTW][4];
 #pragma unroll
-        for (int u = 0; u < kF32Unroll; ++u) {
-            const int64_t b = blk + u * kF32Waves;
+        for (int u = 0; u < U; ++u) {
+            const int64_t b0 = blk + u * kF32Waves;
+            const int64_t b = b0 < re ? b0 : re - 1;
             a[u] = *reinterpret_cast<const float4_t*>(vals + b * 256 + li * 16 + g * 4);
             b_panel((int64_t)bci[b], bv[u]);
         }
 #pragma unroll
-        for (int u = 0; u < kF32Unroll; ++u) multiply(a[u], bv[u]);
-    }
-    for (; blk < re; blk += kF32Waves) {
-        const float4_t a0 = *reinterpret_cast<const float4_t*>(vals + blk * 256 + li * 16 + g * 4);
-        float b0[NTW][4];
-        b_panel((int64_t)bci[blk], b0);
-        multiply(a0, b0);
+        for (int u = 0; u < U; ++u)
+            if (blk + u * kF32Waves < re) multiply(a[u], bv[u]);
     }
 
 #pragma unroll
