@@ -8,7 +8,7 @@ count, above it -- as the reference's conversion does
 nnz = 256 * nnzb, so there the bound is 256x the exact size.
 xspmm_pipeline_temp_bytes reports the most the last call held at once.
 Products the packed kernels cover take packed column batches instead of BCSR
-arrays, sized from a bound on the batch count while that fits 128 MiB.
+arrays, sized from a bound on the batch count while that fits 256 MiB.
 """
 from __future__ import annotations
 
@@ -49,10 +49,12 @@ def block_diagonal(Mb, N, seed=0, dtype=np.float32):
 
 
 def test_full_blocks_take_exact_bcsr(torch):
-    """131072^2 block-diagonal fp32: the bound's block values would take
-    2 GiB, the exact arrays 8 MiB; the pipeline takes within 1.5x of the
-    exact bytes and C equals the block products."""
-    Mb, N = 8192, 16
+    """262144^2 block-diagonal fp32: the BCSR bound's block values would take
+    4 GiB and the packed batches' bound 300 MB, the exact arrays 17 MB; the
+    pipeline tries the packed form, whose device decision rejects full
+    blocks, and takes within 1.5x of the exact BCSR bytes; C equals the
+    block products."""
+    Mb, N = 16384, 16
     p, blocks = block_diagonal(Mb, N)
     sT, sI = 4, 4
     cap = min(p.nnz, Mb * Mb)

@@ -283,3 +283,36 @@ def test_fp32_templates_full_size(torch):
         C1, C0, packed = both_forms(torch, p, True)
     assert packed
     assert rel(C1, C0) <= 1e-6
+
+
+def heavy_strips(dtype, seed=11, M=2000, K=40000, N=64):
+    """Strips of more than 1024 column blocks (the emit kernels' heavy
+    launch): 24 rows of 1800 random columns among sparse ones, on a grid of
+    2500 column blocks."""
+    rng = np.random.default_rng(seed)
+    heavy = set(rng.choice(M, size=24, replace=False).tolist())
+    rows = []
+    for r in range(M):
+        k = 1800 if r in heavy else rng.binomial(K, 0.0008)
+        rows.append(np.sort(rng.choice(K, size=k, replace=False)))
+    rp = np.zeros(M + 1, np.int64)
+    rp[1:] = np.cumsum([len(x) for x in rows])
+    ci = np.concatenate(rows).astype(np.int32)
+    vals = rng.uniform(-1, 1, len(ci)).astype(dtype)
+    B = rng.uniform(-1, 1, size=(K, N)).astype(dtype)
+    return synth.Problem("heavy", M, K, N, rp.astype(np.int32), ci, vals, B)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("cluster", [False, True])
+def test_heavy_strips(torch, dtype, cluster):
+    p = heavy_strips(dtype)
+    brp, _, _ = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    assert np.diff(brp).max() > 1024
+    C1, C0, packed = both_forms(torch, p, cluster)
+    assert packed
+    if dtype == np.float16:
+        assert C1.tobytes() == C0.tobytes()
+    else:
+        assert rel(C1, C0) <= 1e-6
+    assert oracle.errors(C1, truth(p))["rel_frob"] <= (2e-3 if dtype == np.float16 else 1e-5)

@@ -535,11 +535,13 @@ __global__ void pack_decide_kernel(const int64_t* __restrict__ off_end, const I*
 }
 
 // One workgroup scans both count arrays and decides (one launch instead of
-// two device-wide scans and pack_decide_kernel) while the batch counts
-// number at most kPackScanMax.
+// two device-wide scans and pack_decide_kernel) while the batch counts fit
+// one pass of the workgroup (kPackScanMax); longer arrays take the
+// device-wide scans (at gnn, 32768 counts: 41 us in four passes of one
+// workgroup against 13 us).
 constexpr int kPackScanThreads = 1024;
 constexpr int kPackScanItems = 8;
-constexpr int64_t kPackScanMax = int64_t(1) << 17;
+constexpr int64_t kPackScanMax = (int64_t)kPackScanThreads * kPackScanItems;
 
 __device__ __forceinline__ int64_t wg_exclusive_scan_1024(int64_t v, int64_t* total, int64_t* red)
 {

@@ -39,7 +39,7 @@
 // for fp16 finite, whose batches save a quarter of the block bytes), and when
 // it is not, the host converts to BCSR at the exact size (the count is then
 // known), inside the unused batch arrays when they hold it, else in a new
-// allocation after releasing them.  Bound-sized batch arrays above 128 MiB
+// allocation after releasing them.  Bound-sized batch arrays above 256 MiB
 // are not taken: the host reads the status first and sizes the batches (or
 // the BCSR arrays) exactly.  XSPMM_PIPELINE_FORMAT=bcsr keeps the BCSR form.
 #include <algorithm>
@@ -63,8 +63,10 @@ constexpr size_t kFusedConversionBytes = size_t(1) << 30;
 // Largest bound-sized batch arrays the packed conversion takes (above it,
 // exact sizing after one host round trip): the bound can exceed the exact
 // size many times over for dense blocks (17x for fp32 full blocks), and
-// what the pipeline holds stays reserved in the device pool.
-constexpr size_t kPackedFusedBytes = size_t(128) << 20;
+// what the pipeline holds stays reserved in the device pool.  gnn's bound
+// (184 MB fp16, 151 MB fp32) stays under it: its exact path costs about
+// 100 us more (the host read and a new pool allocation).
+constexpr size_t kPackedFusedBytes = size_t(256) << 20;
 
 // Bytes of one packed column batch: fp16, its A' operand (1 KB) and 32 B-row
 // indices; fp32, its A' operand (16 rows x 4 slots) and 4 B-row indices.
