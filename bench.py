@@ -113,13 +113,17 @@ def tier1_kernel(value_bytes, K, N, nnzb, Mb):
     block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL selects
     another one; fp32 takes its column-batch kernel when N % 4 == 0 and B
     fits 32-bit offsets and the grid has at least 512 workgroups of 128
-    columns, unless XSPMM_F32_KERNEL=tile or =batch forces one)."""
+    columns, unless XSPMM_F32_KERNEL=tile or =batch forces one; otherwise
+    the short-grid kernel where 64 * Kb * N <= 2^30, unless
+    XSPMM_F32_SHORT=off)."""
     if value_bytes == 4:
         Kb = (K + 15) // 16
         choice = os.environ.get("XSPMM_F32_KERNEL", "")
         if (N % 4 == 0 and K * N * 4 <= 1 << 31 and Kb < 1 << 21 and choice != "tile"
                 and (choice == "batch" or Mb * ((N + 127) // 128) >= 512)):
             return "spmm_f32_batch_kernel"
+        if 64 * Kb * N <= 1 << 30 and os.environ.get("XSPMM_F32_SHORT", "") != "off":
+            return "spmm_f32_short_kernel"
         return "spmm_f32_kernel"
     Kb = (K + 15) // 16
     if (nnzb == Mb * Kb and N % 8 == 0 and Mb * Kb * 512 < 1 << 31 and K * N * 2 < 1 << 31

@@ -4,8 +4,11 @@ float is the only value type the reference exports
 (src/xspmm.cpp:102-114, src/hip/unstructured_mtx_mul.hip:105-106) and every
 reference benchmark runs in it, so a drop-in caller lands here.  Two fp32
 kernels exist: the column-batch kernel (spmm_f32.hip; the default where
-N % 4 == 0 and the grid has at least 512 workgroups) and the tile kernel
-(spmm.hip); XSPMM_F32_KERNEL=batch|tile forces one.  Bars:
+N % 4 == 0 and the grid has at least 512 workgroups) and the tile kernels
+(spmm.hip: the short-grid kernel with B through a buffer resource, and with
+XSPMM_F32_SHORT=off the one with 64-bit B addressing, which takes B beyond
+1 GiB); XSPMM_F32_KERNEL=batch|tile forces a family.  The tests name the
+64-bit form "tile64".  Bars:
   * C against the fp64 truth, relative Frobenius <= 1e-5 (the north-star
     tolerance of the fp32 path), for both kernels;
   * the examples/05 density sweep in fp32 (banded 16384^2, N = 128, B = ones):
@@ -41,17 +44,26 @@ def torch():
     return torch
 
 
+KERNEL_ENV = {
+    "batch": {"XSPMM_F32_KERNEL": "batch"},
+    "tile": {"XSPMM_F32_KERNEL": "tile"},
+    "tile64": {"XSPMM_F32_KERNEL": "tile", "XSPMM_F32_SHORT": "off"},
+}
+
+
 @contextlib.contextmanager
 def f32_kernel(name):
-    old = os.environ.get("XSPMM_F32_KERNEL")
-    os.environ["XSPMM_F32_KERNEL"] = name
+    env = KERNEL_ENV[name]
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         yield
     finally:
-        if old is None:
-            del os.environ["XSPMM_F32_KERNEL"]
-        else:
-            os.environ["XSPMM_F32_KERNEL"] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
 
 
 def note(msg):
@@ -109,7 +121,7 @@ def test_both_kernels_against_fp64(torch, shape):
                          dup_frac=0.05 if dups else 0.0)
     ref = truth(p)
     out = {}
-    for kern in ("batch", "tile"):
+    for kern in ("batch", "tile", "tile64"):
         C, Bm = run_tier1(torch, p, idx, kern)
         e = oracle.errors(C, ref)
         note(f"{M}x{K} N={N} d={dens} {np.dtype(idx).name} {kern}: nnzb {Bm.num_blocks} "
@@ -118,6 +130,44 @@ def test_both_kernels_against_fp64(torch, shape):
         assert e["rel_frob"] <= TOL, (kern, e)
         out[kern] = C
     assert oracle.errors(out["batch"], out["tile"])["rel_frob"] <= TOL
+    assert oracle.errors(out["tile64"], out["tile"])["rel_frob"] <= TOL
+
+
+@pytest.mark.parametrize("kern", ["tile", "tile64"])
+@pytest.mark.parametrize("itype", [np.int32, np.int64])
+def test_tile_invalid_block_columns_and_ragged_edges(torch, itype, kern):
+    """Malformed BCSR for the tile kernels: block columns >= Kb (negative ones
+    with int32 indices, ones with high bits set with int64) contribute
+    nothing, where the reference would read B out of bounds; K = 250 and
+    N = 37 leave ragged last block columns and column tiles.  C against the
+    fp64 product of the same blocks without the bad ones."""
+    p = synth.random_csr(300, 250, 37, 0.05, seed=21, dtype=np.float32)
+    A = X.CSRMatrix.from_host(p.M, p.K, p.rp.astype(itype), p.ci.astype(itype), p.vals)
+    Bm = X.csr_to_bcsr(A)
+    bci = Bm.col_ind.cpu().numpy().copy()
+    rng = np.random.default_rng(5)
+    bad = rng.random(len(bci)) < 0.25
+    Kb = Bm.num_block_cols
+    bci_bad = bci.copy()
+    bci_bad[bad] = Kb + rng.integers(0, 1000, size=int(bad.sum()))
+    alt = bad & (rng.random(len(bci)) < 0.5)
+    if itype == np.int32:
+        bci_bad[alt] = -1 - rng.integers(0, 1 << 20, size=int(alt.sum()))
+    else:
+        bci_bad[alt] = (np.int64(1) << 40) + bci[alt]
+    Bm.col_ind = torch.as_tensor(bci_bad.astype(itype)).cuda()
+    with f32_kernel(kern):
+        C = X.spmm(Bm, torch.as_tensor(p.B).cuda()).cpu().numpy()
+    brp, bci_o, bv = oracle.csr_to_bcsr(p.M, p.K, p.rp, p.ci, p.vals)
+    assert np.array_equal(bci_o, bci)
+    bv = bv.reshape(-1, 256).copy()
+    bv[bad] = 0
+    ref = oracle.bcsr_spmm_f64(p.M, p.K, p.N, brp, bci_o, bv, p.B)
+    e = oracle.errors(C, ref)
+    note(f"tile {kern} {np.dtype(itype).name}: {int(bad.sum())} bad of {len(bci)} blocks, "
+         f"rel_frob {e['rel_frob']:.2e}")
+    assert np.all(np.isfinite(C))
+    assert e["rel_frob"] <= TOL, e
 
 
 def test_batch_is_deterministic_and_linear(torch):
@@ -179,7 +229,7 @@ def test_nonfinite_a_propagates(torch):
     p.vals[int(p.rp[10])] = np.inf
     p.vals[int(p.rp[40]) + 1] = np.nan
     ref = sampled_rows_f64(p, np.arange(p.M))
-    for kern in ("batch", "tile"):
+    for kern in ("batch", "tile", "tile64"):
         C, _ = run_tier1(torch, p, kernel=kern)
         assert np.array_equal(np.isnan(C), np.isnan(ref)), kern
         assert np.array_equal(np.isposinf(C), np.isposinf(ref)), kern
@@ -215,7 +265,7 @@ def test_nonfinite_b_in_a_zero_column(torch, dtype):
     meets only such columns leaves C finite and equal to the product with
     that row zeroed; the reference (spmm_math.hpp:93-110) multiplies every
     block column and turns the 16 rows of that block-row into NaN.  The fp32
-    tile kernel multiplies every block column, as the reference does."""
+    tile kernels multiply every block column, as the reference does."""
     p, Binf = zero_column_block()
     if dtype == np.float16:
         p.vals = p.vals.astype(np.float16)
@@ -228,9 +278,10 @@ def test_nonfinite_b_in_a_zero_column(torch, dtype):
     assert np.all(np.isfinite(C_inf))
     assert np.array_equal(C_inf, C_zero)
     if dtype == np.float32:
-        C_tile, _ = run_tier1(torch, p, kernel="tile", B=Binf)
-        assert np.all(np.isnan(C_tile[0:16]))
-        assert np.all(np.isfinite(C_tile[16:]))
+        for kern in ("tile", "tile64"):
+            C_tile, _ = run_tier1(torch, p, kernel=kern, B=Binf)
+            assert np.all(np.isnan(C_tile[0:16])), kern
+            assert np.all(np.isfinite(C_tile[16:])), kern
 
 
 # ---------------------------------------------------------------------------

@@ -25,9 +25,12 @@
 //                           least 512 workgroups of 128 columns: the non-zero
 //                           block columns of a block-row packed four to a
 //                           K = 4 batch;
-//   spmm_f32_kernel         short grids: lane l loads A[l&15][4g .. 4g+3]
+//   spmm_f32_short_kernel   short grids: lane l loads A[l&15][4g .. 4g+3]
 //                           (g = l>>4) once per block and issues four MFMAs,
-//                           step s pairing A[i][4g+s] with B[16*col + 4g + s][n].
+//                           step s pairing A[i][4g+s] with B[16*col + 4g + s][n]
+//                           (B through a buffer resource);
+//   spmm_f32_kernel         the same with 64-bit B addressing, for short
+//                           grids whose B offsets exceed 30 bits.
 //
 // Work split: one workgroup per block-row (grid.x, or the dispatch order of
 // order_rows_kernel / xcd_rows_kernel), N split over grid.y.
@@ -1399,6 +1402,120 @@ __global__ __launch_bounds__(64 * kF32Waves) void spmm_f32_kernel(const I* __res
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 short-grid kernel where B's byte offsets fit 30 bits (16 * Kb * N * 4
+// <= 2^30): the tile kernel's product with B read through a buffer resource.
+// A lane's B offset within a block's 16 rows is fixed for the kernel, so each
+// B load is one add and one buffer load; an offset past the end of B (rows
+// >= K, columns >= N, invalid block columns) reads zero, so no load needs a
+// branch of its own and every step issues the same loads.  Sixteen waves
+// split a block-row's blocks (wave w: blocks w, w + 16, ...), four blocks'
+// loads in flight per wave; the partial tiles are summed through LDS in wave
+// order.  Every block column multiplies, as in the tile kernel: a non-finite
+// B row makes NaN wherever it meets a block.
+// ---------------------------------------------------------------------------
+constexpr int kF32ShortWaves = 16;
+constexpr int kF32ShortUnroll = 4;
+// an offset part past every in-range offset: in-range parts are below 2^30,
+// so a sum with one or two of these parts stays below 2^32 and past the end
+constexpr uint32_t kF32ShortPast = 1u << 30;
+constexpr int64_t kF32ShortMaxBytes = int64_t(1) << 30;
+
+template <typename I, int NTW>
+__global__ __launch_bounds__(64 * kF32ShortWaves) void spmm_f32_short_kernel(
+    const I* __restrict__ brp, const I* __restrict__ bci, const float* __restrict__ vals,
+    const float* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N, int64_t Kb,
+    int ntiles)
+{
+    constexpr int W = kF32ShortWaves;
+    constexpr int U = kF32ShortUnroll;
+    __shared__ float red[W][16][NTW * 16];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int tile0 = blockIdx.y * NTW;
+    const int64_t br = blockIdx.x;
+    const int64_t rs = brp[br];
+    const int64_t re = brp[br + 1];
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)(K * N * 4));
+    // byte offset of lane (li, g)'s B element at step s, tile t, from the
+    // block's first B row
+    uint32_t loff[NTW][4];
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int64_t n = (int64_t)(tile0 + t) * 16 + li;
+            loff[t][s] = n < N ? (uint32_t)(((4 * g + s) * N + n) * 4) : kF32ShortPast;
+        }
+    const uint32_t rowbytes = (uint32_t)(16 * N * 4);
+
+    float4_t acc[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // U blocks per step, loads first; a block past the row's end loads the
+    // row's last block again and is not multiplied
+    for (int64_t blk = rs + wave; blk < re; blk += (int64_t)U * W) {
+        float4_t a[U];
+        uint32_t base[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t b0 = blk + u * W;
+            const int64_t b = b0 < re ? b0 : re - 1;
+            a[u] = *reinterpret_cast<const float4_t*>(vals + b * 256 + li * 16 + g * 4);
+            const int64_t col = (int64_t)bci[b];
+            base[u] = (col >= 0 && col < Kb) ? (uint32_t)col * rowbytes : kF32ShortPast;
+        }
+        float bv[U][4][NTW];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int t = 0; t < NTW; ++t)
+                    bv[u][s][t] = __builtin_bit_cast(
+                        float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                                   rb, (int)(base[u] + loff[t][s]), 0, 0));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (blk + u * W < re) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int t = 0; t < NTW; ++t)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][s], bv[u][s][t], acc[t],
+                                                                       0, 0, 0);
+            }
+    }
+
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][4 * g + r][16 * j + li] = acc[j][r];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 16 * NTW * 16; o += 64 * W) {
+        const int row = o / (NTW * 16), c = o % (NTW * 16);
+        float sum = red[0][row][c];
+#pragma unroll
+        for (int w = 1; w < W; ++w) sum += red[w][row][c];
+        const int64_t grow = br * 16 + row;
+        const int64_t col = (int64_t)tile0 * 16 + c;
+        if (grow < M && col < N && tile0 + c / 16 < ntiles) C[grow * N + col] = sum;
+    }
+}
+
+// Whether the fp32 short-grid product takes spmm_f32_short_kernel: B's
+// offsets fit its 30-bit range, unless XSPMM_F32_SHORT=off (read on every
+// call, so a process can compare the two kernels).
+bool f32_short_wanted(int64_t Kb, int64_t N)
+{
+    const char* e = std::getenv("XSPMM_F32_SHORT");
+    if (e && std::string(e) == "off") return false;
+    return N > 0 && N <= kF32ShortMaxBytes / 64 && Kb <= kF32ShortMaxBytes / (64 * N);
+}
+
 // Launch geometry: waves per workgroup and 16-column tiles per wave.
 struct Geometry {
     int ntw;
@@ -1717,6 +1834,25 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
         const int64_t gy = (ntiles + ntw - 1) / ntw;
         if (gy > 65535) throw std::invalid_argument("xSpMM: N too large.");
         const dim3 fgrid((unsigned)Mb, (unsigned)gy);
+        if (f32_short_wanted(Kb, N)) {
+            const dim3 sblock(64 * kF32ShortWaves);
+            switch (ntw) {
+            case 4:
+                hipLaunchKernelGGL((spmm_f32_short_kernel<I, 4>), fgrid, sblock, 0, s, brp, bci, v,
+                                   b, C, M, K, N, Kb, ntiles);
+                break;
+            case 2:
+                hipLaunchKernelGGL((spmm_f32_short_kernel<I, 2>), fgrid, sblock, 0, s, brp, bci, v,
+                                   b, C, M, K, N, Kb, ntiles);
+                break;
+            default:
+                hipLaunchKernelGGL((spmm_f32_short_kernel<I, 1>), fgrid, sblock, 0, s, brp, bci, v,
+                                   b, C, M, K, N, Kb, ntiles);
+                break;
+            }
+            XSPMM_LAUNCH_CHECK();
+            return true;
+        }
         const dim3 fblock(64 * kF32Waves);
         switch (ntw) {
         case 4:
