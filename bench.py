@@ -106,9 +106,11 @@ def cpu_baseline(p, N, nnz, seconds):
     }
 
 
-def tier1_kernel(value_bytes, K, N, nnzb, Mb):
+def tier1_kernel(value_bytes, K, N, nnzb, Mb, band=False):
     """Name of the kernel one Tier-1 call launches (the launcher's own rule in
-    xspmm_amd/csrc/spmm.hip: fp16 takes the GEMM-tiled kernel when every block
+    xspmm_amd/csrc/spmm.hip: fp16 takes the band kernel when csr_to_bcsr
+    found contiguous, overlapping block-rows (`band`) and N % 8 == 0 and B
+    fits 32-bit offsets; else the GEMM-tiled kernel when every block
     is present, else the column-batch kernel when N % 8 == 0 and B and the
     block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL selects
     another one; fp32 takes its column-batch kernel when N % 4 == 0 and B
@@ -126,10 +128,12 @@ def tier1_kernel(value_bytes, K, N, nnzb, Mb):
             return "spmm_f32_short_kernel"
         return "spmm_f32_kernel"
     Kb = (K + 15) // 16
+    fits = K * N * 2 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20
+    if band and N % 8 == 0 and fits:
+        return "spmm_f16_band_kernel"
     if (nnzb == Mb * Kb and N % 8 == 0 and Mb * Kb * 512 < 1 << 31 and K * N * 2 < 1 << 31
             and os.environ.get("XSPMM_SPMM_KERNEL", "") == ""):
         return "spmm_f16_dense_kernel"
-    fits = K * N * 2 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20
     choice = os.environ.get("XSPMM_SPMM_KERNEL", "")
     if choice in ("", "batch") and N % 8 == 0 and fits:
         return "spmm_f16_batch_kernel"
@@ -382,7 +386,7 @@ def main():
     eff = 2.0 * nnz * N / t / 1e12
     padded = 2.0 * nnzb * 256 * N / t / 1e12
     mfma_peak = FP16_PEAK_TFLOPS if sT == 2 else FP32_MFMA_PEAK_TFLOPS
-    kernel = tier1_kernel(sT, K, N, nnzb, Mb)
+    kernel = tier1_kernel(sT, K, N, nnzb, Mb, band=sT == 2 and Bm.band_rows())
     # Matrix-core work the kernel executes: the column-batch kernels multiply
     # only the block columns that hold a non-zero entry (32 flops per such
     # column, row and output column: 16 rows x multiply-add), the other

@@ -50,7 +50,7 @@ public:
           num_block_rows_(o.num_block_rows_), num_block_cols_(o.num_block_cols_), num_blocks_(o.num_blocks_),
           r_block_(o.r_block_), c_block_(o.c_block_), num_rows_(o.num_rows_), num_cols_(o.num_cols_),
           bcsr_row_ptr_(o.bcsr_row_ptr_), bcsr_col_ind_(o.bcsr_col_ind_), bcsr_values_(o.bcsr_values_),
-          dispatch_order_(o.dispatch_order_)
+          dispatch_order_(o.dispatch_order_), band_rows_(o.band_rows_)
     {
         o.bcsr_row_ptr_ = nullptr;
         o.bcsr_col_ind_ = nullptr;
@@ -73,6 +73,7 @@ public:
             bcsr_col_ind_ = o.bcsr_col_ind_;
             bcsr_values_ = o.bcsr_values_;
             dispatch_order_ = o.dispatch_order_;
+            band_rows_ = o.band_rows_;
             o.bcsr_row_ptr_ = nullptr;
             o.bcsr_col_ind_ = nullptr;
             o.bcsr_values_ = nullptr;
@@ -121,10 +122,20 @@ public:
         dispatch_order_ = order;
     }
 
+    // Whether Tier-1 (fp16) takes the band kernel for this matrix: every
+    // block-row one contiguous run of block columns, and four neighbouring
+    // block-rows sharing B tiles gather fewer B rows than the column-batch
+    // kernel would.  csr_to_bcsr decides it once per matrix; the band kernel
+    // is only correct on contiguous rows, so set it only from that check.
+    // copy_from_host clears it.
+    bool get_band_rows() const { return band_rows_; }
+    void set_band_rows(bool band) { band_rows_ = band; }
+
     void copy_from_host(const IndexType* host_row_ptr, const IndexType* host_col_ind,
                         const ValueType* host_values)
     {
         free_dispatch_order();
+        band_rows_ = false;
         exec_->copy_from_host(bcsr_row_ptr_, host_row_ptr,
                               (static_cast<size_t>(num_block_rows_) + 1) * sizeof(IndexType));
         if (num_blocks_ > 0) {
@@ -177,6 +188,7 @@ private:
     IndexType* bcsr_col_ind_ = nullptr;
     ValueType* bcsr_values_ = nullptr;
     int32_t* dispatch_order_ = nullptr;
+    bool band_rows_ = false;
 };
 
 }  // namespace xspmm

@@ -259,7 +259,9 @@ def test_spmm_locality_order(torch, case):
     from the block columns -- contiguous block-row ranges per XCD for short,
     alike neighbouring rows (a narrow band) -- and none for unrelated
     neighbours (random dense blocks), long rows (a wide band) or fewer than
-    256 block-rows.  C equals the unordered entry point's bit for bit."""
+    256 block-rows.  C of the ordered call equals the unordered entry point's
+    bit for bit; where the grid takes the band kernel (contiguous block-rows),
+    the Python Tier-1 call equals the band entry point's C."""
     import ctypes as C
     if case == "band":
         p = synth.banded_sweep(0.01, M=8192, N=64)          # 512 block-rows, ~6 blocks each
@@ -283,10 +285,24 @@ def test_spmm_locality_order(torch, case):
     else:
         assert order is None  # the identity (or a short grid): no order passed
     B = dev(torch, np.random.default_rng(3).uniform(-1, 1, (p.K, p.N)).astype(p.vals.dtype))
-    C1 = X.spmm(Bm, B)
     L = X.load()
     ptr = lambda t: C.c_void_p(t.data_ptr())
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    C1 = torch.full((p.M, p.N), float("nan"), dtype=torch.float32, device="cuda")
+    assert L.xspmm_bcsr_spmm_ordered(X.vcode(Bm.values.dtype), X.icode(Bm.row_ptr.dtype), Bm.num_rows,
+                                     Bm.num_cols, Mb, Bm.num_block_cols, Bm.num_blocks,
+                                     ptr(Bm.row_ptr), ptr(Bm.col_ind), ptr(Bm.values), ptr(B), ptr(C1),
+                                     p.N, ptr(order) if order is not None else None, stream) == X.OK
+    if Bm.band_rows():
+        C3 = torch.full((p.M, p.N), float("nan"), dtype=torch.float32, device="cuda")
+        assert L.xspmm_bcsr_spmm_band(X.icode(Bm.row_ptr.dtype), Bm.num_rows, Bm.num_cols, Mb,
+                                      Bm.num_block_cols, Bm.num_blocks, ptr(Bm.row_ptr),
+                                      ptr(Bm.col_ind), ptr(Bm.values), ptr(B), ptr(C3), p.N,
+                                      stream) == X.OK
+        assert torch.equal(X.spmm(Bm, B), C3)
+        check_c(host(C3), host(C1).astype(np.float64), np.float16)
+    else:
+        assert torch.equal(X.spmm(Bm, B), C1)
     C2 = torch.full((p.M, p.N), float("nan"), dtype=torch.float32, device="cuda")
     assert L.xspmm_bcsr_spmm(X.vcode(Bm.values.dtype), X.icode(Bm.row_ptr.dtype), Bm.num_rows,
                              Bm.num_cols, Mb, Bm.num_block_cols, Bm.num_blocks, ptr(Bm.row_ptr),

@@ -67,6 +67,10 @@ def load():
                                           p, p]
     L.xspmm_bcsr_dispatch_order.restype = i32
     L.xspmm_bcsr_dispatch_order.argtypes = [i32, i64, p, p, C.POINTER(C.c_int), p]
+    L.xspmm_bcsr_band_rows.restype = i32
+    L.xspmm_bcsr_band_rows.argtypes = [i32, i64, i64, i64, i64, i64, i64, p, p, C.POINTER(C.c_int), p]
+    L.xspmm_bcsr_spmm_band.restype = i32
+    L.xspmm_bcsr_spmm_band.argtypes = [i32, i64, i64, i64, i64, i64, p, p, p, p, p, i64, p]
     L.xspmm_bcsr_dispatch_order_cols.restype = i32
     L.xspmm_bcsr_dispatch_order_cols.argtypes = [i32, i64, p, p, p, C.POINTER(C.c_int), p]
     L.xspmm_csr_to_bcsr_count.restype = i32
@@ -243,6 +247,13 @@ class BCSRMatrix:
     # from (their identities and versions).
     _order: object = field(default=None, repr=False, compare=False)
     _order_key: object = field(default=None, repr=False, compare=False)
+    # Whether fp16 Tier-1 takes the band kernel (every block-row a contiguous
+    # run of block columns, see xspmm_bcsr_band_rows), decided once for the
+    # same tensors as the order; _nnz: CSR entries behind the grid (0: not
+    # known), which csr_to_bcsr records.
+    _band: object = field(default=None, repr=False, compare=False)
+    _band_key: object = field(default=None, repr=False, compare=False)
+    _nnz: int = field(default=0, repr=False, compare=False)
 
     @property
     def num_blocks(self) -> int:
@@ -266,6 +277,24 @@ class BCSRMatrix:
             self._order = order[:int(self.num_block_rows)] if written.value else None
             self._order_key = key
         return self._order
+
+    def band_rows(self) -> bool:
+        """Whether fp16 Tier-1 multiplies this grid with the band kernel
+        (decided on first use for the current row_ptr and col_ind)."""
+        key = (id(self.row_ptr), self.row_ptr.data_ptr(), self.row_ptr._version,
+               id(self.col_ind), self.col_ind.data_ptr(), self.col_ind._version,
+               int(self.num_block_rows))
+        if self._band_key != key:
+            band = C.c_int(0)
+            if self.r_block == 16 and self.c_block == 16:
+                _check(load().xspmm_bcsr_band_rows(icode(self.row_ptr.dtype), int(self.num_rows),
+                                                   int(self.num_cols), int(self.num_block_rows),
+                                                   int(self.num_block_cols), int(self._nnz),
+                                                   self.num_blocks, _ptr(self.row_ptr),
+                                                   _ptr(self.col_ind), C.byref(band), _stream()))
+            self._band = bool(band.value)
+            self._band_key = key
+        return self._band
 
 
 # ---------------------------------------------------------------------------
@@ -292,8 +321,11 @@ def csr_to_bcsr(A: CSRMatrix, r_block: int = 16, c_block: int = 16) -> BCSRMatri
                                     A.nnz, _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values),
                                     r_block, c_block, _ptr(brp), _ptr(bci), _ptr(bv), _stream()))
     out = BCSRMatrix(Mb, Kb, r_block, c_block, A.num_rows, A.num_cols, brp, bci, bv)
+    out._nnz = int(A.nnz)
     if r_block == 16 and c_block == 16:
         out.dispatch_order()  # once here rather than in every Tier-1 call
+        if A.values.dtype == torch.float16:
+            out.band_rows()
     return out
 
 
@@ -309,6 +341,12 @@ def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
         C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=dev)
     _check_dense(B, "B", A.num_cols, N, A.values.dtype, dev)
     _check_dense(C_out, "C_out", A.num_rows, N, torch.float32, dev)
+    if B.dtype == torch.float16 and A.band_rows():
+        _check(L.xspmm_bcsr_spmm_band(icode(A.row_ptr.dtype), A.num_rows, A.num_cols,
+                                      A.num_block_rows, A.num_block_cols, A.num_blocks,
+                                      _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values), _ptr(B),
+                                      _ptr(C_out), N, _stream()))
+        return C_out
     order = A.dispatch_order()
     _check(L.xspmm_bcsr_spmm_ordered(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows,
                                      A.num_cols, A.num_block_rows, A.num_block_cols, A.num_blocks,

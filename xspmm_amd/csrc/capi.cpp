@@ -173,6 +173,40 @@ int xspmm_bcsr_spmm_ordered(int vtype, int itype, int64_t M, int64_t K, int64_t 
     });
 }
 
+int xspmm_bcsr_band_rows(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnz,
+                         int64_t nnzb, const void* brp, const void* bci, int* band, void* stream)
+{
+    return guarded([&] {
+        if (!band) throw std::invalid_argument("xSpMM: band must not be NULL.");
+        *band = 0;
+        if (M < 0 || K < 0 || Mb < 0 || Kb < 0 || nnzb < 0)
+            throw std::invalid_argument("xSpMM: negative size passed to BCSR SpMM.");
+        if (Mb == 0 || nnzb == 0) return;
+        if (!brp || !bci) throw std::invalid_argument("xSpMM: brp and bci must not be NULL.");
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            *band = spmm_band_wanted<I>(static_cast<const I*>(brp), static_cast<const I*>(bci), M, K, Mb, Kb,
+                                        nnz, nnzb, 0, as_stream(stream))
+                        ? 1
+                        : 0;
+        });
+    });
+}
+
+int xspmm_bcsr_spmm_band(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
+                         const void* brp, const void* bci, const void* bvals, const void* B, float* C,
+                         int64_t N, void* stream)
+{
+    return guarded([&] {
+        with_index(itype, [&](auto ti) {
+            using I = typename decltype(ti)::type;
+            bcsr_spmm_band<I>(M, K, Mb, Kb, nnzb, static_cast<const I*>(brp), static_cast<const I*>(bci),
+                              static_cast<const uint16_t*>(bvals), static_cast<const uint16_t*>(B), C, N,
+                              as_stream(stream));
+        });
+    });
+}
+
 int xspmm_csr_to_bcsr_count(int itype, int64_t M, int64_t K, int64_t nnz, const void* rp,
                             const void* ci, int64_t r_block, int64_t c_block,
                             void* bcsr_row_ptr, int64_t* nnzb_out, void* stream)

@@ -1,0 +1,412 @@
+// spmm_band.hip -- Tier-1 BCSR SpMM (fp16) for grids whose block-rows are
+// contiguous runs of block columns that neighbouring block-rows share: banded
+// and block-banded matrices (the density sweep of the reference's
+// examples/05_core_spmm_benchmark.cpp:56-77 is of this shape).
+//
+// In such a grid the column-batch kernel gathers the same B rows once for
+// every block-row that meets them: at the 90 % band (16384^2, N = 128) that is
+// 3 GB of B rows out of L2 for a 0.4 GB product, and the gathers bound it.
+// Here a workgroup owns four consecutive block-rows (one per wave) and one
+// 128-column chunk of C, and walks the union of their block columns once, in
+// aligned pairs (block columns 2p and 2p + 1, i.e. B rows 32p .. 32p + 31):
+//   * each pair's 32 x 128 B tile is loaded once for the four rows -- each wave
+//     loads 8 of its rows into registers L pairs ahead and writes them into
+//     one of three LDS stages two pairs ahead, so a B row leaves L2 once per
+//     group instead of once per block-row;
+//   * each wave loads its own row's two blocks of the pair straight into the
+//     v_mfma_f32_16x16x32_f16 A operand (one 16-byte load per lane, L pairs
+//     ahead); a block the row does not hold reads as zeros;
+//   * each wave reads the next pair's tile back with the gfx950 transpose
+//     read ds_read_b64_tr_b16 (the B operands of its 8 column tiles) while
+//     this pair's 8 MFMAs run; one s_barrier per pair hands the stages over.
+// A row's block (br, c) sits at index row_ptr[br] + c - col_ind[row_ptr[br]]
+// (the row is contiguous), so no column index is read inside the loop.  The
+// Tier-1 entry points take this kernel only for grids checked to have
+// contiguous rows (spmm_band_wanted); on any other grid every access still
+// stays inside A and B (buffer resources with their sizes), but C would be
+// wrong.
+//
+// Semantics are those of the tile kernel (reference
+// src/common/spmm_math.hpp:20-146): each block a row holds multiplies all 16
+// of its columns, and B rows meet a row only through the blocks it holds (so
+// an Inf/NaN in B gives NaN exactly where the reference's would), fp32
+// accumulators, C overwritten; rows >= M and columns >= N are not stored and
+// B rows >= K contribute nothing.  A row's pairs accumulate in ascending
+// column order, the same order on every call.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+
+#include "internal.hpp"
+
+namespace xspmm {
+namespace detail {
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+constexpr int kBandRows = 4;        // block-rows per workgroup, one per wave
+constexpr int kBandTile = 32 * 256; // LDS stage: 32 B rows x 128 fp16 columns
+constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every resource: reads zeros
+
+#ifndef XSPMM_BAND_DEPTH
+#define XSPMM_BAND_DEPTH 6
+#endif
+static_assert(XSPMM_BAND_DEPTH >= 6 && XSPMM_BAND_DEPTH <= 18, "band ring depth 6 .. 18");
+#ifndef XSPMM_BAND_CW
+#define XSPMM_BAND_CW 128
+#endif
+#ifndef XSPMM_BAND_RPW
+#define XSPMM_BAND_RPW 1
+#endif
+
+constexpr int kRawBufferWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t band_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             kRawBufferWord3);
+}
+
+// swizzle of tile row e (16-byte chunk c of the row is stored at chunk
+// c ^ swz(e)): the 16 rows one transpose read touches spread over all banks
+__device__ __forceinline__ uint32_t band_swz(uint32_t e)
+{
+    return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
+}
+
+// LDS write of the staged B rows and the barrier that publishes them: every
+// LDS access of this wave done, then the workgroup meets.  The memory clobber
+// keeps the compiler from moving LDS accesses across it; outstanding global
+// loads (the ring) stay in flight.
+__device__ __forceinline__ void band_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// CW: columns of C per workgroup (128 or 64); RPW: block-rows per wave (1:
+// each wave one row and all CW columns; 2: each wave two rows and half the
+// columns, so a B operand read from LDS serves two rows).
+template <typename I, int L, int CW, int RPW>
+__global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
+    const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
+    const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
+    int64_t Mb, const I* __restrict__ row_map)
+{
+    static_assert(CW == 128 || CW == 64, "128 or 64 columns per workgroup");
+    static_assert(RPW == 1 || RPW == 2, "one or two block-rows per wave");
+    static_assert(L % 6 == 0, "ring depth a multiple of 6 (ring slot, stage and operand set align)");
+    constexpr int NT = CW / 16 / RPW;   // 16-column tiles per wave
+    constexpr int LB = CW / 64;         // this wave's 1 KB B loads per pair
+    constexpr int CPR = CW / 8;         // 16-byte chunks per B row of the tile
+    constexpr int RPLD = 64 / CPR;      // tile rows per load
+    __shared__ __align__(16) unsigned char stage[3][kBandTile];
+    // 8 rows of a tile, all zero: the transpose reads of a B-operand half
+    // that a row's missing block would multiply come from here
+    __shared__ __align__(16) unsigned char zeros[8 * 256];
+    __shared__ int32_t s_first[kBandRows];
+    __shared__ int32_t s_last[kBandRows];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const int64_t br0 = (int64_t)blockIdx.x * kBandRows;
+    const int64_t n0 = (int64_t)blockIdx.y * CW;
+
+    // first / last block column of the group's rows (wave w reads row w)
+    {
+        const int64_t br = br0 + wave;
+        int32_t first = 0x7fffffff, last = -1;
+        if (br < Mb) {
+            const int64_t rs = (int64_t)brp[br], re = (int64_t)brp[br + 1];
+            if (re > rs) {
+                first = (int32_t)bci[rs];
+                last = (int32_t)bci[re - 1];
+            }
+        }
+        if (lane == 0) {
+            s_first[wave] = first;
+            s_last[wave] = last;
+        }
+    }
+    for (int i = threadIdx.x; i < 8 * 256 / 4; i += 64 * kBandRows) reinterpret_cast<uint32_t*>(zeros)[i] = 0u;
+    __syncthreads();
+    int32_t lo = 0x7fffffff, hi = -1;
+#pragma unroll
+    for (int w = 0; w < kBandRows; ++w) {
+        lo = min(lo, s_first[w]);
+        hi = max(hi, s_last[w]);
+    }
+    // pairs of the group's span (aligned block-column pairs)
+    const int32_t p0 = hi >= 0 ? (lo >> 1) : 0;
+    const int32_t steps = hi >= 0 ? (hi >> 1) - p0 + 1 : 0;
+
+    // this wave's rows (RPW of them) and column slice
+    const int rw0 = RPW == 1 ? wave : 2 * (wave >> 1);
+    const int cs = RPW == 1 ? 0 : (wave & 1);
+    // A of row k: lane (li, g) reads row li, columns 8 (g & 1) .. + 7 of
+    // block 2p + (g >> 1); blocks outside the row read as zeros
+    __amdgpu_buffer_rsrc_t a_rsrc[RPW];
+    int32_t a_rel0[RPW], a_n[RPW], r_rel0[RPW];
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int64_t br = br0 + rw0 + k;
+        int64_t rs = 0, re = 0;
+        if (br < Mb) {
+            rs = (int64_t)brp[br];
+            re = (int64_t)brp[br + 1];
+        }
+        a_n[k] = (int32_t)(re - rs);
+        a_rsrc[k] = band_rsrc(vals + rs * 256, (uint32_t)a_n[k] * 512u);
+        r_rel0[k] = 2 * p0 - s_first[rw0 + k];  // index in the row of block 2 p0 (uniform)
+        a_rel0[k] = r_rel0[k] + (g >> 1);       // this lane's block at pair 0
+    }
+    const uint32_t a_lane = (uint32_t)(li * 32 + (g & 1) * 16);
+    auto a_off = [&](int k, int32_t t) __attribute__((always_inline)) -> uint32_t {
+        const int32_t rel = a_rel0[k] + 2 * t;
+        return (uint32_t)rel < (uint32_t)a_n[k] ? (uint32_t)rel * 512u + a_lane : kOob;
+    };
+
+    // B rows of the tile: load v of this wave moves tile rows
+    // RPLD (LB wave + v) + lane / CPR, chunk lane % CPR (written at chunk
+    // position chunk ^ swz(row)).  Rows past K read as zeros (their offsets
+    // pass the end of B).  A chunk past N (last column chunk, N % CW != 0)
+    // loads the row's last chunk instead: it only meets columns of C that are
+    // not stored.
+    const __amdgpu_buffer_rsrc_t b_rsrc = band_rsrc(B, (uint32_t)(K * N * 2));
+    const uint32_t rowbytes = (uint32_t)(2 * N);
+    uint32_t b_col[LB], b_row0[LB], st_w[LB];
+#pragma unroll
+    for (int v = 0; v < LB; ++v) {
+        const uint32_t e = (uint32_t)(RPLD * (LB * wave + v) + lane / CPR);
+        const uint32_t ch = (uint32_t)(lane % CPR);
+        const int64_t col = n0 + 8 * (int64_t)ch;
+        b_col[v] = (uint32_t)(2 * (col < N ? col : N - 8));
+        b_row0[v] = (uint32_t)(32 * p0) + e;
+        st_w[v] = e * 256u + 16u * (ch ^ band_swz(e));
+    }
+    auto b_off = [&](int32_t t, int v) __attribute__((always_inline)) -> uint32_t {
+        return __umul24(b_row0[v] + 32u * (uint32_t)t, rowbytes) + b_col[v];
+    };
+
+    // transpose-read address of column tile j of the tile: tr_a0 ^ 32 j
+    const uint32_t tr_e0 = (uint32_t)(8 * g + (li >> 2));
+    const uint32_t tr_a0 = (tr_e0 * 256u + 16u * (uint32_t)((li & 3) >> 1) + 8u * (uint32_t)(li & 1)) ^
+                           (band_swz(tr_e0) << 4);
+
+    float4_t acc[RPW][NT];
+#pragma unroll
+    for (int k = 0; k < RPW; ++k)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[k][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // ring of L pairs in flight (A operands and this wave's B rows per pair),
+    // three LDS stages (pair t in stage t % 3) and the B operands of two
+    // pairs (the one being multiplied and the next)
+    half8_t ar[L][RPW];
+    u32x4_t bq[L][LB];
+    half8_t bop[2][NT];
+    auto issue = [&](int slot, int32_t t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < RPW; ++k)
+            ar[slot][k] = __builtin_bit_cast(
+                half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc[k], (int)a_off(k, t), 0, 0));
+#pragma unroll
+        for (int v = 0; v < LB; ++v)
+            bq[slot][v] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)b_off(t, v), 0, 0));
+    };
+    auto put = [&](int slot, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < LB; ++v) *reinterpret_cast<u32x4_t*>(&stage[st][st_w[v]]) = bq[slot][v];
+    };
+    // Operands of pair t (tile in stage st) into operand set o.  With both
+    // of the row's blocks of the pair present (the row's interior) they come
+    // from the tile; otherwise the lanes of the half that a missing block
+    // would multiply (lane group g >= 2 carries block 2p + 1) read the same
+    // positions of `zeros` instead (a row holding neither block adds zeros).
+    // So B rows meet a row only through blocks it holds, as in the
+    // reference's tile product: an Inf or NaN in B gives NaN exactly where a
+    // held block covers it, never through a neighbour's span.  Lane group g's
+    // transpose reads touch tile rows 8g .. 8g + 7 only.
+    static_assert(RPW == 1, "masking the B operands per row needs one row per wave");
+    const uint32_t z_base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)zeros -
+                            (uint32_t)(8 * g * 256);
+    auto fetch = [&](int st, int o, int32_t t) __attribute__((always_inline)) {
+        const int32_t b0 = r_rel0[0] + 2 * t;
+        const bool has0 = (uint32_t)b0 < (uint32_t)a_n[0];
+        const bool has1 = (uint32_t)(b0 + 1) < (uint32_t)a_n[0];
+        const bool keep = (g >= 2) ? has1 : has0;
+        const uint32_t base =
+            keep ? (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)stage[st] : z_base;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t a = base + (tr_a0 ^ (uint32_t)(32 * (cs * NT + j)));
+            typedef __attribute__((address_space(3))) short4_t* lp_t;
+            const short4_t blo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp_t)(uintptr_t)a);
+            const short4_t bhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lp_t)(uintptr_t)(a + 4 * 256));
+            bop[o][j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(blo, bhi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    };
+    auto multiply = [&](int slot, int o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < RPW; ++k)
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                acc[k][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ar[slot][k], bop[o][j], acc[k][j], 0, 0, 0);
+    };
+
+    if (steps > 0) {
+        // prologue: pairs 0 .. L-1 in flight, pairs 0 and 1 in stages 0 and
+        // 1, pair 0's operands read
+#pragma unroll
+        for (int t = 0; t < L; ++t) issue(t, t);
+        put(0, 0);
+        put(1, 1);
+        band_barrier();
+        fetch(0, 0, 0);
+        for (int32_t s0 = 0; s0 < steps; s0 += L) {
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+                const int32_t s = s0 + u;
+                // pair s + 2's rows into the stage pair s - 1 used (its
+                // readers passed the barrier of pair s - 1), pair s's MFMAs
+                // (operands read before the last barrier), pair s + 1's
+                // operands out of its stage (written before the last
+                // barrier) while they run, then pair s + L's loads into the
+                // slot pair s used
+                if (s + 2 < steps) put((u + 2) % L, (u + 2) % 3);
+                if (s < steps) multiply(u, u & 1);
+                asm volatile("" ::: "memory");
+                if (s + 1 < steps) fetch((u + 1) % 3, (u + 1) & 1, s + 1);
+                issue(u, s + L);
+                band_barrier();
+            }
+        }
+    }
+
+    // store: lane (li, g) holds rows 4g .. 4g + 3 of column 16 j + li of
+    // its tiles
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        const int64_t br = br0 + rw0 + k;
+        if (br >= Mb) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t grow = br * 16 + 4 * g + q;
+            if (grow >= M) continue;
+            const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+            const int64_t c0 = n0 + 16 * cs * NT + li;
+            float* dst = C + crow * N + c0;
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                if (c0 + 16 * j < N) dst[16 * j] = acc[k][j][q];
+        }
+    }
+}
+
+// One thread per group of kBandRows block-rows: counts the block-rows that
+// are not one contiguous run of block columns, and adds the group's span in
+// aligned pairs (the pairs the band kernel walks for it).
+template <typename I>
+__global__ __launch_bounds__(256) void band_analyse_kernel(const I* __restrict__ brp,
+                                                           const I* __restrict__ bci, int64_t Mb,
+                                                           unsigned long long* __restrict__ out)
+{
+    const int64_t grp = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    unsigned long long gaps = 0, span = 0;
+    if (grp * kBandRows < Mb) {
+        int64_t lo = INT64_MAX, hi = -1;
+        for (int w = 0; w < kBandRows; ++w) {
+            const int64_t br = grp * kBandRows + w;
+            if (br >= Mb) break;
+            const int64_t rs = (int64_t)brp[br], re = (int64_t)brp[br + 1];
+            if (re <= rs) continue;
+            const int64_t first = (int64_t)bci[rs], last = (int64_t)bci[re - 1];
+            if (last - first + 1 != re - rs) ++gaps;
+            lo = min(lo, first);
+            hi = max(hi, last);
+        }
+        if (hi >= 0) span = (unsigned long long)((hi >> 1) - (lo >> 1) + 1);
+    }
+    // one atomic per wave and counter
+    for (int o = 32; o > 0; o >>= 1) {
+        gaps += __shfl_down(gaps, o);
+        span += __shfl_down(span, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        if (gaps) atomicAdd(&out[0], gaps);
+        if (span) atomicAdd(&out[1], span);
+    }
+}
+
+}  // namespace
+
+template <typename I>
+bool spmm_band_wanted(const I* brp, const I* bci, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
+                      int64_t nnz, int64_t nnzb, int64_t N, hipStream_t s)
+{
+    (void)M;
+    if (Mb < 1 || nnzb < 1 || !spmm_band_f16_covers(K, Kb, Mb, N > 0 ? N : 128)) return false;
+    if (nnzb == Mb * Kb) return false;  // every block present: the GEMM-tiled kernel's grid
+    // a kernel forced by the diagnostic switch XSPMM_SPMM_KERNEL keeps its grids
+    if (const char* e = std::getenv("XSPMM_SPMM_KERNEL"); e && *e) return false;
+    Scratch counters(2 * sizeof(unsigned long long), s);
+    XSPMM_HIP_CHECK(hipMemsetAsync(counters.get(), 0, 2 * sizeof(unsigned long long), s));
+    const int64_t groups = (Mb + kBandRows - 1) / kBandRows;
+    hipLaunchKernelGGL((band_analyse_kernel<I>), dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s,
+                       brp, bci, Mb, counters.as<unsigned long long>());
+    XSPMM_LAUNCH_CHECK();
+    unsigned long long h[2] = {0, 0};
+    XSPMM_HIP_CHECK(hipMemcpyAsync(h, counters.get(), sizeof(h), hipMemcpyDeviceToHost, s));
+    XSPMM_HIP_CHECK(hipStreamSynchronize(s));
+    if (h[0] != 0) return false;  // a block-row with a gap: the kernel needs contiguous rows
+    // B rows each kernel gathers per 128 columns: the band kernel 32 per pair
+    // of a group's span; the column-batch kernel one per non-zero column of
+    // each block (estimated for entries spread evenly over the blocks; all
+    // 16 when the entry count is not known)
+    const double f = nnz > 0 ? std::min(1.0, (double)nnz / (256.0 * (double)nnzb)) : 1.0;
+    const double batch_rows = (double)nnzb * 16.0 * (1.0 - std::pow(1.0 - f, 16.0));
+    return 32.0 * (double)h[1] <= batch_rows;
+}
+
+template bool spmm_band_wanted<int32_t>(const int32_t*, const int32_t*, int64_t, int64_t, int64_t,
+                                        int64_t, int64_t, int64_t, int64_t, hipStream_t);
+template bool spmm_band_wanted<int64_t>(const int64_t*, const int64_t*, int64_t, int64_t, int64_t,
+                                        int64_t, int64_t, int64_t, int64_t, hipStream_t);
+
+bool spmm_band_f16_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N)
+{
+    return Mb > 0 && N > 0 && N % 8 == 0 && K * N * 2 <= (int64_t(1) << 31) &&
+           N < (int64_t(1) << 22) && Kb < (int64_t(1) << 20) && (N + 63) / 64 <= 65535;
+}
+
+template <typename I>
+bool bcsr_spmm_band_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                        const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,
+                        const I* row_map, hipStream_t s)
+{
+    if (!spmm_band_f16_covers(K, Kb, Mb, N)) return false;
+    constexpr int CW = XSPMM_BAND_CW;
+    const dim3 grid((unsigned)((Mb + kBandRows - 1) / kBandRows), (unsigned)((N + CW - 1) / CW));
+    hipLaunchKernelGGL((spmm_f16_band_kernel<I, XSPMM_BAND_DEPTH, CW, XSPMM_BAND_RPW>), grid,
+                       dim3(64 * kBandRows), 0, s, brp, bci, bvals, B, C, M, K, N, Mb, row_map);
+    XSPMM_LAUNCH_CHECK();
+    return true;
+}
+
+template bool bcsr_spmm_band_f16<int32_t>(int64_t, int64_t, int64_t, int64_t, const int32_t*,
+                                          const int32_t*, const uint16_t*, const uint16_t*, float*,
+                                          int64_t, const int32_t*, hipStream_t);
+template bool bcsr_spmm_band_f16<int64_t>(int64_t, int64_t, int64_t, int64_t, const int64_t*,
+                                          const int64_t*, const uint16_t*, const uint16_t*, float*,
+                                          int64_t, const int64_t*, hipStream_t);
+
+}  // namespace detail
+}  // namespace xspmm
