@@ -6,19 +6,25 @@
 // In such a grid the column-batch kernel gathers the same B rows once for
 // every block-row that meets them: at the 90 % band (16384^2, N = 128) that is
 // 3 GB of B rows out of L2 for a 0.4 GB product, and the gathers bound it.
-// Here a workgroup owns four consecutive block-rows (one per wave) and one
+// Here a workgroup owns four consecutive block-rows (a group) and one
 // 128-column chunk of C, and walks the union of their block columns once, in
-// aligned pairs (block columns 2p and 2p + 1, i.e. B rows 32p .. 32p + 31):
+// aligned pairs (block columns 2p and 2p + 1, i.e. B rows 32p .. 32p + 31).
+// Eight waves, two per block-row, each with 64 of the columns (two waves per
+// SIMD, so one hides the other's waits):
 //   * each pair's 32 x 128 B tile is loaded once for the four rows -- each wave
-//     loads 8 of its rows into registers L pairs ahead and writes them into
+//     loads 4 of its rows into registers L pairs ahead and writes them into
 //     one of three LDS stages two pairs ahead, so a B row leaves L2 once per
 //     group instead of once per block-row;
-//   * each wave loads its own row's two blocks of the pair straight into the
+//   * each wave loads its row's two blocks of the pair straight into the
 //     v_mfma_f32_16x16x32_f16 A operand (one 16-byte load per lane, L pairs
 //     ahead); a block the row does not hold reads as zeros;
 //   * each wave reads the next pair's tile back with the gfx950 transpose
-//     read ds_read_b64_tr_b16 (the B operands of its 8 column tiles) while
-//     this pair's 8 MFMAs run; one s_barrier per pair hands the stages over.
+//     read ds_read_b64_tr_b16 (the B operands of its 4 column tiles) while
+//     this pair's 4 MFMAs run; one s_barrier per pair hands the stages over,
+//     waiting only for the wave's LDS writes (its reads stay in flight);
+//   * XCD x (workgroups go to the 8 XCDs round-robin) takes a contiguous range
+//     of groups, so neighbouring groups, which walk the same B tiles a few
+//     pairs apart, meet them in one L2.
 // A row's block (br, c) sits at index row_ptr[br] + c - col_ind[row_ptr[br]]
 // (the row is contiguous), so no column index is read inside the loop.  The
 // Tier-1 entry points take this kernel only for grids checked to have
@@ -51,7 +57,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-constexpr int kBandRows = 4;        // block-rows per workgroup, one per wave
+constexpr int kBandRows = 4;        // block-rows per workgroup (a group)
 constexpr int kBandTile = 32 * 256; // LDS stage: 32 B rows x 128 fp16 columns
 constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every resource: reads zeros
 
@@ -59,11 +65,12 @@ constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every resource: 
 #define XSPMM_BAND_DEPTH 6
 #endif
 static_assert(XSPMM_BAND_DEPTH >= 6 && XSPMM_BAND_DEPTH <= 18, "band ring depth 6 .. 18");
-#ifndef XSPMM_BAND_CW
-#define XSPMM_BAND_CW 128
+#ifndef XSPMM_BAND_XCD
+#define XSPMM_BAND_XCD 1
 #endif
-#ifndef XSPMM_BAND_RPW
-#define XSPMM_BAND_RPW 1
+constexpr bool kBandXcd = XSPMM_BAND_XCD != 0;
+#ifndef XSPMM_BAND_WPR
+#define XSPMM_BAND_WPR 2
 #endif
 
 constexpr int kRawBufferWord3 = 0x00020000;
@@ -80,31 +87,38 @@ __device__ __forceinline__ uint32_t band_swz(uint32_t e)
     return 2u * ((e & 3u) | (((e >> 3) & 1u) << 2));
 }
 
-// LDS write of the staged B rows and the barrier that publishes them: every
-// LDS access of this wave done, then the workgroup meets.  The memory clobber
-// keeps the compiler from moving LDS accesses across it; outstanding global
-// loads (the ring) stay in flight.
+// The barrier that publishes a wave's LDS writes: every LDS access of this
+// wave done, then the workgroup meets.  The memory clobber keeps the compiler
+// from moving LDS accesses across it; outstanding global loads (the ring)
+// stay in flight.
 __device__ __forceinline__ void band_barrier()
 {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+// The same when this wave issued its LDS writes before R >= 1 LDS reads (LDS
+// operations of a wave complete in order): the writes are done once at most R
+// operations are outstanding, and the reads may stay in flight across the
+// barrier (their consumers wait for them).
+template <int R>
+__device__ __forceinline__ void band_barrier_writes()
+{
+    static_assert(R >= 1 && R <= 15, "lgkmcnt holds 0 .. 15");
+    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(R) : "memory");
+}
 
-// CW: columns of C per workgroup (128 or 64); RPW: block-rows per wave (1:
-// each wave one row and all CW columns; 2: each wave two rows and half the
-// columns, so a B operand read from LDS serves two rows).
-template <typename I, int L, int CW, int RPW>
-__global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
+// WPR: waves per block-row (1: a wave owns its row's 128 columns; 2: two
+// waves split them, 8 waves per workgroup, two per SIMD).
+template <typename I, int L, int WPR>
+__global__ __launch_bounds__(64 * kBandRows * WPR) void spmm_f16_band_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
     int64_t Mb, const I* __restrict__ row_map)
 {
-    static_assert(CW == 128 || CW == 64, "128 or 64 columns per workgroup");
-    static_assert(RPW == 1 || RPW == 2, "one or two block-rows per wave");
+    static_assert(WPR == 1 || WPR == 2, "one or two waves per block-row");
     static_assert(L % 6 == 0, "ring depth a multiple of 6 (ring slot, stage and operand set align)");
-    constexpr int NT = CW / 16 / RPW;   // 16-column tiles per wave
-    constexpr int LB = CW / 64;         // this wave's 1 KB B loads per pair
-    constexpr int CPR = CW / 8;         // 16-byte chunks per B row of the tile
-    constexpr int RPLD = 64 / CPR;      // tile rows per load
+    constexpr int W = kBandRows * WPR;  // waves per workgroup
+    constexpr int NT = 8 / WPR;         // 16-column tiles per wave
+    constexpr int LB = 8 / W;           // this wave's 1 KB B loads per pair (8 per tile)
     __shared__ __align__(16) unsigned char stage[3][kBandTile];
     // 8 rows of a tile, all zero: the transpose reads of a B-operand half
     // that a row's missing block would multiply come from here
@@ -116,26 +130,31 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 15;
     const int g = lane >> 4;
-    const int64_t br0 = (int64_t)blockIdx.x * kBandRows;
-    const int64_t n0 = (int64_t)blockIdx.y * CW;
+    const int row = wave % kBandRows;  // this wave's block-row in the group
+    const int cs = wave / kBandRows;   // and its column slice (16 NT columns)
+    // group of this workgroup: workgroups go to the 8 XCDs round-robin, and
+    // XCD x takes a contiguous range of groups (start x * (G / 8) +
+    // min(x, G % 8)), so neighbouring groups, which walk the same B tiles a
+    // few pairs apart, meet them in one L2
+    const uint32_t G = gridDim.x;
+    const uint32_t x8 = blockIdx.x & 7u;
+    const uint32_t grp = kBandXcd ? x8 * (G >> 3) + min(x8, G & 7u) + (blockIdx.x >> 3) : blockIdx.x;
+    const int64_t br0 = (int64_t)grp * kBandRows;
+    const int64_t n0 = (int64_t)blockIdx.y * 128;
 
-    // first / last block column of the group's rows (wave w reads row w)
-    {
-        const int64_t br = br0 + wave;
-        int32_t first = 0x7fffffff, last = -1;
-        if (br < Mb) {
-            const int64_t rs = (int64_t)brp[br], re = (int64_t)brp[br + 1];
-            if (re > rs) {
-                first = (int32_t)bci[rs];
-                last = (int32_t)bci[re - 1];
-            }
-        }
-        if (lane == 0) {
-            s_first[wave] = first;
-            s_last[wave] = last;
-        }
+    // this wave's row: its blocks, and first / last block column
+    const int64_t br = br0 + row;
+    int64_t rs = 0, re = 0;
+    if (br < Mb) {
+        rs = (int64_t)brp[br];
+        re = (int64_t)brp[br + 1];
     }
-    for (int i = threadIdx.x; i < 8 * 256 / 4; i += 64 * kBandRows) reinterpret_cast<uint32_t*>(zeros)[i] = 0u;
+    const int32_t nblk = (int32_t)(re - rs);
+    if (cs == 0 && lane == 0) {
+        s_first[row] = nblk > 0 ? (int32_t)bci[rs] : 0x7fffffff;
+        s_last[row] = nblk > 0 ? (int32_t)bci[re - 1] : -1;
+    }
+    for (int i = threadIdx.x; i < 8 * 256 / 4; i += 64 * W) reinterpret_cast<uint32_t*>(zeros)[i] = 0u;
     __syncthreads();
     int32_t lo = 0x7fffffff, hi = -1;
 #pragma unroll
@@ -147,45 +166,30 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
     const int32_t p0 = hi >= 0 ? (lo >> 1) : 0;
     const int32_t steps = hi >= 0 ? (hi >> 1) - p0 + 1 : 0;
 
-    // this wave's rows (RPW of them) and column slice
-    const int rw0 = RPW == 1 ? wave : 2 * (wave >> 1);
-    const int cs = RPW == 1 ? 0 : (wave & 1);
-    // A of row k: lane (li, g) reads row li, columns 8 (g & 1) .. + 7 of
+    // A of the row: lane (li, g) reads row li, columns 8 (g & 1) .. + 7 of
     // block 2p + (g >> 1); blocks outside the row read as zeros
-    __amdgpu_buffer_rsrc_t a_rsrc[RPW];
-    int32_t a_rel0[RPW], a_n[RPW], r_rel0[RPW];
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) {
-        const int64_t br = br0 + rw0 + k;
-        int64_t rs = 0, re = 0;
-        if (br < Mb) {
-            rs = (int64_t)brp[br];
-            re = (int64_t)brp[br + 1];
-        }
-        a_n[k] = (int32_t)(re - rs);
-        a_rsrc[k] = band_rsrc(vals + rs * 256, (uint32_t)a_n[k] * 512u);
-        r_rel0[k] = 2 * p0 - s_first[rw0 + k];  // index in the row of block 2 p0 (uniform)
-        a_rel0[k] = r_rel0[k] + (g >> 1);       // this lane's block at pair 0
-    }
+    const __amdgpu_buffer_rsrc_t a_rsrc = band_rsrc(vals + rs * 256, (uint32_t)nblk * 512u);
+    const int32_t r_rel0 = 2 * p0 - s_first[row];  // index in the row of block 2 p0 (uniform)
+    const int32_t a_rel0 = r_rel0 + (g >> 1);       // this lane's block at pair 0
     const uint32_t a_lane = (uint32_t)(li * 32 + (g & 1) * 16);
-    auto a_off = [&](int k, int32_t t) __attribute__((always_inline)) -> uint32_t {
-        const int32_t rel = a_rel0[k] + 2 * t;
-        return (uint32_t)rel < (uint32_t)a_n[k] ? (uint32_t)rel * 512u + a_lane : kOob;
+    auto a_off = [&](int32_t t) __attribute__((always_inline)) -> uint32_t {
+        const int32_t rel = a_rel0 + 2 * t;
+        return (uint32_t)rel < (uint32_t)nblk ? (uint32_t)rel * 512u + a_lane : kOob;
     };
 
     // B rows of the tile: load v of this wave moves tile rows
-    // RPLD (LB wave + v) + lane / CPR, chunk lane % CPR (written at chunk
-    // position chunk ^ swz(row)).  Rows past K read as zeros (their offsets
-    // pass the end of B).  A chunk past N (last column chunk, N % CW != 0)
-    // loads the row's last chunk instead: it only meets columns of C that are
-    // not stored.
+    // 4 (LB wave + v) + lane / 16, chunk lane % 16 (written at chunk position
+    // chunk ^ swz(row)).  Rows past K read as zeros (their offsets pass the
+    // end of B).  A chunk past N (last column chunk, N % 128 != 0) loads the
+    // row's last chunk instead: it only meets columns of C that are not
+    // stored.
     const __amdgpu_buffer_rsrc_t b_rsrc = band_rsrc(B, (uint32_t)(K * N * 2));
     const uint32_t rowbytes = (uint32_t)(2 * N);
     uint32_t b_col[LB], b_row0[LB], st_w[LB];
 #pragma unroll
     for (int v = 0; v < LB; ++v) {
-        const uint32_t e = (uint32_t)(RPLD * (LB * wave + v) + lane / CPR);
-        const uint32_t ch = (uint32_t)(lane % CPR);
+        const uint32_t e = (uint32_t)(4 * (LB * wave + v) + (lane >> 4));
+        const uint32_t ch = (uint32_t)(lane & 15);
         const int64_t col = n0 + 8 * (int64_t)ch;
         b_col[v] = (uint32_t)(2 * (col < N ? col : N - 8));
         b_row0[v] = (uint32_t)(32 * p0) + e;
@@ -200,23 +204,18 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
     const uint32_t tr_a0 = (tr_e0 * 256u + 16u * (uint32_t)((li & 3) >> 1) + 8u * (uint32_t)(li & 1)) ^
                            (band_swz(tr_e0) << 4);
 
-    float4_t acc[RPW][NT];
+    float4_t acc[NT];
 #pragma unroll
-    for (int k = 0; k < RPW; ++k)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) acc[k][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // ring of L pairs in flight (A operands and this wave's B rows per pair),
+    // ring of L pairs in flight (A operand and this wave's B rows per pair),
     // three LDS stages (pair t in stage t % 3) and the B operands of two
     // pairs (the one being multiplied and the next)
-    half8_t ar[L][RPW];
+    half8_t ar[L];
     u32x4_t bq[L][LB];
     half8_t bop[2][NT];
     auto issue = [&](int slot, int32_t t) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < RPW; ++k)
-            ar[slot][k] = __builtin_bit_cast(
-                half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc[k], (int)a_off(k, t), 0, 0));
+        ar[slot] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (int)a_off(t), 0, 0));
 #pragma unroll
         for (int v = 0; v < LB; ++v)
             bq[slot][v] = __builtin_bit_cast(
@@ -235,13 +234,12 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
     // reference's tile product: an Inf or NaN in B gives NaN exactly where a
     // held block covers it, never through a neighbour's span.  Lane group g's
     // transpose reads touch tile rows 8g .. 8g + 7 only.
-    static_assert(RPW == 1, "masking the B operands per row needs one row per wave");
     const uint32_t z_base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)zeros -
                             (uint32_t)(8 * g * 256);
     auto fetch = [&](int st, int o, int32_t t) __attribute__((always_inline)) {
-        const int32_t b0 = r_rel0[0] + 2 * t;
-        const bool has0 = (uint32_t)b0 < (uint32_t)a_n[0];
-        const bool has1 = (uint32_t)(b0 + 1) < (uint32_t)a_n[0];
+        const int32_t b0 = r_rel0 + 2 * t;
+        const bool has0 = (uint32_t)b0 < (uint32_t)nblk;
+        const bool has1 = (uint32_t)(b0 + 1) < (uint32_t)nblk;
         const bool keep = (g >= 2) ? has1 : has0;
         const uint32_t base =
             keep ? (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)stage[st] : z_base;
@@ -256,10 +254,8 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
     };
     auto multiply = [&](int slot, int o) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < RPW; ++k)
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-                acc[k][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ar[slot][k], bop[o][j], acc[k][j], 0, 0, 0);
+        for (int j = 0; j < NT; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ar[slot], bop[o][j], acc[j], 0, 0, 0);
     };
 
     if (steps > 0) {
@@ -286,17 +282,17 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
                 asm volatile("" ::: "memory");
                 if (s + 1 < steps) fetch((u + 1) % 3, (u + 1) & 1, s + 1);
                 issue(u, s + L);
-                band_barrier();
+                // pair s + 2's writes (when made, pair s + 1's 2 NT reads
+                // follow them) must land before the barrier; pair s + 1's
+                // reads are consumed by its MFMAs before the next barrier
+                band_barrier_writes<2 * NT < 15 ? 2 * NT : 14>();
             }
         }
     }
 
     // store: lane (li, g) holds rows 4g .. 4g + 3 of column 16 j + li of
-    // its tiles
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) {
-        const int64_t br = br0 + rw0 + k;
-        if (br >= Mb) continue;
+    // the wave's tiles
+    if (br < Mb) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int64_t grow = br * 16 + 4 * g + q;
@@ -306,7 +302,7 @@ __global__ __launch_bounds__(64 * kBandRows) void spmm_f16_band_kernel(
             float* dst = C + crow * N + c0;
 #pragma unroll
             for (int j = 0; j < NT; ++j)
-                if (c0 + 16 * j < N) dst[16 * j] = acc[k][j][q];
+                if (c0 + 16 * j < N) dst[16 * j] = acc[j][q];
         }
     }
 }
@@ -384,7 +380,7 @@ template bool spmm_band_wanted<int64_t>(const int64_t*, const int64_t*, int64_t,
 bool spmm_band_f16_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N)
 {
     return Mb > 0 && N > 0 && N % 8 == 0 && K * N * 2 <= (int64_t(1) << 31) &&
-           N < (int64_t(1) << 22) && Kb < (int64_t(1) << 20) && (N + 63) / 64 <= 65535;
+           N < (int64_t(1) << 22) && Kb < (int64_t(1) << 20) && (N + 127) / 128 <= 65535;
 }
 
 template <typename I>
@@ -393,10 +389,10 @@ bool bcsr_spmm_band_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
                         const I* row_map, hipStream_t s)
 {
     if (!spmm_band_f16_covers(K, Kb, Mb, N)) return false;
-    constexpr int CW = XSPMM_BAND_CW;
-    const dim3 grid((unsigned)((Mb + kBandRows - 1) / kBandRows), (unsigned)((N + CW - 1) / CW));
-    hipLaunchKernelGGL((spmm_f16_band_kernel<I, XSPMM_BAND_DEPTH, CW, XSPMM_BAND_RPW>), grid,
-                       dim3(64 * kBandRows), 0, s, brp, bci, bvals, B, C, M, K, N, Mb, row_map);
+    const dim3 grid((unsigned)((Mb + kBandRows - 1) / kBandRows), (unsigned)((N + 127) / 128));
+    hipLaunchKernelGGL((spmm_f16_band_kernel<I, XSPMM_BAND_DEPTH, XSPMM_BAND_WPR>), grid,
+                       dim3(64 * kBandRows * XSPMM_BAND_WPR), 0, s, brp, bci, bvals, B, C, M, K, N, Mb,
+                       row_map);
     XSPMM_LAUNCH_CHECK();
     return true;
 }
