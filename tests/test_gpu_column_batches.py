@@ -220,3 +220,57 @@ def test_batch_invalid_block_columns_contribute_nothing(torch, itype):
                 c = bci[k]
                 Dg[16 * i:16 * i + 16, 16 * c:16 * c + 16] = 0
     assert np.array_equal(C.astype(np.float64), Dg @ B.astype(np.float64))
+
+
+XCD_CHILD = r"""
+import hashlib, json, sys
+import numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import xspmm_amd as X
+out = {}
+for Mb, N in ((64, 256), (64, 200), (66, 256)):
+    rng = np.random.default_rng(Mb + N)
+    Kb = 96
+    D = np.zeros((16 * Mb, 16 * Kb), np.float16)
+    for b in range(Mb):
+        for c in np.nonzero(rng.random(Kb) < 0.2)[0]:
+            D[16 * b:16 * b + 16, 16 * c:16 * c + 16] = rng.integers(-3, 4, size=(16, 16))
+    nzr, nzc = np.nonzero(D)
+    rp = np.concatenate([[0], np.cumsum(np.bincount(nzr, minlength=16 * Mb))]).astype(np.int32)
+    A = X.CSRMatrix.from_host(16 * Mb, 16 * Kb, rp, nzc.astype(np.int32), D[nzr, nzc])
+    Bm = X.csr_to_bcsr(A)
+    B = rng.integers(-4, 5, size=(16 * Kb, N)).astype(np.float16)
+    C = X.spmm(Bm, torch.as_tensor(B).cuda(), N=N).cpu().numpy()
+    ref = D.astype(np.float64) @ B.astype(np.float64)
+    out[f"{Mb}x{N}"] = {"exact": bool(np.array_equal(C.astype(np.float64), ref)),
+                        "sha256": hashlib.sha256(C.tobytes()).hexdigest()}
+print(json.dumps(out))
+"""
+
+
+def test_batch_two_chunks_on_xcd_halves():
+    """Grids of two 128-column chunks with Mb % 4 == 0 (configs[1]'s shape)
+    put each chunk on its own half of the XCDs (workgroup l runs chunk
+    (l / 4) % 2 of block-row 4 (l / 8) + l % 4).  Exact small-integer products
+    with the mapping (default) and without it (XSPMM_BATCH_XCD=off, read once
+    per process, so each runs in its own process), bit-identical C; Mb = 66
+    keeps the plain grid either way."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+    res = {}
+    for mode in ("on", "off"):
+        env = dict(os.environ)
+        env.pop("XSPMM_BATCH_XCD", None)
+        if mode == "off":
+            env["XSPMM_BATCH_XCD"] = "off"
+        note(f"two-chunk grids, XCD halves {mode}")
+        r = subprocess.run([sys.executable, "-c", XCD_CHILD, root], env=env, capture_output=True,
+                           text=True, timeout=180)
+        assert r.returncode == 0, r.stderr[-2000:]
+        res[mode] = json.loads(r.stdout.strip().splitlines()[-1])
+    for k in res["on"]:
+        assert res["on"][k]["exact"] and res["off"][k]["exact"], k
+        assert res["on"][k]["sha256"] == res["off"][k]["sha256"], k

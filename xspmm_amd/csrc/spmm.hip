@@ -724,7 +724,12 @@ __device__ __forceinline__ constexpr uint32_t kslot(uint32_t k)
 // chunk's accumulators, B rows and LDS tile, and two workgroups fit a CU.
 // (HIP's second __launch_bounds__ argument is the minimum number of waves per
 // SIMD: kBW for four resident workgroups per CU, kBW / 2 for two.)
-template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply, int NC = 1>
+//
+// XM (two 128-column chunks, Mb % 4 == 0, grid (2 Mb, 1)): workgroup l runs
+// chunk (l / 4) % 2 of block-row 4 (l / 8) + l % 4, so (workgroups going to
+// the 8 XCDs round-robin) XCDs 0-3 take the first chunk and XCDs 4-7 the
+// second, and each XCD's L2 holds half of B's columns instead of all of them.
+template <typename I, int NT, BatchMode MODE = BatchMode::kMultiply, int NC = 1, bool XM = false>
 __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_batch_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N,
@@ -757,11 +762,15 @@ __global__ __launch_bounds__(64 * kBW, NC == 1 ? kBW : kBW / 2) void spmm_f16_ba
         return c == 0 ? W : W + kBatchWaveLds + (c - 1) * kBtBytes;
     };
 
-    const int64_t br = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+    static_assert(!XM || (NC == 1 && NT == 8 && MODE == BatchMode::kMultiply), "XCD chunk map: two 128-column chunks");
+    const uint32_t bx = XM ? (((blockIdx.x >> 3) << 2) | (blockIdx.x & 3u)) : blockIdx.x;
+    const uint32_t by = XM ? ((blockIdx.x >> 2) & 1u) : blockIdx.y;
+    const uint32_t rows = XM ? (gridDim.x >> 1) : gridDim.x;
+    const int64_t br = order ? (int64_t)order[bx] : (int64_t)bx;
     // a caller-supplied order holds a permutation of the block-rows; an id
     // outside the grid is skipped rather than read past row_ptr
-    if ((uint64_t)br >= (uint64_t)gridDim.x) return;
-    const int64_t n0 = (int64_t)blockIdx.y * 128 * NC;
+    if ((uint64_t)br >= (uint64_t)rows) return;
+    const int64_t n0 = (int64_t)by * 128 * NC;
     const int64_t rs = brp[br];
     const int64_t re = brp[br + 1];
     const int64_t npairs = (re - rs + 1) >> 1;
@@ -1559,6 +1568,17 @@ Fp16Kernel fp16_kernel_choice()
 // chunks, the headline matrix at N = 256 1.43x faster).  XSPMM_BATCH_WIDE=on
 // or off forces the choice; C is the same either way.  Read on every call,
 // so a process can compare the two.
+// Whether a grid of two 128-column chunks puts each chunk on its own half of
+// the XCDs (XSPMM_BATCH_XCD=off keeps both chunks of a block-row on one XCD).
+bool batch_xcd_chunks()
+{
+    static const bool on = [] {
+        const char* e = std::getenv("XSPMM_BATCH_XCD");
+        return !(e && std::string(e) == "off");
+    }();
+    return on;
+}
+
 bool wide_batches(int64_t Mb, int64_t N)
 {
     const char* e = std::getenv("XSPMM_BATCH_WIDE");
@@ -1765,6 +1785,10 @@ bool bcsr_spmm_launch(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb
             else if (N <= 64)
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 4>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
+            else if (chunks == 2 && Mb % 4 == 0 && !wide_batches(Mb, N) && batch_xcd_chunks())
+                hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8, BatchMode::kMultiply, 1, true>),
+                                   dim3((unsigned)(2 * Mb), 1), dim3(64 * kBW), 0, s, brp, bci, v, b, C, M,
+                                   K, N, Kb, order, row_map, BatchPack{});
             else if (N <= 128 || !wide_batches(Mb, N))
                 hipLaunchKernelGGL((spmm_f16_batch_kernel<I, 8>), ggrid, dim3(64 * kBW), 0, s, brp, bci,
                                    v, b, C, M, K, N, Kb, order, row_map, BatchPack{});
