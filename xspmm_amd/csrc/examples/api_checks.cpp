@@ -86,6 +86,36 @@ HostCsr<I> banded(I M, I bw, unsigned seed)
     return h;
 }
 
+// The banded shape with one extra column per row, far from the band: every
+// block-row then has a gap, so Tier-1 keeps the column-batch kernel.
+template <typename I>
+HostCsr<I> banded_gap(I M, I bw, unsigned seed)
+{
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> u(0.1f, 1.0f);
+    HostCsr<I> h;
+    h.M = h.K = M;
+    h.rp.push_back(0);
+    for (I i = 0; i < M; ++i) {
+        const I lo = std::max<I>(0, i - bw), hi = std::min<I>(M - 1, i + bw);
+        const I far = (I)((i + M / 2) % M);
+        if (far < lo) {
+            h.ci.push_back(far);
+            h.vals.push_back(u(rng));
+        }
+        for (I j = lo; j <= hi; ++j) {
+            h.ci.push_back(j);
+            h.vals.push_back(u(rng));
+        }
+        if (far > hi) {
+            h.ci.push_back(far);
+            h.vals.push_back(u(rng));
+        }
+        h.rp.push_back((I)h.ci.size());
+    }
+    return h;
+}
+
 template <typename I>
 std::vector<double> row_sums(const HostCsr<I>& h)
 {
@@ -244,11 +274,11 @@ template <typename I>
 void check_dispatch_order(std::shared_ptr<const xspmm::Executor> ex, const char* tname)
 {
     const I M = 40000, N = 64;
-    auto h = banded<I>(M, 20, 5);
+    auto h = banded_gap<I>(M, 20, 5);
     std::vector<__half> hv;
     auto A = upload<__half, I>(ex, h, hv);
     auto Ab = xspmm::csr_to_bcsr(ex, A, (I)16, (I)16);
-    bool ok = Ab.get_dispatch_order() != nullptr;
+    bool ok = Ab.get_dispatch_order() != nullptr && !Ab.get_band_rows();
     auto Am = std::move(Ab);
     ok = ok && Am.get_dispatch_order() != nullptr && Ab.get_dispatch_order() == nullptr;
     const I Mb = Am.get_num_block_rows(), nnzb = Am.get_num_blocks();
@@ -284,6 +314,64 @@ void check_dispatch_order(std::shared_ptr<const xspmm::Executor> ex, const char*
     const double rf = rel_frob_vs_rowsums(C1, rs, (size_t)N);
     report(std::string("cached dispatch order ") + tname, ok && rf < 1e-5,
            "rel_frob " + std::to_string(rf));
+}
+
+// examples/05 shape in fp16: csr_to_bcsr finds the contiguous block-rows and
+// keeps the band flag on the matrix (moved with it, cleared by
+// copy_from_host); Tier-1 then runs the band kernel.  A hand-filled copy with
+// the flag set gives the same C bit for bit, without it the column-batch
+// kernel's C (fp32 summation order apart).
+template <typename I>
+void check_band_rows(std::shared_ptr<const xspmm::Executor> ex, const char* tname)
+{
+    const I M = 4096, N = 128;
+    auto h = banded<I>(M, 300, 9);
+    std::vector<__half> hv;
+    auto A = upload<__half, I>(ex, h, hv);
+    auto Ab = xspmm::csr_to_bcsr(ex, A, (I)16, (I)16);
+    bool ok = Ab.get_band_rows();
+    auto Am = std::move(Ab);
+    ok = ok && Am.get_band_rows();
+    const I Mb = Am.get_num_block_rows(), nnzb = Am.get_num_blocks();
+    std::vector<I> brp((size_t)Mb + 1), bci((size_t)nnzb);
+    std::vector<__half> bv((size_t)nnzb * 256);
+    ex->copy_to_host(brp.data(), Am.get_bcsr_row_ptr(), sizeof(I) * brp.size());
+    ex->copy_to_host(bci.data(), Am.get_bcsr_col_ind(), sizeof(I) * bci.size());
+    ex->copy_to_host(bv.data(), Am.get_bcsr_values(), sizeof(__half) * bv.size());
+    xspmm::BCSRMatrix<__half, I> Ac(ex, Mb, Am.get_num_block_cols(), nnzb, 16, 16);
+    Ac.set_shape(M, M);
+    Ac.set_band_rows(true);
+    Ac.copy_from_host(brp.data(), bci.data(), bv.data());
+    ok = ok && !Ac.get_band_rows();  // copy_from_host clears it
+    std::vector<__half> hB((size_t)M * N, __half(1.0f));
+    __half* d_B = nullptr;
+    float *d_C1 = nullptr, *d_C2 = nullptr, *d_C3 = nullptr;
+    ex->allocate(reinterpret_cast<void**>(&d_B), sizeof(__half) * hB.size());
+    ex->allocate(reinterpret_cast<void**>(&d_C1), sizeof(float) * (size_t)M * N);
+    ex->allocate(reinterpret_cast<void**>(&d_C2), sizeof(float) * (size_t)M * N);
+    ex->allocate(reinterpret_cast<void**>(&d_C3), sizeof(float) * (size_t)M * N);
+    ex->copy_from_host(d_B, hB.data(), sizeof(__half) * hB.size());
+    xspmm::spmm(Am, d_B, d_C1, N);  // band kernel
+    xspmm::spmm(Ac, d_B, d_C2, N);  // column-batch kernel
+    Ac.set_band_rows(true);         // the rows are contiguous: the caller may say so
+    xspmm::spmm(Ac, d_B, d_C3, N);  // band kernel
+    ex->synchronize();
+    std::vector<float> C1((size_t)M * N), C2((size_t)M * N), C3((size_t)M * N);
+    ex->copy_to_host(C1.data(), d_C1, sizeof(float) * C1.size());
+    ex->copy_to_host(C2.data(), d_C2, sizeof(float) * C2.size());
+    ex->copy_to_host(C3.data(), d_C3, sizeof(float) * C3.size());
+    ex->free(d_B);
+    ex->free(d_C1);
+    ex->free(d_C2);
+    ex->free(d_C3);
+    ok = ok && std::memcmp(C1.data(), C3.data(), sizeof(float) * C1.size()) == 0;
+    std::vector<double> rs((size_t)M, 0.0);
+    for (I r = 0; r < M; ++r)
+        for (I k = h.rp[(size_t)r]; k < h.rp[(size_t)r + 1]; ++k) rs[(size_t)r] += (float)hv[(size_t)k];
+    const double rf1 = rel_frob_vs_rowsums(C1, rs, (size_t)N);
+    const double rf2 = rel_frob_vs_rowsums(C2, rs, (size_t)N);
+    report(std::string("band kernel from csr_to_bcsr ") + tname, ok && rf1 < 1e-5 && rf2 < 1e-5,
+           "rel_frob band " + std::to_string(rf1) + ", column batches " + std::to_string(rf2));
 }
 
 // CPU and GPU conversions of the same matrix agree bit for bit.
@@ -413,6 +501,8 @@ int main()
         check_ragged_n<__half, int32_t>(ex, "f16/i32");
         check_dispatch_order<int32_t>(ex, "i32");
         check_dispatch_order<int64_t>(ex, "i64");
+        check_band_rows<int32_t>(ex, "i32");
+        check_band_rows<int64_t>(ex, "i64");
         check_cpu_gpu_conversion<int32_t>(ex);
         check_cpu_gpu_conversion<int64_t>(ex);
         check_errors(ex);
