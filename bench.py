@@ -108,9 +108,10 @@ def cpu_baseline(p, N, nnz, seconds):
 
 def tier1_kernel(value_bytes, K, N, nnzb, Mb, band=False):
     """Name of the kernel one Tier-1 call launches (the launcher's own rule in
-    xspmm_amd/csrc/spmm.hip: fp16 takes the band kernel when csr_to_bcsr
-    found contiguous, overlapping block-rows (`band`) and N % 8 == 0 and B
-    fits 32-bit offsets; else the GEMM-tiled kernel when every block
+    xspmm_amd/csrc/spmm.hip: a grid csr_to_bcsr found to have contiguous,
+    overlapping block-rows (`band`) takes the band kernel of its type where
+    it covers the shape (fp16: N % 8 == 0; fp32: N % 4 == 0; B within 32-bit
+    offsets); else fp16 takes the GEMM-tiled kernel when every block
     is present, else the column-batch kernel when N % 8 == 0 and B and the
     block grid fit its 32-bit offsets, unless XSPMM_SPMM_KERNEL selects
     another one; fp32 takes its column-batch kernel when N % 4 == 0 and B
@@ -120,6 +121,8 @@ def tier1_kernel(value_bytes, K, N, nnzb, Mb, band=False):
     XSPMM_F32_SHORT=off)."""
     if value_bytes == 4:
         Kb = (K + 15) // 16
+        if band and N % 4 == 0 and K * N * 4 <= 1 << 31 and N < 1 << 22 and Kb < 1 << 20:
+            return "spmm_f32_band_kernel"
         choice = os.environ.get("XSPMM_F32_KERNEL", "")
         if (N % 4 == 0 and K * N * 4 <= 1 << 31 and Kb < 1 << 21 and choice != "tile"
                 and (choice == "batch" or Mb * ((N + 127) // 128) >= 512)):
@@ -386,7 +389,7 @@ def main():
     eff = 2.0 * nnz * N / t / 1e12
     padded = 2.0 * nnzb * 256 * N / t / 1e12
     mfma_peak = FP16_PEAK_TFLOPS if sT == 2 else FP32_MFMA_PEAK_TFLOPS
-    kernel = tier1_kernel(sT, K, N, nnzb, Mb, band=sT == 2 and Bm.band_rows())
+    kernel = tier1_kernel(sT, K, N, nnzb, Mb, band=Bm.band_rows())
     # Matrix-core work the kernel executes: the column-batch kernels multiply
     # only the block columns that hold a non-zero entry (32 flops per such
     # column, row and output column: 16 rows x multiply-add), the other

@@ -139,35 +139,39 @@ int xspmm_bcsr_spmm_ordered(int vtype, int itype, int64_t M, int64_t K, int64_t 
                             void* stream);
 
 /*
- * Whether an fp16 grid takes the band kernel (xspmm_bcsr_spmm_band): *band =
- * 1 when every block-row is one contiguous run of block columns and the
- * band kernel's B-row gathers (32 rows per aligned pair of block columns in
- * the span of each group of four block-rows) do not exceed the column-batch
- * kernel's (one row per non-zero column of each block, estimated from nnz,
- * the CSR entries behind the grid; 0 = not known, every column counted).
- * Fully populated grids (the GEMM-tiled kernel's) and runs with the
- * diagnostic switch XSPMM_SPMM_KERNEL set give 0.  Reads two counters back
- * (synchronizes `stream`).  csr_to_bcsr makes this check once for a C++
- * BCSRMatrix (BCSRMatrix::get_band_rows).
+ * Whether a grid takes a band kernel (xspmm_bcsr_spmm_band): *band = 1 when
+ * every block-row is one contiguous run of block columns, the grid is not
+ * full, and the band kernel's B-row gathers (32 rows per aligned pair of block
+ * columns in the span of each group of four block-rows) do not exceed the
+ * column-batch kernel's (one row per non-zero column of each block, estimated
+ * from nnz, the CSR entries behind the grid; 0 = not known, every column
+ * counted); for fp32 (vtype XSPMM_F32) also when the block-rows hold at least
+ * 16 blocks on average.  Fully populated grids (the GEMM-tiled kernel's) and
+ * runs with the diagnostic switch XSPMM_SPMM_KERNEL (fp16) or
+ * XSPMM_F32_KERNEL (fp32) set give 0.  Reads two
+ * counters back (synchronizes `stream`).  csr_to_bcsr makes this check once
+ * for a C++ BCSRMatrix (BCSRMatrix::get_band_rows).
  * No counterpart in the reference (whose Tier-1 has one kernel,
  * src/common/spmm_math.hpp:20-146).
  */
-int xspmm_bcsr_band_rows(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnz,
+int xspmm_bcsr_band_rows(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnz,
                          int64_t nnzb, const void* brp, const void* bci, int* band, void* stream);
 
 /*
- * xspmm_bcsr_spmm (fp16 A and B, fp32 C) with the band kernel: four
- * neighbouring block-rows share each 32-row B tile through LDS.  Only
+ * xspmm_bcsr_spmm with the band kernel of vtype.  fp16: four neighbouring
+ * block-rows share each 32-row B tile through LDS; fp32: four neighbouring
+ * block-rows share each B load in registers (v_mfma_f32_16x16x4f32).  Only
  * correct when every block-row is one contiguous run of block columns
- * (xspmm_bcsr_band_rows checks; on other grids the kernel stays inside A, B
- * and C but C is wrong).  Shapes the kernel does not cover (N % 8 != 0, K * N
- * * 2 > 2^31) run the column-batch kernel instead.  Every block multiplies
- * all 16 of its columns, so an Inf/NaN in B gives NaN as in the reference.
- * Asynchronous on `stream`.
+ * (xspmm_bcsr_band_rows checks; on other grids the kernels stay inside A, B
+ * and C but C is wrong).  Shapes a band kernel does not cover (fp16: N % 8 !=
+ * 0; fp32: N % 4 != 0 or B / C off a 16-byte boundary; K * N * value bytes >
+ * 2^31) run the column-batch kernel instead.  Every block a row holds
+ * multiplies all 16 of its columns, so an Inf/NaN in B gives NaN in the rows
+ * the reference's does.  Asynchronous on `stream`.
  * Replaces, for banded grids, the same call as xspmm_bcsr_spmm
  * (reference src/hip/unstructured_mtx_mul.hip:108-146).
  */
-int xspmm_bcsr_spmm_band(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
+int xspmm_bcsr_spmm_band(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
                          const void* brp, const void* bci, const void* bvals, const void* B, float* C,
                          int64_t N, void* stream);
 

@@ -1,10 +1,12 @@
-"""GPU parity of the fp16 band kernel (xspmm_bcsr_spmm_band) and of the check
-that selects it (xspmm_bcsr_band_rows).
+"""GPU parity of the band kernels (xspmm_bcsr_spmm_band: spmm_f16_band_kernel
+and spmm_f32_band_kernel) and of the check that selects them
+(xspmm_bcsr_band_rows).
 
-The band kernel multiplies grids whose block-rows are contiguous runs of block
-columns, four neighbouring block-rows per workgroup sharing each B tile; the
-density sweep of the reference (examples/05_core_spmm_benchmark.cpp:56-77,
-banded matrices) is of this shape.  Bars:
+The band kernels multiply grids whose block-rows are contiguous runs of block
+columns, four neighbouring block-rows per workgroup sharing each B tile (fp16,
+through LDS) or each B load (fp32, in registers); the density sweep of the
+reference (examples/05_core_spmm_benchmark.cpp:56-77, banded matrices) is of
+this shape.  Bars, for fp16 and fp32 values:
   * integer-valued A and B keep every fp32 partial sum exact, so C must equal
     the fp64 product bit for bit (a row, column or pair mix-up cannot hide in
     a tolerance);
@@ -14,9 +16,11 @@ banded matrices) is of this shape.  Bars:
     end, empty block-rows and whole empty groups, single block-rows, int32
     and int64 indices, N from 8 to 264 (one to three 128-column chunks);
   * an Inf in B that meets a zero column of a present block gives NaN, as the
-    reference's tile product (src/common/spmm_math.hpp:93-110) does;
-  * the selection: bands and shifted bands take the kernel; a grid with a gap
-    in a block-row, a random sparse grid and a fully populated grid do not.
+    reference's tile product (src/common/spmm_math.hpp:93-110) does, and
+    never reaches a row that does not hold that block;
+  * the selection: bands and shifted bands take the kernel (fp32 from 16
+    blocks per block-row); a grid with a gap in a block-row, a random sparse
+    grid and a fully populated grid do not.
 All calls go through the C ABI.
 """
 from __future__ import annotations
@@ -45,7 +49,10 @@ def note(msg):
     print(msg, flush=True)
 
 
-def band_csr(M, K, bw, shift=0, empty_every=0, rng=None, integer=False):
+DTYPES = [np.float16, np.float32]
+
+
+def band_csr(M, K, bw, shift=0, empty_every=0, rng=None, integer=False, dtype=np.float16):
     """Rows i: columns max(0, i + shift - bw) .. min(K - 1, i + shift + bw);
     block-rows b with b % empty_every == 1 left empty."""
     rows = []
@@ -61,9 +68,9 @@ def band_csr(M, K, bw, shift=0, empty_every=0, rng=None, integer=False):
     np.cumsum(lens, out=rp[1:])
     ci = np.concatenate(rows) if rp[-1] else np.zeros(0, np.int64)
     if integer:
-        vals = rng.integers(-3, 4, size=len(ci)).astype(np.float16)
+        vals = rng.integers(-3, 4, size=len(ci)).astype(dtype)
     else:
-        vals = rng.standard_normal(len(ci)).astype(np.float16)
+        vals = rng.standard_normal(len(ci)).astype(dtype)
     return rp, ci, vals
 
 
@@ -74,7 +81,8 @@ def device_bcsr(torch, M, K, rp, ci, vals, itype):
 
 def band_rows(Bm, nnz):
     band = ctypes.c_int(-1)
-    X._check(X.load().xspmm_bcsr_band_rows(X.icode(Bm.row_ptr.dtype), Bm.num_rows, Bm.num_cols,
+    X._check(X.load().xspmm_bcsr_band_rows(X.vcode(Bm.values.dtype), X.icode(Bm.row_ptr.dtype),
+                                           Bm.num_rows, Bm.num_cols,
                                            Bm.num_block_rows, Bm.num_block_cols, nnz, Bm.num_blocks,
                                            X._ptr(Bm.row_ptr), X._ptr(Bm.col_ind), ctypes.byref(band),
                                            X._stream()))
@@ -84,7 +92,8 @@ def band_rows(Bm, nnz):
 def spmm_band(torch, Bm, B):
     N = int(B.shape[1])
     C = torch.full((Bm.num_rows, N), float("nan"), dtype=torch.float32, device="cuda")
-    X._check(X.load().xspmm_bcsr_spmm_band(X.icode(Bm.row_ptr.dtype), Bm.num_rows, Bm.num_cols,
+    X._check(X.load().xspmm_bcsr_spmm_band(X.vcode(B.dtype), X.icode(Bm.row_ptr.dtype),
+                                           Bm.num_rows, Bm.num_cols,
                                            Bm.num_block_rows, Bm.num_block_cols, Bm.num_blocks,
                                            X._ptr(Bm.row_ptr), X._ptr(Bm.col_ind), X._ptr(Bm.values),
                                            X._ptr(B), X._ptr(C), N, X._stream()))
@@ -117,27 +126,29 @@ def case_id(c):
     return f"M{M}_K{K}_bw{bw}_s{sh}_e{ee}_N{N}_{np.dtype(it).name}"
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f16", "f32"])
 @pytest.mark.parametrize("case", CASES, ids=[case_id(c) for c in CASES])
-def test_band_integer_exact(torch, case):
+def test_band_integer_exact(torch, case, dtype):
     M, K, bw, shift, ee, N, itype = case
     rng = np.random.default_rng(M + K + N)
-    rp, ci, vals = band_csr(M, K, bw, shift, ee, rng, integer=True)
-    note(f"band exact: {case_id(case)}, nnz {len(ci)}")
+    rp, ci, vals = band_csr(M, K, bw, shift, ee, rng, integer=True, dtype=dtype)
+    note(f"band exact: {case_id(case)} {np.dtype(dtype).name}, nnz {len(ci)}")
     Bm = device_bcsr(torch, M, K, rp, ci, vals, itype)
-    Bh = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    Bh = rng.integers(-4, 5, size=(K, N)).astype(dtype)
     C = spmm_band(torch, Bm, torch.as_tensor(Bh).cuda()).cpu().numpy()
     ref = oracle.csr_spmm_f64(M, N, rp, ci, vals, Bh)
     assert np.array_equal(C, ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f16", "f32"])
 @pytest.mark.parametrize("case", CASES, ids=[case_id(c) for c in CASES])
-def test_band_random_against_oracle(torch, case):
+def test_band_random_against_oracle(torch, case, dtype):
     M, K, bw, shift, ee, N, itype = case
     rng = np.random.default_rng(7 * M + K + N)
-    rp, ci, vals = band_csr(M, K, bw, shift, ee, rng)
-    note(f"band random: {case_id(case)}, nnz {len(ci)}")
+    rp, ci, vals = band_csr(M, K, bw, shift, ee, rng, dtype=dtype)
+    note(f"band random: {case_id(case)} {np.dtype(dtype).name}, nnz {len(ci)}")
     Bm = device_bcsr(torch, M, K, rp, ci, vals, itype)
-    Bh = rng.standard_normal((K, N)).astype(np.float16)
+    Bh = rng.standard_normal((K, N)).astype(dtype)
     Bd = torch.as_tensor(Bh).cuda()
     C = spmm_band(torch, Bm, Bd)
     C2 = spmm_band(torch, Bm, Bd)
@@ -154,15 +165,17 @@ def test_band_random_against_oracle(torch, case):
         assert torch.equal(X.spmm(Bm, Bd), C)
 
 
-def test_band_inf_meets_zero_column(torch):
-    """B row k holds Inf; row 3 of A has a present block over column k whose
-    column k is zero in every row: the reference multiplies the whole block,
-    so 0 * Inf gives NaN in every row of that block-row, and only there."""
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f16", "f32"])
+def test_band_inf_meets_zero_column(torch, dtype):
+    """B row k holds Inf; column k of A is zero in every row, but the blocks
+    over it stay present: the reference multiplies each block a row holds
+    whole, so 0 * Inf gives NaN in every row of the block-rows holding that
+    block, and only there."""
     M = K = 256
     N = 32
     rng = np.random.default_rng(3)
-    rp, ci, vals = band_csr(M, K, 20, 0, 0, rng)
-    D = np.zeros((M, K), np.float16)
+    rp, ci, vals = band_csr(M, K, 20, 0, 0, rng, dtype=dtype)
+    D = np.zeros((M, K), dtype)
     for i in range(M):
         D[i, ci[rp[i]:rp[i + 1]]] = vals[rp[i]:rp[i + 1]]
     k = 16 * 5 + 3
@@ -172,7 +185,7 @@ def test_band_inf_meets_zero_column(torch):
     np.add.at(rp2, nzr + 1, 1)
     rp2 = np.cumsum(rp2)
     Bm = device_bcsr(torch, M, K, rp2, nzc, D[nzr, nzc], np.int32)
-    Bh = rng.standard_normal((K, N)).astype(np.float16)
+    Bh = rng.standard_normal((K, N)).astype(dtype)
     Bh[k, 7] = np.inf
     C = spmm_band(torch, Bm, torch.as_tensor(Bh).cuda()).cpu().numpy()
     brp, bci, _ = host_bcsr(Bm)
@@ -217,3 +230,11 @@ def test_band_selection(torch):
     rp3 = np.concatenate([[0], np.cumsum(np.bincount(nzr, minlength=256))])
     Bm = device_bcsr(torch, 256, 256, rp3, nzc, D[nzr, nzc], np.int32)
     assert band_rows(Bm, len(nzc)) == 0
+    # fp32: a wide band (about 90 blocks per block-row) takes the fp32 band
+    # kernel, a narrow one (about 5) keeps the column-batch kernel
+    rp, ci, vals = band_csr(4096, 4096, 700, 0, 0, rng, dtype=np.float32)
+    Bm = device_bcsr(torch, 4096, 4096, rp, ci, vals, np.int32)
+    assert band_rows(Bm, len(ci)) == 1 and Bm.band_rows()
+    rp, ci, vals = band_csr(4096, 4096, 30, 0, 0, rng, dtype=np.float32)
+    Bm = device_bcsr(torch, 4096, 4096, rp, ci, vals, np.int32)
+    assert band_rows(Bm, len(ci)) == 0 and not Bm.band_rows()

@@ -295,7 +295,8 @@ def test_spmm_locality_order(torch, case):
                                      p.N, ptr(order) if order is not None else None, stream) == X.OK
     if Bm.band_rows():
         C3 = torch.full((p.M, p.N), float("nan"), dtype=torch.float32, device="cuda")
-        assert L.xspmm_bcsr_spmm_band(X.icode(Bm.row_ptr.dtype), Bm.num_rows, Bm.num_cols, Mb,
+        assert L.xspmm_bcsr_spmm_band(X.vcode(Bm.values.dtype), X.icode(Bm.row_ptr.dtype), Bm.num_rows,
+                                      Bm.num_cols, Mb,
                                       Bm.num_block_cols, Bm.num_blocks, ptr(Bm.row_ptr),
                                       ptr(Bm.col_ind), ptr(Bm.values), ptr(B), ptr(C3), p.N,
                                       stream) == X.OK

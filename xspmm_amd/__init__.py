@@ -68,9 +68,9 @@ def load():
     L.xspmm_bcsr_dispatch_order.restype = i32
     L.xspmm_bcsr_dispatch_order.argtypes = [i32, i64, p, p, C.POINTER(C.c_int), p]
     L.xspmm_bcsr_band_rows.restype = i32
-    L.xspmm_bcsr_band_rows.argtypes = [i32, i64, i64, i64, i64, i64, i64, p, p, C.POINTER(C.c_int), p]
+    L.xspmm_bcsr_band_rows.argtypes = [i32, i32, i64, i64, i64, i64, i64, i64, p, p, C.POINTER(C.c_int), p]
     L.xspmm_bcsr_spmm_band.restype = i32
-    L.xspmm_bcsr_spmm_band.argtypes = [i32, i64, i64, i64, i64, i64, p, p, p, p, p, i64, p]
+    L.xspmm_bcsr_spmm_band.argtypes = [i32, i32, i64, i64, i64, i64, i64, p, p, p, p, p, i64, p]
     L.xspmm_bcsr_dispatch_order_cols.restype = i32
     L.xspmm_bcsr_dispatch_order_cols.argtypes = [i32, i64, p, p, p, C.POINTER(C.c_int), p]
     L.xspmm_csr_to_bcsr_count.restype = i32
@@ -247,10 +247,10 @@ class BCSRMatrix:
     # from (their identities and versions).
     _order: object = field(default=None, repr=False, compare=False)
     _order_key: object = field(default=None, repr=False, compare=False)
-    # Whether fp16 Tier-1 takes the band kernel (every block-row a contiguous
-    # run of block columns, see xspmm_bcsr_band_rows), decided once for the
-    # same tensors as the order; _nnz: CSR entries behind the grid (0: not
-    # known), which csr_to_bcsr records.
+    # Whether Tier-1 takes a band kernel (every block-row a contiguous run of
+    # block columns, see xspmm_bcsr_band_rows), decided once for the same
+    # tensors as the order; _nnz: CSR entries behind the grid (0: not known),
+    # which csr_to_bcsr records.
     _band: object = field(default=None, repr=False, compare=False)
     _band_key: object = field(default=None, repr=False, compare=False)
     _nnz: int = field(default=0, repr=False, compare=False)
@@ -279,15 +279,16 @@ class BCSRMatrix:
         return self._order
 
     def band_rows(self) -> bool:
-        """Whether fp16 Tier-1 multiplies this grid with the band kernel
-        (decided on first use for the current row_ptr and col_ind)."""
+        """Whether Tier-1 multiplies this grid with a band kernel (decided on
+        first use for the current row_ptr and col_ind)."""
         key = (id(self.row_ptr), self.row_ptr.data_ptr(), self.row_ptr._version,
                id(self.col_ind), self.col_ind.data_ptr(), self.col_ind._version,
                int(self.num_block_rows))
         if self._band_key != key:
             band = C.c_int(0)
             if self.r_block == 16 and self.c_block == 16:
-                _check(load().xspmm_bcsr_band_rows(icode(self.row_ptr.dtype), int(self.num_rows),
+                _check(load().xspmm_bcsr_band_rows(vcode(self.values.dtype), icode(self.row_ptr.dtype),
+                                                   int(self.num_rows),
                                                    int(self.num_cols), int(self.num_block_rows),
                                                    int(self.num_block_cols), int(self._nnz),
                                                    self.num_blocks, _ptr(self.row_ptr),
@@ -324,8 +325,7 @@ def csr_to_bcsr(A: CSRMatrix, r_block: int = 16, c_block: int = 16) -> BCSRMatri
     out._nnz = int(A.nnz)
     if r_block == 16 and c_block == 16:
         out.dispatch_order()  # once here rather than in every Tier-1 call
-        if A.values.dtype == torch.float16:
-            out.band_rows()
+        out.band_rows()
     return out
 
 
@@ -341,8 +341,8 @@ def spmm(A: BCSRMatrix, B, C_out=None, N: int | None = None):
         C_out = torch.empty((A.num_rows, N), dtype=torch.float32, device=dev)
     _check_dense(B, "B", A.num_cols, N, A.values.dtype, dev)
     _check_dense(C_out, "C_out", A.num_rows, N, torch.float32, dev)
-    if B.dtype == torch.float16 and A.band_rows():
-        _check(L.xspmm_bcsr_spmm_band(icode(A.row_ptr.dtype), A.num_rows, A.num_cols,
+    if A.band_rows():
+        _check(L.xspmm_bcsr_spmm_band(vcode(B.dtype), icode(A.row_ptr.dtype), A.num_rows, A.num_cols,
                                       A.num_block_rows, A.num_block_cols, A.num_blocks,
                                       _ptr(A.row_ptr), _ptr(A.col_ind), _ptr(A.values), _ptr(B),
                                       _ptr(C_out), N, _stream()))

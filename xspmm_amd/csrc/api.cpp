@@ -165,15 +165,12 @@ void spmm(const BCSRMatrix<InputType, IndexType>& A, const InputType* B, OutputT
         if (A.get_r_block() != 16 || A.get_c_block() != 16)
             throw std::invalid_argument("xSpMM: the MFMA tile kernel requires 16x16 blocks.");
         use_device(h);
-        if constexpr (sizeof(InputType) == 2) {
-            if (A.get_band_rows()) {
-                detail::bcsr_spmm_band<IndexType>(
-                    A.get_num_rows(), A.get_num_cols(), A.get_num_block_rows(), A.get_num_block_cols(),
-                    A.get_num_blocks(), A.get_bcsr_row_ptr(), A.get_bcsr_col_ind(),
-                    reinterpret_cast<const uint16_t*>(A.get_bcsr_values()),
-                    reinterpret_cast<const uint16_t*>(B), C, N, kStream);
-                return;
-            }
+        if (A.get_band_rows()) {
+            detail::bcsr_spmm_band<dev_t<InputType>, IndexType>(
+                A.get_num_rows(), A.get_num_cols(), A.get_num_block_rows(), A.get_num_block_cols(),
+                A.get_num_blocks(), A.get_bcsr_row_ptr(), A.get_bcsr_col_ind(), dev(A.get_bcsr_values()),
+                dev(B), C, N, kStream);
+            return;
         }
         (void)detail::bcsr_spmm_ex<dev_t<InputType>, IndexType>(
             A.get_num_rows(), A.get_num_cols(), A.get_num_block_rows(), A.get_num_block_cols(),
@@ -302,10 +299,11 @@ BCSRMatrix<ValueType, IndexType> csr_to_bcsr(std::shared_ptr<const Executor> tar
                                                              Mb, order, kStream))
                 out.set_dispatch_order(nullptr);  // the identity: not worth a load per workgroup
         }
-        // fp16 grids of contiguous, overlapping block-rows: the band kernel
-        if (sizeof(ValueType) == 2 && r_block == 16 && c_block == 16)
+        // grids of contiguous, overlapping block-rows: the band kernels
+        if (r_block == 16 && c_block == 16)
             out.set_band_rows(detail::spmm_band_wanted<IndexType>(out.get_bcsr_row_ptr(), out.get_bcsr_col_ind(),
-                                                                  M, K, Mb, Kb, nnz, nnzb, 0, kStream));
+                                                                  M, K, Mb, Kb, nnz, nnzb, 0,
+                                                                  (int)sizeof(ValueType), kStream));
     } else {
         // GPU-resident input, host target: convert on the GPU, then copy down.
         detail::Scratch bci((size_t)(nnzb > 0 ? nnzb : 1) * sizeof(IndexType), kStream);

@@ -173,12 +173,13 @@ int xspmm_bcsr_spmm_ordered(int vtype, int itype, int64_t M, int64_t K, int64_t 
     });
 }
 
-int xspmm_bcsr_band_rows(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnz,
+int xspmm_bcsr_band_rows(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnz,
                          int64_t nnzb, const void* brp, const void* bci, int* band, void* stream)
 {
     return guarded([&] {
         if (!band) throw std::invalid_argument("xSpMM: band must not be NULL.");
         *band = 0;
+        if (vtype != XSPMM_F16 && vtype != XSPMM_F32) throw std::invalid_argument("xSpMM: unknown value type.");
         if (M < 0 || K < 0 || Mb < 0 || Kb < 0 || nnzb < 0)
             throw std::invalid_argument("xSpMM: negative size passed to BCSR SpMM.");
         if (Mb == 0 || nnzb == 0) return;
@@ -186,23 +187,23 @@ int xspmm_bcsr_band_rows(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb
         with_index(itype, [&](auto ti) {
             using I = typename decltype(ti)::type;
             *band = spmm_band_wanted<I>(static_cast<const I*>(brp), static_cast<const I*>(bci), M, K, Mb, Kb,
-                                        nnz, nnzb, 0, as_stream(stream))
+                                        nnz, nnzb, 0, vtype == XSPMM_F16 ? 2 : 4, as_stream(stream))
                         ? 1
                         : 0;
         });
     });
 }
 
-int xspmm_bcsr_spmm_band(int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
+int xspmm_bcsr_spmm_band(int vtype, int itype, int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb,
                          const void* brp, const void* bci, const void* bvals, const void* B, float* C,
                          int64_t N, void* stream)
 {
     return guarded([&] {
-        with_index(itype, [&](auto ti) {
+        with_types(vtype, itype, [&](auto tv, auto ti) {
+            using T = typename decltype(tv)::type;
             using I = typename decltype(ti)::type;
-            bcsr_spmm_band<I>(M, K, Mb, Kb, nnzb, static_cast<const I*>(brp), static_cast<const I*>(bci),
-                              static_cast<const uint16_t*>(bvals), static_cast<const uint16_t*>(B), C, N,
-                              as_stream(stream));
+            bcsr_spmm_band<T, I>(M, K, Mb, Kb, nnzb, static_cast<const I*>(brp), static_cast<const I*>(bci),
+                                 static_cast<const T*>(bvals), static_cast<const T*>(B), C, N, as_stream(stream));
         });
     });
 }

@@ -222,12 +222,13 @@ template <typename T, typename I>
 bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,
                   const I* bci, const T* bvals, const T* B, float* C, int64_t N,
                   const int32_t* order, const I* row_map, hipStream_t s);
-// Tier-1 (fp16) with the band kernel where its shape conditions hold, else as
-// bcsr_spmm_ex with no order.  The band kernel is only correct when every
-// block-row is one contiguous run of block columns (spmm_band_wanted checks).
-template <typename I>
+// Tier-1 with the band kernel of T (uint16_t: fp16, float: fp32) where its
+// shape conditions hold, else as bcsr_spmm_ex with no order.  The band
+// kernels are only correct when every block-row is one contiguous run of
+// block columns (spmm_band_wanted checks).
+template <typename T, typename I>
 void bcsr_spmm_band(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp, const I* bci,
-                    const uint16_t* bvals, const uint16_t* B, float* C, int64_t N, hipStream_t s);
+                    const T* bvals, const T* B, float* C, int64_t N, hipStream_t s);
 // Tier-1 without any allocation: the temporaries come from a fixed device
 // array of kNoAllocScratchBytes (one copy per GPU, shared by every call on
 // it).  Throws std::invalid_argument when a product needs more.
@@ -317,14 +318,24 @@ bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t n
 // Only correct when every block-row is contiguous; spmm_band_f16_covers tells
 // whether the shape is covered (false: nothing launched).
 bool spmm_band_f16_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N);
-// Whether Tier-1 should take the band kernel for this fp16 grid: every
-// block-row contiguous, and the groups' spans gather fewer B rows than the
-// column-batch kernel would (nnz: CSR entries behind the grid, 0 if not
-// known; N: a typical column count, 0 for 128).  Reads two counters back
-// (synchronizes `s`).
+// Tier-1 fp32 SpMM for banded grids (contiguous block-rows): four
+// neighbouring block-rows per workgroup share each B load in registers.
+// False (nothing launched) when the shape is not covered (N % 4 != 0, B or C
+// not 16-byte aligned, K * N * 4 > 2^31).
+bool spmm_band_f32_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N, const void* B, const void* C);
+template <typename I>
+bool bcsr_spmm_band_f32(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                        const float* bvals, const float* B, float* C, int64_t N, const I* row_map,
+                        hipStream_t s);
+// Whether Tier-1 should take a band kernel for this grid of fp16
+// (value_bytes 2) or fp32 (4) blocks: every block-row contiguous, the grid not
+// full, the groups' spans gathering fewer B rows than the column-batch kernel
+// would (nnz: CSR entries behind the grid, 0 if not known; N: a typical column
+// count, 0 for 128), and for fp32 at least 16 blocks per block-row on average.
+// Reads two counters back (synchronizes `s`).
 template <typename I>
 bool spmm_band_wanted(const I* brp, const I* bci, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
-                      int64_t nnz, int64_t nnzb, int64_t N, hipStream_t s);
+                      int64_t nnz, int64_t nnzb, int64_t N, int value_bytes, hipStream_t s);
 template <typename I>
 bool bcsr_spmm_band_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
                         const uint16_t* bvals, const uint16_t* B, float* C, int64_t N,

@@ -1949,22 +1949,28 @@ bool bcsr_spmm_ex(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, co
                                   arena, s);
 }
 
-template <typename I>
+template <typename T, typename I>
 void bcsr_spmm_band(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp, const I* bci,
-                    const uint16_t* bvals, const uint16_t* B, float* C, int64_t N, hipStream_t s)
+                    const T* bvals, const T* B, float* C, int64_t N, hipStream_t s)
 {
     check_shape(M, K, Mb, Kb, nnzb, N);
     if (M == 0 || N == 0 || Mb == 0) return;
-    check_alignment(bvals, B, true);
-    if (bcsr_spmm_band_f16<I>(M, K, Mb, Kb, brp, bci, bvals, B, C, N, nullptr, s)) return;
-    (void)bcsr_spmm_ex<uint16_t, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr, s);
+    check_alignment(bvals, B, sizeof(T) == 2);
+    if constexpr (sizeof(T) == 2) {
+        if (bcsr_spmm_band_f16<I>(M, K, Mb, Kb, brp, bci, bvals, B, C, N, nullptr, s)) return;
+    } else {
+        if (bcsr_spmm_band_f32<I>(M, K, Mb, Kb, brp, bci, bvals, B, C, N, nullptr, s)) return;
+    }
+    (void)bcsr_spmm_ex<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr, s);
 }
-template void bcsr_spmm_band<int32_t>(int64_t, int64_t, int64_t, int64_t, int64_t, const int32_t*,
-                                      const int32_t*, const uint16_t*, const uint16_t*, float*, int64_t,
-                                      hipStream_t);
-template void bcsr_spmm_band<int64_t>(int64_t, int64_t, int64_t, int64_t, int64_t, const int64_t*,
-                                      const int64_t*, const uint16_t*, const uint16_t*, float*, int64_t,
-                                      hipStream_t);
+#define XSPMM_SPMM_BAND(T, I)                                                                          \
+    template void bcsr_spmm_band<T, I>(int64_t, int64_t, int64_t, int64_t, int64_t, const I*, const I*, \
+                                       const T*, const T*, float*, int64_t, hipStream_t);
+XSPMM_SPMM_BAND(uint16_t, int32_t)
+XSPMM_SPMM_BAND(uint16_t, int64_t)
+XSPMM_SPMM_BAND(float, int32_t)
+XSPMM_SPMM_BAND(float, int64_t)
+#undef XSPMM_SPMM_BAND
 
 template <typename T, typename I>
 void bcsr_spmm_noalloc(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, const I* brp,

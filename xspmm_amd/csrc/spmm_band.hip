@@ -69,6 +69,9 @@ static_assert(XSPMM_BAND_DEPTH >= 6 && XSPMM_BAND_DEPTH <= 18, "band ring depth 
 #define XSPMM_BAND_XCD 1
 #endif
 constexpr bool kBandXcd = XSPMM_BAND_XCD != 0;
+#ifndef XSPMM_BAND_F32_DEPTH
+#define XSPMM_BAND_F32_DEPTH 4
+#endif
 #ifndef XSPMM_BAND_WPR
 #define XSPMM_BAND_WPR 2
 #endif
@@ -307,6 +310,180 @@ __global__ __launch_bounds__(64 * kBandRows * WPR) void spmm_f16_band_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 banded grids: spmm_f32_band_kernel.  v_mfma_f32_16x16x4f32 takes one K
+// index per lane group (lane (i, k) holds A[i][k] and B[k][i]), so B rows go
+// from memory straight into MFMA operands and a wave can apply them to
+// several block-rows.  A workgroup owns a group of four consecutive block-rows
+// and 64 columns of C; its 4 waves split the group's block-column span
+// (wave w takes columns lo + w, lo + w + 4, ...), and each wave multiplies
+// every block it meets into all four rows:
+//   * B: for block column c, lane (n, g) loads row 16c + 4g + s, columns
+//     n0 + 4n .. + 3 (one 16-byte load, s = 0 .. 3); component j of load s
+//     is the B operand of MFMA (s, j), K slot g <-> block column 4g + s;
+//   * A: per row, lane (i, g) loads row i, columns 4g .. 4g + 3 of the row's
+//     block at c (one 16-byte load); component s is the A operand of MFMA
+//     (s, j) -- the same K order;
+//   * so one block's 4 B loads per lane serve 4 rows x 16 MFMAs; loads run L
+//     blocks ahead, every block issues the same loads (a row without the
+//     block, or a column past the span, reads zeros), and the MFMAs of a
+//     row that does not hold the block are skipped, so B meets a row only
+//     through the blocks it holds (an Inf or NaN in B gives NaN where the
+//     reference's tile product would);
+//   * the waves' partial tiles are summed through LDS in wave order.
+// Output tile j of a wave holds columns n0 + 4n + j (lane (n, g): rows
+// 4g .. 4g + 3), as in the fp32 column-batch kernel.  Each block-row must be
+// one contiguous run of block columns (spmm_band_wanted); N % 4 == 0, B and C
+// 16-byte aligned.
+template <typename I, int L>
+__global__ __launch_bounds__(256, 2) void spmm_f32_band_kernel(
+    const I* __restrict__ brp, const I* __restrict__ bci, const float* __restrict__ vals,
+    const float* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N, int64_t Mb,
+    const I* __restrict__ row_map)
+{
+    typedef float float4v_t __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) float red[4 * 4 * 16 * 64];  // [wave][row][16][64]
+    __shared__ int32_t s_first[4];
+    __shared__ int32_t s_last[4];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int li = lane & 15;
+    const int g = lane >> 4;
+    const uint32_t G = gridDim.x;
+    const uint32_t x8 = blockIdx.x & 7u;
+    const uint32_t grp = kBandXcd ? x8 * (G >> 3) + min(x8, G & 7u) + (blockIdx.x >> 3) : blockIdx.x;
+    const int64_t br0 = (int64_t)grp * 4;
+    const int64_t n0 = (int64_t)blockIdx.y * 64;
+
+    {
+        const int64_t br = br0 + wave;
+        int32_t first = 0x7fffffff, last = -1;
+        if (br < Mb) {
+            const int64_t rs = (int64_t)brp[br], re = (int64_t)brp[br + 1];
+            if (re > rs) {
+                first = (int32_t)bci[rs];
+                last = (int32_t)bci[re - 1];
+            }
+        }
+        if (lane == 0) {
+            s_first[wave] = first;
+            s_last[wave] = last;
+        }
+    }
+    __syncthreads();
+    int32_t lo = 0x7fffffff, hi = -1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        lo = min(lo, s_first[w]);
+        hi = max(hi, s_last[w]);
+    }
+    const int32_t span = hi >= 0 ? hi - lo + 1 : 0;
+    const int32_t nt = span > wave ? (span - wave + 3) >> 2 : 0;  // this wave's blocks
+    const int32_t c0 = lo + wave;                                 // its first block column
+
+    // rows: block c of row r at index c - first_r, present when in [0, n_r)
+    __amdgpu_buffer_rsrc_t a_rsrc[4];
+    int32_t r_rel0[4], r_n[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t br = br0 + r;
+        int64_t rs = 0, re = 0;
+        if (br < Mb) {
+            rs = (int64_t)brp[br];
+            re = (int64_t)brp[br + 1];
+        }
+        r_n[r] = (int32_t)(re - rs);
+        a_rsrc[r] = band_rsrc(vals + rs * 256, (uint32_t)r_n[r] * 1024u);
+        r_rel0[r] = c0 - s_first[r];
+    }
+    const uint32_t a_lane = (uint32_t)(li * 64 + g * 16);
+    auto a_off = [&](int r, int32_t t) __attribute__((always_inline)) -> uint32_t {
+        const int32_t rel = r_rel0[r] + 4 * t;
+        return (uint32_t)rel < (uint32_t)r_n[r] ? (uint32_t)rel * 1024u + a_lane : kOob;
+    };
+    // B: lane (n, g) of load s reads row 16c + 4g + s, columns n0 + 4n .. +3
+    // (a quad past N reads the row's last quad: it only meets unstored
+    // columns); rows past K read zeros
+    const __amdgpu_buffer_rsrc_t b_rsrc = band_rsrc(B, (uint32_t)(K * N * 4));
+    const uint32_t rowbytes = (uint32_t)(4 * N);
+    const int64_t colq = n0 + 4 * li;
+    const uint32_t b_lane = (uint32_t)(4 * (colq < N ? colq : N - 4)) + __umul24((uint32_t)(4 * g), rowbytes);
+    auto b_off = [&](int32_t t, int sidx) __attribute__((always_inline)) -> uint32_t {
+        const int32_t c = c0 + 4 * t;
+        return t < nt ? __umul24((uint32_t)(16 * c + sidx), rowbytes) + b_lane : kOob;
+    };
+
+    float4v_t acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[r][j] = float4v_t{0.f, 0.f, 0.f, 0.f};
+
+    float4v_t ar[L][4];  // A of the wave's block t, four rows (slot t % L)
+    float4v_t bq[L][4];  // its four B loads
+    auto issue = [&](int slot, int32_t t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sidx = 0; sidx < 4; ++sidx)
+            bq[slot][sidx] = __builtin_bit_cast(
+                float4v_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)b_off(t, sidx), 0, 0));
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            ar[slot][r] = __builtin_bit_cast(
+                float4v_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc[r], (int)a_off(r, t), 0, 0));
+    };
+    auto multiply = [&](int slot, int32_t t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            // uniform: does row r hold this block?
+            if ((uint32_t)(r_rel0[r] + 4 * t) < (uint32_t)r_n[r]) {
+#pragma unroll
+                for (int sidx = 0; sidx < 4; ++sidx)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[slot][r][sidx], bq[slot][sidx][j],
+                                                                         acc[r][j], 0, 0, 0);
+            }
+        }
+    };
+
+    if (nt > 0) {
+#pragma unroll
+        for (int t = 0; t < L; ++t) issue(t, t);
+        for (int32_t t0 = 0; t0 < nt; t0 += L) {
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+                const int32_t t = t0 + u;
+                if (t < nt) multiply(u, t);
+                issue(u, t + L);
+            }
+        }
+    }
+
+    // sum the waves' partial tiles in wave order and store C
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4v_t*>(red + ((wave * 4 + r) * 16 + 4 * g + q) * 64 + 4 * li) =
+                float4v_t{acc[r][0][q], acc[r][1][q], acc[r][2][q], acc[r][3][q]};
+    __syncthreads();
+    for (int e = threadIdx.x; e < 4 * 16 * 16; e += 256) {
+        const int r = e >> 8;              // block-row of the group
+        const int row = (e >> 4) & 15;     // row in the block-row
+        const int c4 = 4 * (e & 15);       // column quad
+        const int64_t grow = (br0 + r) * 16 + row;
+        const int64_t col = n0 + c4;
+        if (br0 + r >= Mb || grow >= M || col >= N) continue;
+        const int o = (r * 16 + row) * 64 + c4;
+        float4v_t v = *reinterpret_cast<const float4v_t*>(red + o);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const float4v_t*>(red + w * 4 * 16 * 64 + o);
+        const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
+        *reinterpret_cast<float4v_t*>(C + crow * N + col) = v;
+    }
+}
+
 // One thread per group of kBandRows block-rows: counts the block-rows that
 // are not one contiguous run of block columns, and adds the group's span in
 // aligned pairs (the pairs the band kernel walks for it).
@@ -346,13 +523,20 @@ __global__ __launch_bounds__(256) void band_analyse_kernel(const I* __restrict__
 
 template <typename I>
 bool spmm_band_wanted(const I* brp, const I* bci, int64_t M, int64_t K, int64_t Mb, int64_t Kb,
-                      int64_t nnz, int64_t nnzb, int64_t N, hipStream_t s)
+                      int64_t nnz, int64_t nnzb, int64_t N, int value_bytes, hipStream_t s)
 {
     (void)M;
+    if (value_bytes != 2 && value_bytes != 4) return false;
     if (Mb < 1 || nnzb < 1 || !spmm_band_f16_covers(K, Kb, Mb, N > 0 ? N : 128)) return false;
+    if (value_bytes == 4 && K * (N > 0 ? N : 128) * 4 > (int64_t(1) << 31)) return false;
+    // fp32: the band kernel's waves split each group's blocks four ways, which
+    // pays from about 16 blocks per block-row (the examples/05 bands from 5 %)
+    if (value_bytes == 4 && nnzb < 16 * Mb) return false;
     if (nnzb == Mb * Kb) return false;  // every block present: the GEMM-tiled kernel's grid
-    // a kernel forced by the diagnostic switch XSPMM_SPMM_KERNEL keeps its grids
-    if (const char* e = std::getenv("XSPMM_SPMM_KERNEL"); e && *e) return false;
+    // a kernel forced by the diagnostic switches XSPMM_SPMM_KERNEL (fp16) or
+    // XSPMM_F32_KERNEL (fp32) keeps its grids
+    if (const char* e = std::getenv(value_bytes == 2 ? "XSPMM_SPMM_KERNEL" : "XSPMM_F32_KERNEL"); e && *e)
+        return false;
     Scratch counters(2 * sizeof(unsigned long long), s);
     XSPMM_HIP_CHECK(hipMemsetAsync(counters.get(), 0, 2 * sizeof(unsigned long long), s));
     const int64_t groups = (Mb + kBandRows - 1) / kBandRows;
@@ -373,9 +557,9 @@ bool spmm_band_wanted(const I* brp, const I* bci, int64_t M, int64_t K, int64_t 
 }
 
 template bool spmm_band_wanted<int32_t>(const int32_t*, const int32_t*, int64_t, int64_t, int64_t,
-                                        int64_t, int64_t, int64_t, int64_t, hipStream_t);
+                                        int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
 template bool spmm_band_wanted<int64_t>(const int64_t*, const int64_t*, int64_t, int64_t, int64_t,
-                                        int64_t, int64_t, int64_t, int64_t, hipStream_t);
+                                        int64_t, int64_t, int64_t, int64_t, int, hipStream_t);
 
 bool spmm_band_f16_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N)
 {
@@ -396,6 +580,32 @@ bool bcsr_spmm_band_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
     XSPMM_LAUNCH_CHECK();
     return true;
 }
+
+bool spmm_band_f32_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N, const void* B, const void* C)
+{
+    return Mb > 0 && N > 0 && N % 4 == 0 && K * N * 4 <= (int64_t(1) << 31) && N < (int64_t(1) << 22) &&
+           Kb < (int64_t(1) << 20) && (N + 63) / 64 <= 65535 && (reinterpret_cast<uintptr_t>(B) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(C) & 15) == 0;
+}
+
+template <typename I>
+bool bcsr_spmm_band_f32(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
+                        const float* bvals, const float* B, float* C, int64_t N, const I* row_map,
+                        hipStream_t s)
+{
+    if (!spmm_band_f32_covers(K, Kb, Mb, N, B, C)) return false;
+    const dim3 grid((unsigned)((Mb + 3) / 4), (unsigned)((N + 63) / 64));
+    hipLaunchKernelGGL((spmm_f32_band_kernel<I, XSPMM_BAND_F32_DEPTH>), grid, dim3(256), 0, s, brp, bci, bvals,
+                       B, C, M, K, N, Mb, row_map);
+    XSPMM_LAUNCH_CHECK();
+    return true;
+}
+template bool bcsr_spmm_band_f32<int32_t>(int64_t, int64_t, int64_t, int64_t, const int32_t*,
+                                          const int32_t*, const float*, const float*, float*, int64_t,
+                                          const int32_t*, hipStream_t);
+template bool bcsr_spmm_band_f32<int64_t>(int64_t, int64_t, int64_t, int64_t, const int64_t*,
+                                          const int64_t*, const float*, const float*, float*, int64_t,
+                                          const int64_t*, hipStream_t);
 
 template bool bcsr_spmm_band_f16<int32_t>(int64_t, int64_t, int64_t, int64_t, const int32_t*,
                                           const int32_t*, const uint16_t*, const uint16_t*, float*,
