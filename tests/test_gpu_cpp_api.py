@@ -21,4 +21,4 @@ def test_cpp_api_checks():
     print(out.stderr)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "[FAIL]" not in out.stdout
-    assert out.stdout.count("[PASS]") >= 16
+    assert out.stdout.count("[PASS]") >= 17

@@ -33,6 +33,13 @@ void report(const std::string& name, bool ok, const std::string& detail = "")
     if (!ok) ++failures;
 }
 
+std::string sci(double v)
+{
+    char b[32];
+    std::snprintf(b, sizeof(b), "%.2e", v);
+    return b;
+}
+
 template <typename I>
 struct HostCsr {
     I M = 0, K = 0;
@@ -316,41 +323,41 @@ void check_dispatch_order(std::shared_ptr<const xspmm::Executor> ex, const char*
            "rel_frob " + std::to_string(rf));
 }
 
-// examples/05 shape in fp16: csr_to_bcsr finds the contiguous block-rows and
+// examples/05 shape (fp16 and fp32): csr_to_bcsr finds the contiguous block-rows and
 // keeps the band flag on the matrix (moved with it, cleared by
 // copy_from_host); Tier-1 then runs the band kernel.  A hand-filled copy with
 // the flag set gives the same C bit for bit, without it the column-batch
 // kernel's C (fp32 summation order apart).
-template <typename I>
+template <typename T, typename I>
 void check_band_rows(std::shared_ptr<const xspmm::Executor> ex, const char* tname)
 {
     const I M = 4096, N = 128;
     auto h = banded<I>(M, 300, 9);
-    std::vector<__half> hv;
-    auto A = upload<__half, I>(ex, h, hv);
+    std::vector<T> hv;
+    auto A = upload<T, I>(ex, h, hv);
     auto Ab = xspmm::csr_to_bcsr(ex, A, (I)16, (I)16);
     bool ok = Ab.get_band_rows();
     auto Am = std::move(Ab);
     ok = ok && Am.get_band_rows();
     const I Mb = Am.get_num_block_rows(), nnzb = Am.get_num_blocks();
     std::vector<I> brp((size_t)Mb + 1), bci((size_t)nnzb);
-    std::vector<__half> bv((size_t)nnzb * 256);
+    std::vector<T> bv((size_t)nnzb * 256);
     ex->copy_to_host(brp.data(), Am.get_bcsr_row_ptr(), sizeof(I) * brp.size());
     ex->copy_to_host(bci.data(), Am.get_bcsr_col_ind(), sizeof(I) * bci.size());
-    ex->copy_to_host(bv.data(), Am.get_bcsr_values(), sizeof(__half) * bv.size());
-    xspmm::BCSRMatrix<__half, I> Ac(ex, Mb, Am.get_num_block_cols(), nnzb, 16, 16);
+    ex->copy_to_host(bv.data(), Am.get_bcsr_values(), sizeof(T) * bv.size());
+    xspmm::BCSRMatrix<T, I> Ac(ex, Mb, Am.get_num_block_cols(), nnzb, 16, 16);
     Ac.set_shape(M, M);
     Ac.set_band_rows(true);
     Ac.copy_from_host(brp.data(), bci.data(), bv.data());
     ok = ok && !Ac.get_band_rows();  // copy_from_host clears it
-    std::vector<__half> hB((size_t)M * N, __half(1.0f));
-    __half* d_B = nullptr;
+    std::vector<T> hB((size_t)M * N, T(1.0f));
+    T* d_B = nullptr;
     float *d_C1 = nullptr, *d_C2 = nullptr, *d_C3 = nullptr;
-    ex->allocate(reinterpret_cast<void**>(&d_B), sizeof(__half) * hB.size());
+    ex->allocate(reinterpret_cast<void**>(&d_B), sizeof(T) * hB.size());
     ex->allocate(reinterpret_cast<void**>(&d_C1), sizeof(float) * (size_t)M * N);
     ex->allocate(reinterpret_cast<void**>(&d_C2), sizeof(float) * (size_t)M * N);
     ex->allocate(reinterpret_cast<void**>(&d_C3), sizeof(float) * (size_t)M * N);
-    ex->copy_from_host(d_B, hB.data(), sizeof(__half) * hB.size());
+    ex->copy_from_host(d_B, hB.data(), sizeof(T) * hB.size());
     xspmm::spmm(Am, d_B, d_C1, N);  // band kernel
     xspmm::spmm(Ac, d_B, d_C2, N);  // column-batch kernel
     Ac.set_band_rows(true);         // the rows are contiguous: the caller may say so
@@ -371,7 +378,7 @@ void check_band_rows(std::shared_ptr<const xspmm::Executor> ex, const char* tnam
     const double rf1 = rel_frob_vs_rowsums(C1, rs, (size_t)N);
     const double rf2 = rel_frob_vs_rowsums(C2, rs, (size_t)N);
     report(std::string("band kernel from csr_to_bcsr ") + tname, ok && rf1 < 1e-5 && rf2 < 1e-5,
-           "rel_frob band " + std::to_string(rf1) + ", column batches " + std::to_string(rf2));
+           "rel_frob band " + sci(rf1) + ", column batches " + sci(rf2));
 }
 
 // CPU and GPU conversions of the same matrix agree bit for bit.
@@ -501,8 +508,9 @@ int main()
         check_ragged_n<__half, int32_t>(ex, "f16/i32");
         check_dispatch_order<int32_t>(ex, "i32");
         check_dispatch_order<int64_t>(ex, "i64");
-        check_band_rows<int32_t>(ex, "i32");
-        check_band_rows<int64_t>(ex, "i64");
+        check_band_rows<__half, int32_t>(ex, "f16/i32");
+        check_band_rows<__half, int64_t>(ex, "f16/i64");
+        check_band_rows<float, int32_t>(ex, "f32/i32");
         check_cpu_gpu_conversion<int32_t>(ex);
         check_cpu_gpu_conversion<int64_t>(ex);
         check_errors(ex);
