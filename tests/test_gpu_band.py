@@ -238,3 +238,74 @@ def test_band_selection(torch):
     rp, ci, vals = band_csr(4096, 4096, 30, 0, 0, rng, dtype=np.float32)
     Bm = device_bcsr(torch, 4096, 4096, rp, ci, vals, np.int32)
     assert band_rows(Bm, len(ci)) == 0 and not Bm.band_rows()
+
+
+def block_band(Mb, Kb, wb):
+    """Block-row b holds block columns max(0, b - wb) .. min(Kb - 1, b + wb)."""
+    lo = np.maximum(0, np.arange(Mb) - wb)
+    hi = np.minimum(Kb - 1, np.arange(Mb) + wb)
+    lens = hi - lo + 1
+    brp = np.zeros(Mb + 1, np.int64)
+    np.cumsum(lens, out=brp[1:])
+    bci = np.concatenate([np.arange(a, b + 1) for a, b in zip(lo, hi)])
+    return brp, bci
+
+
+def spmm_band_arrays(torch, M, K, Mb, Kb, brp, bci, vals, B):
+    N = int(B.shape[1])
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    X._check(X.load().xspmm_bcsr_spmm_band(X.vcode(B.dtype), X.icode(brp.dtype), M, K, Mb, Kb,
+                                           int(bci.numel()), X._ptr(brp), X._ptr(bci), X._ptr(vals),
+                                           X._ptr(B), X._ptr(C), N, X._stream()))
+    torch.cuda.synchronize()
+    return C
+
+
+# (block-rows, block columns, half-width in blocks, ragged rows cut from M, N, index type)
+SPLIT_CASES = [
+    (1024, 1024, 460, 0, 128, np.int32),   # the examples/05 90 % band, 16384^2: >= 512 blocks per block-row
+    (1024, 1024, 460, 0, 64, np.int64),
+    (256, 300, 120, 7, 132, np.int32),     # 64 groups: fewer than the CUs; ragged M, three chunks
+    (1027, 1100, 60, 3, 8, np.int32),      # neither: one group per workgroup either way
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[f"Mb{c[0]}_Kb{c[1]}_w{c[2]}_N{c[4]}_{np.dtype(c[5]).name}"
+                                                   for c in SPLIT_CASES])
+def test_band_f32_balanced_launch(torch, case, monkeypatch):
+    """The fp32 band kernel's balanced launch (a plan kernel, equal shares of
+    the groups' blocks per workgroup, a group cut by a share border summed
+    from its parts' partial tiles in part order) at full size: small-integer
+    A and B keep every sum exact, so C equals the fp64 product on sampled
+    block-rows and equals the one-group-per-workgroup launch
+    (XSPMM_BAND_SPLIT=off) bit for bit; repeated calls give the same C."""
+    Mb, Kb, wb, cut, N, itype = case
+    M, K = 16 * Mb - cut, 16 * Kb
+    brp_h, bci_h = block_band(Mb, Kb, wb)
+    note(f"fp32 balanced band: Mb {Mb} Kb {Kb} half-width {wb} M {M} N {N} {np.dtype(itype).name}, "
+         f"nnzb {len(bci_h)}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(Mb + N)
+    brp = torch.as_tensor(brp_h.astype(itype)).cuda()
+    bci = torch.as_tensor(bci_h.astype(itype)).cuda()
+    vals = torch.randint(-2, 3, (len(bci_h), 16, 16), generator=g, device="cuda").to(torch.float32)
+    # rows of the last block-row past M are padding: zero, as a conversion leaves them
+    if cut:
+        vals[int(brp_h[Mb - 1]):, 16 - cut:, :] = 0
+    B = torch.randint(-3, 4, (K, N), generator=g, device="cuda").to(torch.float32)
+    monkeypatch.delenv("XSPMM_BAND_SPLIT", raising=False)
+    C = spmm_band_arrays(torch, M, K, Mb, Kb, brp, bci, vals, B)
+    assert torch.equal(C, spmm_band_arrays(torch, M, K, Mb, Kb, brp, bci, vals, B))
+    monkeypatch.setenv("XSPMM_BAND_SPLIT", "off")
+    C_off = spmm_band_arrays(torch, M, K, Mb, Kb, brp, bci, vals, B)
+    monkeypatch.delenv("XSPMM_BAND_SPLIT")
+    assert torch.equal(C, C_off)
+    Bh = B.cpu().numpy().astype(np.float64)
+    Ch = C.cpu().numpy()
+    for b in sorted({0, 1, Mb // 3, Mb // 2, Mb - 2, Mb - 1}):
+        blocks = vals[int(brp_h[b]):int(brp_h[b + 1])].cpu().numpy().astype(np.float64)
+        ref = np.zeros((16, N))
+        for blk, c in zip(blocks, bci_h[brp_h[b]:brp_h[b + 1]]):
+            ref += blk @ Bh[16 * c:16 * c + 16]
+        rows = min(16, M - 16 * b)
+        assert np.array_equal(Ch[16 * b:16 * b + rows], ref[:rows].astype(np.float32)), b

@@ -320,13 +320,16 @@ bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t n
 bool spmm_band_f16_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N);
 // Tier-1 fp32 SpMM for banded grids (contiguous block-rows): four
 // neighbouring block-rows per workgroup share each B load in registers.
-// False (nothing launched) when the shape is not covered (N % 4 != 0, B or C
-// not 16-byte aligned, K * N * 4 > 2^31).
+// Wide bands (nnzb >= 128 Mb) of at most 4096 groups run the balanced launch
+// (a plan kernel, then equal shares of the groups' blocks per workgroup, cut
+// groups summed in part order; stream-ordered scratch).  False (nothing
+// launched) when the shape is not covered (N % 4 != 0, B or C not 16-byte
+// aligned, K * N * 4 > 2^31).
 bool spmm_band_f32_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N, const void* B, const void* C);
 template <typename I>
 bool bcsr_spmm_band_f32(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
                         const float* bvals, const float* B, float* C, int64_t N, const I* row_map,
-                        hipStream_t s);
+                        int64_t nnzb, hipStream_t s);
 // Whether Tier-1 should take a band kernel for this grid of fp16
 // (value_bytes 2) or fp32 (4) blocks: every block-row contiguous, the grid not
 // full, the groups' spans gathering fewer B rows than the column-batch kernel

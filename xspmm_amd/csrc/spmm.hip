@@ -1959,7 +1959,7 @@ void bcsr_spmm_band(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t nnzb, 
     if constexpr (sizeof(T) == 2) {
         if (bcsr_spmm_band_f16<I>(M, K, Mb, Kb, brp, bci, bvals, B, C, N, nullptr, s)) return;
     } else {
-        if (bcsr_spmm_band_f32<I>(M, K, Mb, Kb, brp, bci, bvals, B, C, N, nullptr, s)) return;
+        if (bcsr_spmm_band_f32<I>(M, K, Mb, Kb, brp, bci, bvals, B, C, N, nullptr, nnzb, s)) return;
     }
     (void)bcsr_spmm_ex<T, I>(M, K, Mb, Kb, nnzb, brp, bci, bvals, B, C, N, nullptr, nullptr, s);
 }

@@ -40,9 +40,11 @@
 // B rows >= K contribute nothing.  A row's pairs accumulate in ascending
 // column order, the same order on every call.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
+#include <string>
 
 #include "internal.hpp"
 
@@ -60,6 +62,9 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 constexpr int kBandRows = 4;        // block-rows per workgroup (a group)
 constexpr int kBandTile = 32 * 256; // LDS stage: 32 B rows x 128 fp16 columns
 constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every resource: reads zeros
+// cache policy of a buffer access that is coherent across the XCDs (sc1: the
+// policy of relaxed agent-scope atomic loads and stores)
+constexpr int kAgentCoherent = 16;
 
 #ifndef XSPMM_BAND_DEPTH
 #define XSPMM_BAND_DEPTH 6
@@ -310,6 +315,156 @@ __global__ __launch_bounds__(64 * kBandRows * WPR) void spmm_f16_band_kernel(
     }
 }
 
+// The balanced launch of the fp32 band kernel: the groups' block counts,
+// laid end to end (S[g] = blocks of the spans of groups 0 .. g - 1, S[G] =
+// all), are cut into P ranges of about equal size, one per workgroup slot
+// and column chunk, so every CU gets the same number of MFMAs however the
+// band's width varies along the diagonal.  A border that falls close to a
+// group border moves onto it (a band of even width cuts no group).  A slot
+// walks the groups its range meets: a group it holds whole is stored into
+// C; a group cut by a border is summed from its parts: each part writes its
+// partial tile, then counts itself in `arrivals`, and the part that arrives
+// last adds the partial tiles in part order (part 0 + part 1 + ...) and
+// stores C, so C is the same bit for bit whichever part arrives last.
+struct BandSplit {
+    const int64_t* S;      // G + 1: prefix of the groups' block counts
+    const int64_t* bnd;    // P + 1: slot p's range is [bnd[p], bnd[p + 1])
+    const int32_t* first;  // P: the first group slot p's range meets
+    const int32_t* plo;    // G: the first slot meeting group g
+    const int32_t* parts;  // G: the slots meeting group g (1: one holds it whole)
+    int32_t* arrivals;     // chunks x P: parts counted of the cut group that slot starts
+    float* tiles;          // chunks x 2 x P partial tiles of kBandPart32 floats
+    int64_t G;             // groups
+    int32_t P;             // slots, a multiple of 8
+};
+constexpr int kBandPart32 = 4 * 16 * 64;  // a group's 64 x 64 fp32 tile
+constexpr int kPlanGroups = 4096;         // most groups a balanced launch plans
+constexpr int kPlanSlots = 1024;          // most slots
+
+// Blocks in the union of group grp's block-rows' spans (rows are contiguous
+// runs, so a row spans col_ind[first] .. col_ind[last]); 0 when it holds none.
+// The five row pointers load together, then the eight column indices (from
+// indices clamped into [0, nnzb), so a grid with blocks reads nothing past
+// col_ind).
+template <typename I>
+__device__ __forceinline__ int64_t band_group_blocks(const I* brp, const I* bci, int64_t Mb, int64_t nnzb,
+                                                     int64_t grp)
+{
+    int64_t rp[5];
+#pragma unroll
+    for (int w = 0; w < 5; ++w) rp[w] = (int64_t)brp[min(grp * 4 + w, Mb)];
+    int64_t f[4], l[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        f[w] = (int64_t)bci[min(max(rp[w], (int64_t)0), nnzb - 1)];
+        l[w] = (int64_t)bci[min(max(rp[w + 1] - 1, (int64_t)0), nnzb - 1)];
+    }
+    int64_t lo = INT64_MAX, hi = -1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        if (grp * 4 + w >= Mb || rp[w + 1] <= rp[w]) continue;
+        lo = min(lo, f[w]);
+        hi = max(hi, l[w]);
+    }
+    return hi >= 0 ? hi - lo + 1 : 0;
+}
+
+// The balanced launch's plan, one workgroup, in LDS: the prefix S, the slot
+// borders, each slot's first group, each group's first slot and part count,
+// and the arrival counts cleared.
+template <typename I>
+__global__ __launch_bounds__(1024) void band_plan_kernel(const I* __restrict__ brp, const I* __restrict__ bci,
+                                                          int64_t Mb, int64_t nnzb, BandSplit sp, int32_t chunks)
+{
+    __shared__ int64_t s_S[kPlanGroups + 1];
+    __shared__ int64_t s_b[kPlanSlots + 1];
+    __shared__ int64_t red[16];
+    const int32_t G = (int32_t)sp.G;
+    const int32_t P = sp.P;
+    for (int32_t g = threadIdx.x; g < G; g += 1024) s_S[g + 1] = band_group_blocks(brp, bci, Mb, nnzb, g);
+    __syncthreads();
+    // prefix: thread i scans a run of consecutive groups from the sum of the
+    // runs before it
+    const int32_t per = (G + 1023) / 1024;
+    const int32_t a = min(G, (int32_t)threadIdx.x * per), b = min(G, a + per);
+    int64_t own = 0;
+    for (int32_t i = a; i < b; ++i) own += s_S[i + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int64_t incl = own;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    if (lane == 63) red[wave] = incl;
+    __syncthreads();
+    int64_t run = incl - own;
+    for (int w = 0; w < wave; ++w) run += red[w];
+    for (int32_t i = a; i < b; ++i) {
+        run += s_S[i + 1];
+        s_S[i + 1] = run;
+    }
+    if (threadIdx.x == 0) s_S[0] = 0;
+    __syncthreads();
+    const int64_t total = s_S[G];
+    // lower bound: the first g in [0, G] with s_S[g] >= x
+    auto lower = [&](int64_t x) {
+        int32_t lo = 0, hi = G;
+        while (lo < hi) {
+            const int32_t m = (lo + hi) >> 1;
+            if (s_S[m] >= x) hi = m; else lo = m + 1;
+        }
+        return lo;
+    };
+    // slot borders: ceil(p total / P), moved onto a group border within
+    // total / (16 P) of it
+    const int64_t tol = total / (16 * (int64_t)P);
+    for (int32_t p = threadIdx.x; p <= P; p += 1024) {
+        int64_t x = ((int64_t)p * total + P - 1) / P;
+        if (p > 0 && p < P) {
+            const int32_t j = lower(x);
+            int64_t best = s_S[j];  // j <= G and s_S[G] = total >= x
+            if (j > 0 && x - s_S[j - 1] < best - x) best = s_S[j - 1];
+            if (best - x <= tol && x - best <= tol) x = best;
+        }
+        s_b[p] = x;
+        const_cast<int64_t*>(sp.bnd)[p] = x;
+    }
+    __syncthreads();
+    // slot p's first group: the first one holding a unit from bnd[p] on, or
+    // an empty group there
+    for (int32_t p = threadIdx.x; p < P; p += 1024) {
+        const int64_t beg = s_b[p];
+        int32_t lo = 0, hi = G;  // first g with S[g + 1] > beg
+        while (lo < hi) {
+            const int32_t m = (lo + hi) >> 1;
+            if (s_S[m + 1] > beg) hi = m; else lo = m + 1;
+        }
+        const_cast<int32_t*>(sp.first)[p] = min(lower(beg), lo);
+    }
+    // the slot holding unit x: the last p with bnd[p] <= x (x < total)
+    auto holder = [&](int64_t x) {
+        int32_t lo = 0, hi = P;  // first p in [0, P] with bnd[p] > x
+        while (lo < hi) {
+            const int32_t m = (lo + hi) >> 1;
+            if (s_b[m] > x) hi = m; else lo = m + 1;
+        }
+        return lo - 1;
+    };
+    for (int32_t g = threadIdx.x; g < G; g += 1024) {
+        const int64_t s0 = s_S[g], s1 = s_S[g + 1];
+        int32_t plo = 0, parts = 1;
+        if (s1 > s0) {
+            plo = holder(s0);
+            parts = holder(s1 - 1) - plo + 1;
+        }
+        const_cast<int32_t*>(sp.plo)[g] = plo;
+        const_cast<int32_t*>(sp.parts)[g] = parts;
+    }
+    for (int32_t i = threadIdx.x; i <= G; i += 1024) const_cast<int64_t*>(sp.S)[i] = s_S[i];
+    for (int64_t i = threadIdx.x; i < (int64_t)P * chunks; i += 1024) sp.arrivals[i] = 0;
+}
+
 // ---------------------------------------------------------------------------
 // fp32 banded grids: spmm_f32_band_kernel.  v_mfma_f32_16x16x4f32 takes one K
 // index per lane group (lane (i, k) holds A[i][k] and B[k][i]), so B rows go
@@ -334,74 +489,26 @@ __global__ __launch_bounds__(64 * kBandRows * WPR) void spmm_f16_band_kernel(
 // Output tile j of a wave holds columns n0 + 4n + j (lane (n, g): rows
 // 4g .. 4g + 3), as in the fp32 column-batch kernel.  Each block-row must be
 // one contiguous run of block columns (spmm_band_wanted); N % 4 == 0, B and C
-// 16-byte aligned.
-template <typename I, int L>
+// 16-byte aligned.  SPLIT: the balanced launch (grid P x chunks, with the plan
+// of band_plan_kernel); otherwise one group per workgroup.
+template <typename I, int L, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void spmm_f32_band_kernel(
     const I* __restrict__ brp, const I* __restrict__ bci, const float* __restrict__ vals,
     const float* __restrict__ B, float* __restrict__ C, int64_t M, int64_t K, int64_t N, int64_t Mb,
-    const I* __restrict__ row_map)
+    const I* __restrict__ row_map, BandSplit sp)
 {
     typedef float float4v_t __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) float red[4 * 4 * 16 * 64];  // [wave][row][16][64]
     __shared__ int32_t s_first[4];
     __shared__ int32_t s_last[4];
+    __shared__ int32_t s_arrived;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 15;
     const int g = lane >> 4;
-    const uint32_t G = gridDim.x;
-    const uint32_t x8 = blockIdx.x & 7u;
-    const uint32_t grp = kBandXcd ? x8 * (G >> 3) + min(x8, G & 7u) + (blockIdx.x >> 3) : blockIdx.x;
-    const int64_t br0 = (int64_t)grp * 4;
     const int64_t n0 = (int64_t)blockIdx.y * 64;
-
-    {
-        const int64_t br = br0 + wave;
-        int32_t first = 0x7fffffff, last = -1;
-        if (br < Mb) {
-            const int64_t rs = (int64_t)brp[br], re = (int64_t)brp[br + 1];
-            if (re > rs) {
-                first = (int32_t)bci[rs];
-                last = (int32_t)bci[re - 1];
-            }
-        }
-        if (lane == 0) {
-            s_first[wave] = first;
-            s_last[wave] = last;
-        }
-    }
-    __syncthreads();
-    int32_t lo = 0x7fffffff, hi = -1;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        lo = min(lo, s_first[w]);
-        hi = max(hi, s_last[w]);
-    }
-    const int32_t span = hi >= 0 ? hi - lo + 1 : 0;
-    const int32_t nt = span > wave ? (span - wave + 3) >> 2 : 0;  // this wave's blocks
-    const int32_t c0 = lo + wave;                                 // its first block column
-
-    // rows: block c of row r at index c - first_r, present when in [0, n_r)
-    __amdgpu_buffer_rsrc_t a_rsrc[4];
-    int32_t r_rel0[4], r_n[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t br = br0 + r;
-        int64_t rs = 0, re = 0;
-        if (br < Mb) {
-            rs = (int64_t)brp[br];
-            re = (int64_t)brp[br + 1];
-        }
-        r_n[r] = (int32_t)(re - rs);
-        a_rsrc[r] = band_rsrc(vals + rs * 256, (uint32_t)r_n[r] * 1024u);
-        r_rel0[r] = c0 - s_first[r];
-    }
     const uint32_t a_lane = (uint32_t)(li * 64 + g * 16);
-    auto a_off = [&](int r, int32_t t) __attribute__((always_inline)) -> uint32_t {
-        const int32_t rel = r_rel0[r] + 4 * t;
-        return (uint32_t)rel < (uint32_t)r_n[r] ? (uint32_t)rel * 1024u + a_lane : kOob;
-    };
     // B: lane (n, g) of load s reads row 16c + 4g + s, columns n0 + 4n .. +3
     // (a quad past N reads the row's last quad: it only meets unstored
     // columns); rows past K read zeros
@@ -409,78 +516,198 @@ __global__ __launch_bounds__(256, 2) void spmm_f32_band_kernel(
     const uint32_t rowbytes = (uint32_t)(4 * N);
     const int64_t colq = n0 + 4 * li;
     const uint32_t b_lane = (uint32_t)(4 * (colq < N ? colq : N - 4)) + __umul24((uint32_t)(4 * g), rowbytes);
-    auto b_off = [&](int32_t t, int sidx) __attribute__((always_inline)) -> uint32_t {
-        const int32_t c = c0 + 4 * t;
-        return t < nt ? __umul24((uint32_t)(16 * c + sidx), rowbytes) + b_lane : kOob;
-    };
 
-    float4v_t acc[4][4];
+    // Blocks t0 .. t1 - 1 of group grp's span (clamped to the span), summed
+    // over the waves into red (wave order), which the workgroup reads after
+    // the closing barrier.
+    auto group_blocks = [&](int64_t grp, int32_t t0, int32_t t1) __attribute__((always_inline)) {
+        const int64_t br0 = grp * 4;
+        __syncthreads();  // the previous group's readers of s_first, s_last and red are done
+        {
+            const int64_t br = br0 + wave;
+            int32_t first = 0x7fffffff, last = -1;
+            if (br < Mb) {
+                const int64_t rs = (int64_t)brp[br], re = (int64_t)brp[br + 1];
+                if (re > rs) {
+                    first = (int32_t)bci[rs];
+                    last = (int32_t)bci[re - 1];
+                }
+            }
+            if (lane == 0) {
+                s_first[wave] = first;
+                s_last[wave] = last;
+            }
+        }
+        __syncthreads();
+        int32_t lo = 0x7fffffff, hi = -1;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[r][j] = float4v_t{0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < 4; ++w) {
+            lo = min(lo, s_first[w]);
+            hi = max(hi, s_last[w]);
+        }
+        const int32_t span = hi >= 0 ? hi - lo + 1 : 0;
+        t1 = min(t1, span);
+        t0 = min(t0, t1);
+        const int32_t steps = t1 - t0;
+        const int32_t nt = steps > wave ? (steps - wave + 3) >> 2 : 0;  // this wave's blocks
+        const int32_t c0 = lo + t0 + wave;                               // its first block column
 
-    float4v_t ar[L][4];  // A of the wave's block t, four rows (slot t % L)
-    float4v_t bq[L][4];  // its four B loads
-    auto issue = [&](int slot, int32_t t) __attribute__((always_inline)) {
-#pragma unroll
-        for (int sidx = 0; sidx < 4; ++sidx)
-            bq[slot][sidx] = __builtin_bit_cast(
-                float4v_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)b_off(t, sidx), 0, 0));
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            ar[slot][r] = __builtin_bit_cast(
-                float4v_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc[r], (int)a_off(r, t), 0, 0));
-    };
-    auto multiply = [&](int slot, int32_t t) __attribute__((always_inline)) {
+        // rows: block c of row r at index c - first_r, present when in [0, n_r)
+        __amdgpu_buffer_rsrc_t a_rsrc[4];
+        int32_t r_rel0[4], r_n[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            // uniform: does row r hold this block?
-            if ((uint32_t)(r_rel0[r] + 4 * t) < (uint32_t)r_n[r]) {
+            const int64_t br = br0 + r;
+            int64_t rs = 0, re = 0;
+            if (br < Mb) {
+                rs = (int64_t)brp[br];
+                re = (int64_t)brp[br + 1];
+            }
+            r_n[r] = (int32_t)(re - rs);
+            a_rsrc[r] = band_rsrc(vals + rs * 256, (uint32_t)r_n[r] * 1024u);
+            r_rel0[r] = c0 - s_first[r];
+        }
+        auto a_off = [&](int r, int32_t t) __attribute__((always_inline)) -> uint32_t {
+            const int32_t rel = r_rel0[r] + 4 * t;
+            return (uint32_t)rel < (uint32_t)r_n[r] ? (uint32_t)rel * 1024u + a_lane : kOob;
+        };
+        auto b_off = [&](int32_t t, int sidx) __attribute__((always_inline)) -> uint32_t {
+            const int32_t c = c0 + 4 * t;
+            return t < nt ? __umul24((uint32_t)(16 * c + sidx), rowbytes) + b_lane : kOob;
+        };
+
+        float4v_t acc[4][4];
 #pragma unroll
-                for (int sidx = 0; sidx < 4; ++sidx)
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[slot][r][sidx], bq[slot][sidx][j],
-                                                                         acc[r][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[r][j] = float4v_t{0.f, 0.f, 0.f, 0.f};
+
+        float4v_t ar[L][4];  // A of the wave's block t, four rows (slot t % L)
+        float4v_t bq[L][4];  // its four B loads
+        auto issue = [&](int slot, int32_t t) __attribute__((always_inline)) {
+#pragma unroll
+            for (int sidx = 0; sidx < 4; ++sidx)
+                bq[slot][sidx] = __builtin_bit_cast(
+                    float4v_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, (int)b_off(t, sidx), 0, 0));
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                ar[slot][r] = __builtin_bit_cast(
+                    float4v_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc[r], (int)a_off(r, t), 0, 0));
+        };
+        auto multiply = [&](int slot, int32_t t) __attribute__((always_inline)) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // uniform: does row r hold this block?
+                if ((uint32_t)(r_rel0[r] + 4 * t) < (uint32_t)r_n[r]) {
+#pragma unroll
+                    for (int sidx = 0; sidx < 4; ++sidx)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ar[slot][r][sidx], bq[slot][sidx][j],
+                                                                             acc[r][j], 0, 0, 0);
+                }
+            }
+        };
+
+        if (nt > 0) {
+#pragma unroll
+            for (int t = 0; t < L; ++t) issue(t, t);
+            for (int32_t q0 = 0; q0 < nt; q0 += L) {
+#pragma unroll
+                for (int u = 0; u < L; ++u) {
+                    const int32_t t = q0 + u;
+                    if (t < nt) multiply(u, t);
+                    issue(u, t + L);
+                }
             }
         }
+
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<float4v_t*>(red + ((wave * 4 + r) * 16 + 4 * g + q) * 64 + 4 * li) =
+                    float4v_t{acc[r][0][q], acc[r][1][q], acc[r][2][q], acc[r][3][q]};
+        __syncthreads();
     };
-
-    if (nt > 0) {
-#pragma unroll
-        for (int t = 0; t < L; ++t) issue(t, t);
-        for (int32_t t0 = 0; t0 < nt; t0 += L) {
-#pragma unroll
-            for (int u = 0; u < L; ++u) {
-                const int32_t t = t0 + u;
-                if (t < nt) multiply(u, t);
-                issue(u, t + L);
-            }
-        }
-    }
-
-    // sum the waves' partial tiles in wave order and store C
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<float4v_t*>(red + ((wave * 4 + r) * 16 + 4 * g + q) * 64 + 4 * li) =
-                float4v_t{acc[r][0][q], acc[r][1][q], acc[r][2][q], acc[r][3][q]};
-    __syncthreads();
-    for (int e = threadIdx.x; e < 4 * 16 * 16; e += 256) {
-        const int r = e >> 8;              // block-row of the group
-        const int row = (e >> 4) & 15;     // row in the block-row
-        const int c4 = 4 * (e & 15);       // column quad
-        const int64_t grow = (br0 + r) * 16 + row;
-        const int64_t col = n0 + c4;
-        if (br0 + r >= Mb || grow >= M || col >= N) continue;
-        const int o = (r * 16 + row) * 64 + c4;
+    // quad e of the group's tile: block-row e / 256, row (e / 16) % 16,
+    // columns 4 (e % 16) .. + 3; its sum over the waves, in wave order
+    auto tile_quad = [&](int e) __attribute__((always_inline)) -> float4v_t {
+        const int o = e * 4;
         float4v_t v = *reinterpret_cast<const float4v_t*>(red + o);
 #pragma unroll
         for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const float4v_t*>(red + w * 4 * 16 * 64 + o);
+        return v;
+    };
+    auto store_quad = [&](int64_t grp, int e, const float4v_t& v) __attribute__((always_inline)) {
+        const int64_t br = grp * 4 + (e >> 8);
+        const int64_t grow = br * 16 + ((e >> 4) & 15);
+        const int64_t col = n0 + 4 * (e & 15);
+        if (br >= Mb || grow >= M || col >= N) return;
         const int64_t crow = row_map ? (int64_t)row_map[grow] : grow;
         *reinterpret_cast<float4v_t*>(C + crow * N + col) = v;
+    };
+
+    if constexpr (!SPLIT) {
+        const uint32_t G = gridDim.x;
+        const uint32_t x8 = blockIdx.x & 7u;
+        const uint32_t grp = kBandXcd ? x8 * (G >> 3) + min(x8, G & 7u) + (blockIdx.x >> 3) : blockIdx.x;
+        group_blocks(grp, 0, 0x7fffffff);
+        for (int e = threadIdx.x; e < 4 * 16 * 16; e += 256) store_quad(grp, e, tile_quad(e));
+    } else {
+        // slot of this workgroup: XCD x holds slots x P / 8 .. (x + 1) P / 8 - 1,
+        // a contiguous stretch of groups
+        const int32_t P = sp.P;
+        const int32_t p = (int32_t)((blockIdx.x & 7u) * (uint32_t)(P >> 3) + (blockIdx.x >> 3));
+        const int64_t beg = sp.bnd[p], end = sp.bnd[p + 1];
+        // partial tiles of this column chunk, through agent-coherent accesses
+        // (the cache policy of relaxed agent-scope atomics: no part writes
+        // back or invalidates its XCD's whole L2): bank 1 holds a group's
+        // first part (the last group of the slot holding it), bank 0 a later
+        // part (the first group of its slot)
+        const __amdgpu_buffer_rsrc_t part_rsrc = band_rsrc(
+            sp.tiles + (int64_t)blockIdx.y * 2 * P * kBandPart32, (uint32_t)(2 * P * kBandPart32 * 4));
+        auto part_at = [&](int32_t q, bool head) __attribute__((always_inline)) -> int {
+            return (int)(((head ? P : 0) + q) * (uint32_t)(kBandPart32 * 4));
+        };
+        for (int64_t grp = sp.first[p]; grp < sp.G; ++grp) {
+            const int64_t s0 = sp.S[grp], s1 = sp.S[grp + 1];
+            // groups from `end` on are later slots' (the last slot also
+            // takes the empty groups at the very end)
+            if (s0 >= end && p != P - 1) break;
+            group_blocks(grp, (int32_t)(max(beg, s0) - s0), (int32_t)(min(end, s1) - s0));
+            const int32_t parts = sp.parts[grp];
+            if (parts == 1) {
+                for (int e = threadIdx.x; e < 4 * 16 * 16; e += 256) store_quad(grp, e, tile_quad(e));
+                continue;
+            }
+            const int32_t plo = sp.plo[grp];
+            const int32_t k = p - plo;
+            const int mine = part_at(p, k == 0);
+            for (int e = threadIdx.x; e < 4 * 16 * 16; e += 256)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, tile_quad(e)), part_rsrc,
+                                                       e * 16, mine, kAgentCoherent);
+            // the stores are complete before the part counts itself
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (threadIdx.x == 0)
+                s_arrived = __hip_atomic_fetch_add(sp.arrivals + (int64_t)blockIdx.y * P + plo, 1,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            if (s_arrived != parts - 1) continue;
+            // the last part: the group's tile is part 0 + part 1 + ... in
+            // this order
+            for (int e = threadIdx.x; e < 4 * 16 * 16; e += 256) {
+                float4v_t v = __builtin_bit_cast(
+                    float4v_t, __builtin_amdgcn_raw_buffer_load_b128(part_rsrc, e * 16, part_at(plo, true),
+                                                                     kAgentCoherent));
+                for (int32_t part = 1; part < parts; ++part)
+                    v += __builtin_bit_cast(float4v_t,
+                                            __builtin_amdgcn_raw_buffer_load_b128(
+                                                part_rsrc, e * 16, part_at(plo + part, false), kAgentCoherent));
+                store_quad(grp, e, v);
+            }
+        }
     }
 }
 
@@ -588,24 +815,90 @@ bool spmm_band_f32_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N, const vo
            (reinterpret_cast<uintptr_t>(C) & 15) == 0;
 }
 
+namespace {
+
+// CUs of the current device, asked once per device
+int band_device_cus()
+{
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    XSPMM_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        XSPMM_HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        if (n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// The diagnostic switch XSPMM_BAND_SPLIT=off keeps one group per workgroup
+bool band_split_enabled()
+{
+    const char* e = std::getenv("XSPMM_BAND_SPLIT");
+    return !(e && std::string(e) == "off");
+}
+
+}  // namespace
+
 template <typename I>
 bool bcsr_spmm_band_f32(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* brp, const I* bci,
                         const float* bvals, const float* B, float* C, int64_t N, const I* row_map,
-                        hipStream_t s)
+                        int64_t nnzb, hipStream_t s)
 {
     if (!spmm_band_f32_covers(K, Kb, Mb, N, B, C)) return false;
-    const dim3 grid((unsigned)((Mb + 3) / 4), (unsigned)((N + 63) / 64));
-    hipLaunchKernelGGL((spmm_f32_band_kernel<I, XSPMM_BAND_F32_DEPTH>), grid, dim3(256), 0, s, brp, bci, bvals,
-                       B, C, M, K, N, Mb, row_map);
+    const int64_t G = (Mb + 3) / 4;
+    const int64_t chunks = (N + 63) / 64;
+    const int64_t P = std::min<int64_t>(kPlanSlots, ((int64_t)band_device_cus() + 7) / 8 * 8);
+    const size_t tile_bytes = (size_t)chunks * 2 * (size_t)P * kBandPart32 * sizeof(float);
+    // The balanced launch (on grids of at most kPlanGroups groups) where one
+    // group per workgroup leaves CUs idle: fewer than 3/4 of a group per slot,
+    // or bands of at least 512 blocks per block-row, whose edge groups' spans
+    // run to half the centre's (narrower bands lose the plan's 10 us).
+    const bool idle_cus = 4 * G < 3 * P;
+    if (band_split_enabled() && (idle_cus || nnzb >= 512 * Mb) && G <= kPlanGroups &&
+        tile_bytes <= (size_t(512) << 20)) {
+        Carve cv;
+        const size_t o_S = cv.take((size_t)(G + 1) * sizeof(int64_t));
+        const size_t o_bnd = cv.take((size_t)(P + 1) * sizeof(int64_t));
+        const size_t o_first = cv.take((size_t)P * sizeof(int32_t));
+        const size_t o_plo = cv.take((size_t)G * sizeof(int32_t));
+        const size_t o_parts = cv.take((size_t)G * sizeof(int32_t));
+        const size_t o_arr = cv.take((size_t)(P * chunks) * sizeof(int32_t));
+        const size_t o_tiles = cv.take(tile_bytes);
+        Scratch mem(cv.end, s);
+        char* base = static_cast<char*>(mem.get());
+        BandSplit sp;
+        sp.S = reinterpret_cast<const int64_t*>(base + o_S);
+        sp.bnd = reinterpret_cast<const int64_t*>(base + o_bnd);
+        sp.first = reinterpret_cast<const int32_t*>(base + o_first);
+        sp.plo = reinterpret_cast<const int32_t*>(base + o_plo);
+        sp.parts = reinterpret_cast<const int32_t*>(base + o_parts);
+        sp.arrivals = reinterpret_cast<int32_t*>(base + o_arr);
+        sp.tiles = reinterpret_cast<float*>(base + o_tiles);
+        sp.G = G;
+        sp.P = (int32_t)P;
+        hipLaunchKernelGGL((band_plan_kernel<I>), dim3(1), dim3(1024), 0, s, brp, bci, Mb, nnzb, sp,
+                           (int32_t)chunks);
+        XSPMM_LAUNCH_CHECK();
+        hipLaunchKernelGGL((spmm_f32_band_kernel<I, XSPMM_BAND_F32_DEPTH, true>), dim3((unsigned)P, (unsigned)chunks),
+                           dim3(256), 0, s, brp, bci, bvals, B, C, M, K, N, Mb, row_map, sp);
+        XSPMM_LAUNCH_CHECK();
+        return true;
+    }
+    const dim3 grid((unsigned)G, (unsigned)chunks);
+    hipLaunchKernelGGL((spmm_f32_band_kernel<I, XSPMM_BAND_F32_DEPTH, false>), grid, dim3(256), 0, s, brp, bci,
+                       bvals, B, C, M, K, N, Mb, row_map, BandSplit{});
     XSPMM_LAUNCH_CHECK();
     return true;
 }
 template bool bcsr_spmm_band_f32<int32_t>(int64_t, int64_t, int64_t, int64_t, const int32_t*,
                                           const int32_t*, const float*, const float*, float*, int64_t,
-                                          const int32_t*, hipStream_t);
+                                          const int32_t*, int64_t, hipStream_t);
 template bool bcsr_spmm_band_f32<int64_t>(int64_t, int64_t, int64_t, int64_t, const int64_t*,
                                           const int64_t*, const float*, const float*, float*, int64_t,
-                                          const int64_t*, hipStream_t);
+                                          const int64_t*, int64_t, hipStream_t);
 
 template bool bcsr_spmm_band_f16<int32_t>(int64_t, int64_t, int64_t, int64_t, const int32_t*,
                                           const int32_t*, const uint16_t*, const uint16_t*, float*,
