@@ -309,3 +309,17 @@ def test_band_f32_balanced_launch(torch, case, monkeypatch):
             ref += blk @ Bh[16 * c:16 * c + 16]
         rows = min(16, M - 16 * b)
         assert np.array_equal(Ch[16 * b:16 * b + rows], ref[:rows].astype(np.float32)), b
+
+
+def test_band_f32_empty_grid(torch):
+    """A grid of block-rows without blocks (nnzb = 0) through the band entry:
+    few enough groups for the balanced launch, which an empty grid does not
+    take (its plan would have no column index to read); C is all zeros."""
+    Mb, Kb, N = 40, 30, 64
+    brp = torch.zeros(Mb + 1, dtype=torch.int32, device="cuda")
+    bci = torch.zeros(0, dtype=torch.int32, device="cuda")
+    vals = torch.zeros(0, dtype=torch.float32, device="cuda")
+    B = torch.ones((16 * Kb, N), dtype=torch.float32, device="cuda")
+    note("fp32 band entry, empty grid")
+    C = spmm_band_arrays(torch, 16 * Mb, 16 * Kb, Mb, Kb, brp, bci, vals, B)
+    assert torch.count_nonzero(C).item() == 0

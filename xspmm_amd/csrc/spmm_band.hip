@@ -344,8 +344,8 @@ constexpr int kPlanSlots = 1024;          // most slots
 // Blocks in the union of group grp's block-rows' spans (rows are contiguous
 // runs, so a row spans col_ind[first] .. col_ind[last]); 0 when it holds none.
 // The five row pointers load together, then the eight column indices (from
-// indices clamped into [0, nnzb), so a grid with blocks reads nothing past
-// col_ind).
+// indices clamped into [0, nnzb): the balanced launch is taken only for grids
+// with blocks, nnzb >= 1, so nothing is read past col_ind).
 template <typename I>
 __device__ __forceinline__ int64_t band_group_blocks(const I* brp, const I* bci, int64_t Mb, int64_t nnzb,
                                                      int64_t grp)
@@ -857,7 +857,7 @@ bool bcsr_spmm_band_f32(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
     // or bands of at least 512 blocks per block-row, whose edge groups' spans
     // run to half the centre's (narrower bands lose the plan's 10 us).
     const bool idle_cus = 4 * G < 3 * P;
-    if (band_split_enabled() && (idle_cus || nnzb >= 512 * Mb) && G <= kPlanGroups &&
+    if (band_split_enabled() && nnzb > 0 && (idle_cus || nnzb >= 512 * Mb) && G <= kPlanGroups &&
         tile_bytes <= (size_t(512) << 20)) {
         Carve cv;
         const size_t o_S = cv.take((size_t)(G + 1) * sizeof(int64_t));
