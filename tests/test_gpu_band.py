@@ -323,3 +323,34 @@ def test_band_f32_empty_grid(torch):
     note("fp32 band entry, empty grid")
     C = spmm_band_arrays(torch, 16 * Mb, 16 * Kb, Mb, Kb, brp, bci, vals, B)
     assert torch.count_nonzero(C).item() == 0
+
+
+def test_band_f32_balanced_random_shapes(torch, monkeypatch):
+    """24 seeded random band shapes through the fp32 band entry (ragged M, K
+    and N, shifted bands, runs of empty block-rows, both index types; every
+    one has fewer groups than 3/4 of the CUs, so the balanced launch takes
+    them): small-integer products equal the fp64 product exactly and the
+    one-group-per-workgroup launch bit for bit."""
+    rng = np.random.default_rng(2024)
+    for i in range(24):
+        M = int(rng.integers(17, 2600))
+        K = int(rng.integers(17, 2600))
+        bw = int(rng.integers(1, max(2, K // 2)))
+        shift = int(rng.integers(-K // 4, K // 4 + 1))
+        ee = int(rng.choice([0, 0, 2, 3, 5]))
+        N = 4 * int(rng.integers(1, 50))
+        itype = np.int32 if i % 2 == 0 else np.int64
+        note(f"random fp32 band {i}: M {M} K {K} bw {bw} shift {shift} empty every {ee} N {N} "
+             f"{np.dtype(itype).name}")
+        rp, ci, vals = band_csr(M, K, bw, shift, ee, rng, integer=True, dtype=np.float32)
+        Bm = device_bcsr(torch, M, K, rp, ci, vals, itype)
+        Bh = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
+        Bd = torch.as_tensor(Bh).cuda()
+        monkeypatch.delenv("XSPMM_BAND_SPLIT", raising=False)
+        C = spmm_band(torch, Bm, Bd)
+        monkeypatch.setenv("XSPMM_BAND_SPLIT", "off")
+        C_off = spmm_band(torch, Bm, Bd)
+        monkeypatch.delenv("XSPMM_BAND_SPLIT")
+        ref = oracle.csr_spmm_f64(M, N, rp, ci, vals, Bh)
+        assert np.array_equal(C.cpu().numpy(), ref.astype(np.float32)), i
+        assert torch.equal(C, C_off), i
