@@ -166,12 +166,14 @@ int xspmm_bcsr_band_rows(int vtype, int itype, int64_t M, int64_t K, int64_t Mb,
  * and C but C is wrong).  Shapes a band kernel does not cover (fp16: N % 8 !=
  * 0; fp32: N % 4 != 0 or B / C off a 16-byte boundary; K * N * value bytes >
  * 2^31) run the column-batch kernel instead.  fp32 grids of at most 4096
- * groups of four block-rows take a balanced launch when one group per
- * workgroup would leave CUs idle (fewer groups than 3/4 of the CUs, or at
- * least 512 blocks per block-row): a plan kernel gives every workgroup an
- * equal share of the groups' blocks, and a group cut between shares is summed
- * from its parts in a fixed order (stream-ordered scratch, C the same on every
- * call; XSPMM_BAND_SPLIT=off keeps one group per workgroup).  Every block a
+ * groups of four block-rows take a balanced launch where one group per
+ * workgroup is predicted to leave CUs idle long enough to pay for its fixed
+ * cost (about 25 us; wide bands, and grids of fewer workgroups than the CUs
+ * hold): a plan kernel gives every workgroup an equal share of the groups'
+ * blocks, and a group cut between shares is summed from its parts in a fixed
+ * order (stream-ordered scratch, C the same on every call;
+ * XSPMM_BAND_SPLIT=off keeps one group per workgroup, =force takes the
+ * balanced launch wherever it can run).  Every block a
  * row holds multiplies all 16 of its columns, so an Inf/NaN in B gives NaN in
  * the rows the reference's does.  Asynchronous on `stream`.
  * Replaces, for banded grids, the same call as xspmm_bcsr_spmm

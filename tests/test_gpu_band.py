@@ -263,10 +263,10 @@ def spmm_band_arrays(torch, M, K, Mb, Kb, brp, bci, vals, B):
 
 # (block-rows, block columns, half-width in blocks, ragged rows cut from M, N, index type)
 SPLIT_CASES = [
-    (1024, 1024, 460, 0, 128, np.int32),   # the examples/05 90 % band, 16384^2: >= 512 blocks per block-row
+    (1024, 1024, 460, 0, 128, np.int32),   # the examples/05 90 % band, 16384^2
     (1024, 1024, 460, 0, 64, np.int64),
-    (256, 300, 120, 7, 132, np.int32),     # 64 groups: fewer than the CUs; ragged M, three chunks
-    (1027, 1100, 60, 3, 8, np.int32),      # neither: one group per workgroup either way
+    (256, 300, 120, 7, 132, np.int32),     # 64 groups on 256 CUs; ragged M, three chunks
+    (1027, 1100, 60, 3, 8, np.int32),      # too little work: one group per workgroup either way
 ]
 
 
@@ -327,9 +327,10 @@ def test_band_f32_empty_grid(torch):
 
 def test_band_f32_balanced_random_shapes(torch, monkeypatch):
     """24 seeded random band shapes through the fp32 band entry (ragged M, K
-    and N, shifted bands, runs of empty block-rows, both index types; every
-    one has fewer groups than 3/4 of the CUs, so the balanced launch takes
-    them): small-integer products equal the fp64 product exactly and the
+    and N, shifted bands, runs of empty block-rows, both index types), with
+    the balanced launch forced (XSPMM_BAND_SPLIT=force; the launcher's rule
+    leaves most of these small grids to one group per workgroup):
+    small-integer products equal the fp64 product exactly and the
     one-group-per-workgroup launch bit for bit."""
     rng = np.random.default_rng(2024)
     for i in range(24):
@@ -346,7 +347,7 @@ def test_band_f32_balanced_random_shapes(torch, monkeypatch):
         Bm = device_bcsr(torch, M, K, rp, ci, vals, itype)
         Bh = rng.integers(-3, 4, size=(K, N)).astype(np.float32)
         Bd = torch.as_tensor(Bh).cuda()
-        monkeypatch.delenv("XSPMM_BAND_SPLIT", raising=False)
+        monkeypatch.setenv("XSPMM_BAND_SPLIT", "force")
         C = spmm_band(torch, Bm, Bd)
         monkeypatch.setenv("XSPMM_BAND_SPLIT", "off")
         C_off = spmm_band(torch, Bm, Bd)

@@ -320,9 +320,10 @@ bool bcsr_spmm_dense_f16(int64_t M, int64_t K, int64_t Mb, int64_t Kb, int64_t n
 bool spmm_band_f16_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N);
 // Tier-1 fp32 SpMM for banded grids (contiguous block-rows): four
 // neighbouring block-rows per workgroup share each B load in registers.
-// Wide bands (nnzb >= 128 Mb) of at most 4096 groups run the balanced launch
-// (a plan kernel, then equal shares of the groups' blocks per workgroup, cut
-// groups summed in part order; stream-ordered scratch).  False (nothing
+// Grids of at most 4096 groups where one group per workgroup is predicted to
+// leave CUs idle long enough run the balanced launch (a plan kernel, then
+// equal shares of the groups' blocks per workgroup, cut groups summed in part
+// order; stream-ordered scratch).  False (nothing
 // launched) when the shape is not covered (N % 4 != 0, B or C not 16-byte
 // aligned, K * N * 4 > 2^31).
 bool spmm_band_f32_covers(int64_t K, int64_t Kb, int64_t Mb, int64_t N, const void* B, const void* C);

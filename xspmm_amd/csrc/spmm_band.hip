@@ -833,11 +833,15 @@ int band_device_cus()
     return n;
 }
 
-// The diagnostic switch XSPMM_BAND_SPLIT=off keeps one group per workgroup
-bool band_split_enabled()
+// The diagnostic switch XSPMM_BAND_SPLIT: "off" keeps one group per
+// workgroup, "force" takes the balanced launch wherever it can run (for
+// tests); otherwise the launcher's rule decides.
+int band_split_mode()
 {
     const char* e = std::getenv("XSPMM_BAND_SPLIT");
-    return !(e && std::string(e) == "off");
+    if (e && std::string(e) == "off") return 0;
+    if (e && std::string(e) == "force") return 2;
+    return 1;
 }
 
 }  // namespace
@@ -852,13 +856,29 @@ bool bcsr_spmm_band_f32(int64_t M, int64_t K, int64_t Mb, int64_t Kb, const I* b
     const int64_t chunks = (N + 63) / 64;
     const int64_t P = std::min<int64_t>(kPlanSlots, ((int64_t)band_device_cus() + 7) / 8 * 8);
     const size_t tile_bytes = (size_t)chunks * 2 * (size_t)P * kBandPart32 * sizeof(float);
-    // The balanced launch (on grids of at most kPlanGroups groups) where one
-    // group per workgroup leaves CUs idle: fewer than 3/4 of a group per slot,
-    // or bands of at least 512 blocks per block-row, whose edge groups' spans
-    // run to half the centre's (narrower bands lose the plan's 10 us).
-    const bool idle_cus = 4 * G < 3 * P;
-    if (band_split_enabled() && nnzb > 0 && (idle_cus || nnzb >= 512 * Mb) && G <= kPlanGroups &&
-        tile_bytes <= (size_t(512) << 20)) {
+    // The balanced launch (on grids of at most kPlanGroups groups) where the
+    // one-group-per-workgroup launch is predicted to take 10 % longer:
+    //   balanced:  W + 25 us (plan kernel, schedule loads, hand-off), with
+    //              W = nnzb N / (850 per us and CU x CUs), the rate the
+    //              balanced launch keeps on the 16384^2 90 % band;
+    //   one group: W / (q s), q the share of the grid's workgroup rounds that
+    //              its G x chunks workgroups fill (two per CU), s = 1 - f^2 / 2
+    //              the average group's share of the widest span on a band of
+    //              fill f = nnzb / (Mb Kb) (0.76 at the 90 % band, 0.90 at 50 %).
+    // Measured rule: it picks the faster launch on every band of 4096^2 to
+    // 16384^2 and N of 64 to 256 timed both ways.
+    const int mode = band_split_mode();
+    bool pays = false;
+    if (mode == 1) {
+        const double cus = (double)band_device_cus();
+        const double W = (double)nnzb * (double)N / (850.0 * cus);
+        const double wgs = (double)G * (double)chunks, cap = 2.0 * cus;
+        const double q = wgs / (std::ceil(wgs / cap) * cap);
+        const double f = (double)nnzb / ((double)Mb * (double)Kb);
+        const double sp_share = 1.0 - f * f / 2.0;
+        pays = W / (q * sp_share) > 1.1 * (W + 25.0);
+    }
+    if (mode > 0 && nnzb > 0 && (mode == 2 || pays) && G <= kPlanGroups && tile_bytes <= (size_t(512) << 20)) {
         Carve cv;
         const size_t o_S = cv.take((size_t)(G + 1) * sizeof(int64_t));
         const size_t o_bnd = cv.take((size_t)(P + 1) * sizeof(int64_t));
