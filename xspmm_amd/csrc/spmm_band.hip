@@ -39,6 +39,15 @@
 // accumulators, C overwritten; rows >= M and columns >= N are not stored and
 // B rows >= K contribute nothing.  A row's pairs accumulate in ascending
 // column order, the same order on every call.
+//
+// The fp32 kernel (spmm_f32_band_kernel, below) shares each B load of a
+// group in registers instead (v_mfma_f32_16x16x4f32 takes B rows as they lie
+// in memory) and is bound by the matrix cores of each CU.  Where one group
+// per workgroup would leave CUs idle (the band's edge groups hold half the
+// centre's blocks; a small grid fills few workgroup slots), it runs a
+// balanced launch: band_plan_kernel cuts the groups' blocks into one equal
+// share per CU, and a group cut between shares is summed from its parts'
+// partial tiles in part order by the part that arrives last.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
